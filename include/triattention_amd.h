@@ -1,0 +1,94 @@
+/*
+ * C ABI of the MI355X (gfx950) TriAttention kernels.
+ *
+ * Every entry point replaces one op of the reference's pybind module
+ * (triattention/kernels/cuda/common_host.cuh:96-102), with tensors passed as
+ * device pointers plus explicit sizes and element strides, and with a leading
+ * batch dimension (batch = 1 is the reference's semantics exactly).  All
+ * buffers are allocated by the caller; no entry point allocates.  Work is
+ * enqueued asynchronously on `stream` (a hipStream_t; NULL = default stream).
+ *
+ * Return value: 0 on success, non-zero on a validation or launch error, with
+ * a message available from tri_last_error() (thread-local).
+ *
+ * Record formats per (sequence, KV head, 64-key tile) keep the reference's
+ * sizes: K8 8192 B, K4 4096 B, V16 16384 B, V8 8192 B, V4 4096 B, plus four
+ * fp32 group scales per K tile (decode.py:7-8, prefill_sm80.cu:17-22).
+ */
+#ifndef TRIATTENTION_AMD_H
+#define TRIATTENTION_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tri_last_error(void);
+
+/* Replaces prepare_qk (common_host.cuh:1-25).
+ * q: bf16 [batch][hq][t][128] with element strides (q_sb, q_sh, q_st), feature stride 1.
+ * k: bf16 [batch][hk][t][128] likewise.
+ * Outputs: q8 int8 [batch][hq][t][128], qa f32 [batch][hq][t], kp K8 records
+ * [batch][hk][tiles], ka f32 [batch][hk][tiles][4], partial f32 scratch
+ * [batch][hk][64][3][128], kstat f32 [batch][hk][3][128] (mean, scale, 1/scale).
+ * q4/qa4/k4p/ka4 are all NULL or all set: q4 u8 [batch][hq][t][64] (low nibble =
+ * even feature), qa4 f32 [batch][hq][t], k4p K4 records, ka4 f32 [batch][hk][tiles][4]. */
+int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
+                   int64_t k_sh, int64_t k_st, int batch, int hq, int hk, int t, void* q8, float* qa, void* kp,
+                   float* ka, float* partial, float* kstat, void* q4, float* qa4, void* k4p, float* ka4,
+                   void* stream);
+
+/* Replaces pack_v (common_host.cuh:27-45).
+ * v: bf16 [batch][hk][t][128]; vstat f32 [batch][hk][3][128].  Statistics are
+ * the identity (0, 1, 1) when both v8p and v4p are NULL (common_host.cuh:39).
+ * v16p/v8p/v4p: V16/V8/V4 records [batch][hk][tiles] or NULL. */
+int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batch, int hk, int t, float* partial,
+               float* vstat, void* v16p, void* v8p, void* v4p, void* stream);
+
+/* Replaces attention (prefill_sm80.cu:510-543), band-table form only (the
+ * reference's task-table form has no caller, prefill.py:103).
+ * order int32 [n_order = hq*tiles]: workgroup -> qhead*tiles + qtile.
+ * bands int32 [hq][2] = (w8, w4) per q-head, shared by every sequence.
+ * out: [batch][hq][t][128] with element strides (o_sb, o_sh, o_st), feature
+ * stride 1; out_dtype 0 = fp32, 1 = bf16, 2 = fp16.  scale is the softmax
+ * scale; sm_log2 = f32(scale * log2(e)) as in prefill_sm80.cu:538. */
+int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int batch, int hq, int hk, int t,
+                  const void* v16p, const void* v8p, const float* vstat, const void* q8, const void* k8p,
+                  const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
+                  const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                  double scale, void* stream);
+
+/* Replaces decode (common_host.cuh:47-87), batched and ragged.
+ * q bf16 [batch][hq][1][128] (strides q_sb, q_sh); k8c/k4c/v8c/v4c compacted
+ * records; ka/ka4 f32 [batch][hk][tiles_max][4]; entry/kinfo/slot int32
+ * [batch][hk][maxn] (kinfo = rowmask | is4 << 8 | kslot << 9); count int32
+ * [batch][hk]; fmt int32 [batch][tiles_max] (1 = INT8 V, 2 = INT4 V); prompt
+ * int32 [batch] lengths; vstat/kstat f32 [batch][hk][3][128]; ktail/vtail bf16
+ * [batch][hk][max_tail][128] (strides t_sb, t_sh, t_st); kcur/vcur bf16
+ * [batch][hk][1][128] (strides c_sb, c_sh); step int64 [1] on the device;
+ * out [batch][hq][1][128] (strides o_sb, o_sh), out_dtype 0 = fp32, 1 = bf16;
+ * pm/pl f32 [batch][hq][splits], po f32 [batch][hq][splits][128] with
+ * splits = max(1, ceil(maxn / per)). */
+int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
+               const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
+               const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
+               const float* kstat, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh, int64_t t_st,
+               int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh, const int64_t* step,
+               void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
+               const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max, double scale,
+               void* stream);
+
+/* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
+ * workgroups per compute unit, written to *blocks. */
+int tri_decode_occupancy(int* blocks);
+
+/* Compute units of the current device (used to size decode splits). */
+int tri_device_cus(int* cus);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRIATTENTION_AMD_H */

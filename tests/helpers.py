@@ -1,0 +1,82 @@
+"""Shared helpers of the parity tests: run the product path and the oracle on the same inputs."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle as O
+from triattention_amd.kernels import records as R
+from triattention_amd.kernels.decode import DecodeCache
+from triattention_amd.kernels.prefill import F16, I4, I8, Prefill
+from triattention_amd.maps import from_bands
+from triattention_amd.synthetic import bits
+
+# attention-output tolerance of the parity gate (fp32 outputs vs the oracle)
+MAX_ABS, MEAN_ABS = 2e-3, 1e-3
+
+
+def bands_fn_of(bands: torch.Tensor):
+    table = {"0": bands.tolist()}
+    return from_bands(table)
+
+
+def run_prefill(module, q, k, v, bands, scale, decode_cache=None, out_dtype=torch.float32):
+    """Prefill on the GPU through the host operator; returns (out cpu, operand views)."""
+    pre = Prefill(module, bands_fn_of(bands), decode_cache, out_dtype=out_dtype)
+    dev = torch.device("cuda")
+    out = pre(0, q.to(dev), k.to(dev), v.to(dev), scale)
+    torch.cuda.synchronize()
+    ops = next(iter(pre.views.values()))
+    return out.float().cpu(), ops, pre
+
+
+def u32(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def compare_codes(ops, codes, b, batch, hq, hk, t, kept=None):
+    """Assert bit equality of every GPU operand of sequence b with the oracle's."""
+    tiles = (t + 63) // 64
+    cpu = lambda x: x.detach().cpu().numpy()
+    np.testing.assert_array_equal(cpu(ops["q8"])[b], codes["q8"])
+    np.testing.assert_array_equal(u32(cpu(ops["qa"]).reshape(batch, hq * t)[b]), u32(codes["qa"]))
+    if codes["q4"] is not None:
+        np.testing.assert_array_equal(cpu(ops["q4"]).reshape(batch, hq, t, 64)[b], codes["q4"])
+        np.testing.assert_array_equal(u32(cpu(ops["qa4"]).reshape(batch, hq * t)[b]), u32(codes["qa4"]))
+    ka, kstat, vstat, ka4 = (ops["ka"], ops["kstat"], ops["vstat"], ops["ka4"]) if kept is None else kept
+    np.testing.assert_array_equal(u32(cpu(kstat).reshape(batch, hk, 3, 128)[b]), u32(codes["kstat"]))
+    np.testing.assert_array_equal(u32(cpu(vstat).reshape(batch, hk, 3, 128)[b]), u32(codes["vstat"]))
+    np.testing.assert_array_equal(u32(cpu(ka).reshape(batch, hk, tiles, 4)[b]), u32(codes["ka"]))
+    recs = cpu(ops["kp"]).reshape(batch, hk * tiles, 2048)[b]
+    np.testing.assert_array_equal(R.unpack_k8(recs).reshape(hk, tiles * 64, 128), codes["k8"])
+    if codes["k4"] is not None:
+        np.testing.assert_array_equal(u32(cpu(ka4).reshape(batch, hk, tiles, 4)[b]), u32(codes["ka4"]))
+        recs4 = cpu(ops["k4"]).reshape(batch, hk * tiles, 1024)[b]
+        np.testing.assert_array_equal(R.unpack_k4(recs4).reshape(hk, tiles * 64, 128), codes["k4"])
+    packed = ops["packed"]
+    v16 = cpu(packed[F16]).reshape(batch, hk * tiles, 4096)[b]
+    np.testing.assert_array_equal(R.unpack_v16(v16).reshape(hk, tiles * 64, 128), codes["v16"])
+    if codes["v8"] is not None:
+        v8 = cpu(packed[I8]).reshape(batch, hk * tiles, 2048)[b]
+        np.testing.assert_array_equal(R.unpack_v8(v8).reshape(hk, tiles * 64, 128), codes["v8"])
+    if codes["v4"] is not None:
+        v4 = cpu(packed[I4]).reshape(batch, hk * tiles, 1024)[b]
+        np.testing.assert_array_equal(R.unpack_v4(v4).reshape(hk, tiles * 64, 128), codes["v4"])
+
+
+def oracle_prefill(q, k, v, bands, scale, decode_cache=False):
+    """Per-sequence oracle outputs [B, Hq, T, 128] and codes."""
+    outs, codes = [], []
+    for b in range(q.shape[0]):
+        o, c = O.prefill(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), scale, decode_cache=decode_cache)
+        outs.append(o)
+        codes.append(c)
+    return np.stack(outs), codes
+
+
+def assert_close(gpu, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, what=""):
+    err = np.abs(np.asarray(gpu, np.float64) - np.asarray(ref, np.float64))
+    assert np.isfinite(np.asarray(gpu)).all(), f"{what}: non-finite output"
+    assert err.max() <= max_abs and err.mean() <= mean_abs, \
+        f"{what}: max abs {err.max():.3e} (<= {max_abs}), mean abs {err.mean():.3e} (<= {mean_abs})"
+    return float(err.max()), float(err.mean())

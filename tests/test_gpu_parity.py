@@ -1,0 +1,114 @@
+"""GPU parity: the gfx950 kernels through the C ABI against the CPU oracle.
+
+Bar: quantized codes, scales and statistics bit-exact; attention outputs (fp32)
+within 2e-3 max-abs and 1e-3 mean-abs of the oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_close, compare_codes, oracle_prefill, run_prefill
+from triattention_amd import synthetic as S
+from triattention_amd.kernels.decode import DecodeCache
+from triattention_amd.synthetic import INF, bits
+
+pytestmark = pytest.mark.gpu
+
+
+def small(seed, batch, hq, hk, t):
+    g = S.gen(seed)
+    return (S.outlier_tensor(g, batch, hq, t), S.outlier_tensor(g, batch, hk, t), S.outlier_tensor(g, batch, hk, t))
+
+
+MIXED = [[INF, INF], [INF, INF], [INF, INF], [1, INF], [1, INF], [1, INF]]
+
+
+@pytest.mark.parametrize("t", [1, 63, 64, 65, 200])
+def test_codes_and_output_small(module, t):
+    print(f"\n[parity] small prefill t={t}", flush=True)
+    q, k, v = small(2000 + t, 1, 6, 2, t)
+    bands = torch.tensor(MIXED, dtype=torch.int32)
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5)
+    ref, codes = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    compare_codes(ops, codes[0], 0, 1, 6, 2, t)
+    assert_close(out.numpy(), ref, what=f"prefill t={t}")
+
+
+def test_batch_and_band_variety(module):
+    print("\n[parity] batch=2 t=333 assorted bands", flush=True)
+    q, k, v = small(3000, 2, 8, 2, 333)
+    bands = torch.tensor([[INF, INF], [1, INF], [2, 4], [3, 3], [1, 2], [2, INF], [1, 1], [4, 5]], dtype=torch.int32)
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5)
+    ref, codes = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    for b in range(2):
+        compare_codes(ops, codes[b], b, 2, 8, 2, 333)
+    assert_close(out.numpy(), ref, what="prefill batch 2")
+
+
+def test_config0_prefill(module):
+    print("\n[parity] config 0 (B1 Hq24 Hk8 T1024, 50/50 INT8/INT4)", flush=True)
+    c = S.config0()
+    out, ops, _ = run_prefill(module, c["q"], c["k"], c["v"], c["bands"], c["scale"])
+    ref, codes = oracle_prefill(c["q"], c["k"], c["v"], c["bands"], c["scale"])
+    compare_codes(ops, codes[0], 0, 1, 24, 8, 1024)
+    mx, mn = assert_close(out.numpy(), ref, what="config 0")
+    print(f"config0 max abs {mx:.3e} mean abs {mn:.3e}")
+
+
+def test_bf16_output_within_one_ulp(module):
+    print("\n[parity] bf16 output rounding", flush=True)
+    q, k, v = small(4000, 1, 6, 2, 200)
+    bands = torch.tensor(MIXED, dtype=torch.int32)
+    out16, _, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5, out_dtype=torch.bfloat16)
+    ref, _ = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    r = torch.from_numpy(ref).to(torch.bfloat16).float()
+    ulp = torch.abs(r).clamp(min=1e-30).log2().floor().exp2() * 2.0 ** -7
+    assert bool((torch.abs(out16 - r) <= ulp + 1e-30).all())
+
+
+def _decode_case(module, prompt, bands, batch=1, steps=3, max_tail=8, seed=5000, hq=6, hk=2):
+    print(f"\n[parity] decode prompt={prompt} batch={batch} steps={steps}", flush=True)
+    q, k, v = small(seed, batch, hq, hk, prompt)
+    scale = 128 ** -0.5
+    cache = DecodeCache(module, max_tail=max_tail)
+    cache.out_dtype = torch.float32
+    _, ops, pre = run_prefill(module, q, k, v, bands, scale, decode_cache=cache)
+    ref_codes = [O.prefill_codes(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), decode_cache=True)
+                 for b in range(batch)]
+    kept = next(iter(pre.layer_buffers.values()))
+    for b in range(batch):
+        compare_codes(ops, ref_codes[b], b, batch, hq, hk, prompt, kept=kept)
+    per = cache.layers[0]["per"]
+    g = S.gen(seed + 1)
+    ktail = np.zeros((batch, hk, max_tail, 128), np.uint16)
+    vtail = np.zeros_like(ktail)
+    dev = torch.device("cuda")
+    for step in range(steps):
+        qd, kd, vd = S.outlier_tensor(g, batch, hq, 1), S.outlier_tensor(g, batch, hk, 1), S.outlier_tensor(g, batch, hk, 1)
+        out = cache(0, qd.to(dev), kd.to(dev), vd.to(dev), scale).float().cpu().numpy()
+        for b in range(batch):
+            ref = O.decode(ref_codes[b], bands.numpy(), bits(qd[b, :, 0]), prompt, per, scale, ktail[b], vtail[b],
+                           bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
+            assert_close(out[b, :, 0], ref, what=f"decode step {step} seq {b}")
+            prior = min(step, max_tail - 1)
+            ktail[b, :, prior] = bits(kd[b, :, 0])
+            vtail[b, :, prior] = bits(vd[b, :, 0])
+        cache.advance()
+
+
+def test_decode_mixed(module):
+    bands = torch.tensor(MIXED, dtype=torch.int32)
+    _decode_case(module, 300, bands)
+
+
+def test_decode_bands_and_tail_overflow(module):
+    bands = torch.tensor([[2, 4], [1, INF], [INF, INF], [3, 6], [1, 1], [2, 2]], dtype=torch.int32)
+    _decode_case(module, 1500, bands, batch=2, steps=5, max_tail=3, seed=5100)
+
+
+def test_decode_short_prompt(module):
+    bands = torch.tensor(MIXED, dtype=torch.int32)
+    _decode_case(module, 40, bands, steps=2, seed=5200)

@@ -1,0 +1,242 @@
+// extern "C" entry points: argument validation, launch geometry, error text.
+// One translation unit holds every kernel of the library.
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/triattention_amd.h"
+#include "decode.hip"
+#include "prefill.hip"
+#include "quantize.hip"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return 1;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("%s: launch failed: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* tri_last_error(void) { return g_error.c_str(); }
+
+int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
+                   int64_t k_sh, int64_t k_st, int batch, int hq, int hk, int t, void* q8, float* qa, void* kp,
+                   float* ka, float* partial, float* kstat, void* q4, float* qa4, void* k4p, float* ka4,
+                   void* stream) {
+  g_error.clear();
+  if (!q || !k || !q8 || !qa || !kp || !ka || !partial || !kstat) return fail("prepare_qk: null buffer");
+  if (batch < 1 || hq < 1 || hk < 1 || t < 1) return fail("prepare_qk: empty shape");
+  if (hq % hk != 0) return fail("prepare_qk: q heads (%d) not a multiple of kv heads (%d)", hq, hk);
+  const bool int4 = q4 != nullptr;
+  if (int4 != (qa4 != nullptr) || int4 != (k4p != nullptr) || int4 != (ka4 != nullptr))
+    return fail("prepare_qk: INT4 Q/K buffers (all or none)");
+  if (!aligned(q, 8) || !aligned(k, 8) || (q_st | q_sh | q_sb | k_st | k_sh | k_sb) % 4 != 0)
+    return fail("prepare_qk: Q/K rows must be 8-byte aligned");
+  if (!aligned(kp, 16) || !aligned(q8, 16) || (int4 && (!aligned(k4p, 16) || !aligned(q4, 4))))
+    return fail("prepare_qk: output buffers must be 16-byte aligned");
+  const int tiles = (t + tri::BN - 1) / tri::BN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tri::quantize_q_kernel<<<dim3((t + 7) / 8, hq, batch), 256, 0, s>>>(
+      static_cast<const uint16_t*>(q), q_sb, q_sh, q_st, hq, t, static_cast<int8_t*>(q8), qa,
+      static_cast<uint8_t*>(q4), qa4);
+  tri::partial_kernel<<<dim3(tri::STAT_BLOCKS, hk, batch), tri::D, 0, s>>>(static_cast<const uint16_t*>(k), k_sb,
+                                                                          k_sh, k_st, hk, t, partial);
+  tri::finalize_kernel<<<dim3(hk, batch), tri::D, 0, s>>>(partial, kstat, hk, t, 0);
+  tri::quantize_k_kernel<<<dim3(tiles, hk, batch), 256, 0, s>>>(static_cast<const uint16_t*>(k), k_sb, k_sh, k_st,
+                                                                kstat, hk, t, static_cast<uint8_t*>(kp), ka,
+                                                                static_cast<uint8_t*>(k4p), ka4);
+  return check_launch("prepare_qk");
+}
+
+int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batch, int hk, int t, float* partial,
+               float* vstat, void* v16p, void* v8p, void* v4p, void* stream) {
+  g_error.clear();
+  if (!v || !partial || !vstat) return fail("pack_v: null buffer");
+  if (batch < 1 || hk < 1 || t < 1) return fail("pack_v: empty shape");
+  if (!aligned(v, 8) || (v_st | v_sh | v_sb) % 4 != 0) return fail("pack_v: V rows must be 8-byte aligned");
+  if ((v16p && !aligned(v16p, 16)) || (v8p && !aligned(v8p, 16)) || (v4p && !aligned(v4p, 8)))
+    return fail("pack_v: record buffers must be 16-byte aligned");
+  const int tiles = (t + tri::BN - 1) / tri::BN;
+  const bool identity = v8p == nullptr && v4p == nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!identity)
+    tri::partial_kernel<<<dim3(tri::STAT_BLOCKS, hk, batch), tri::D, 0, s>>>(static_cast<const uint16_t*>(v), v_sb,
+                                                                            v_sh, v_st, hk, t, partial);
+  tri::finalize_kernel<<<dim3(hk, batch), tri::D, 0, s>>>(partial, vstat, hk, t, identity ? 1 : 0);
+  tri::pack_v_kernel<<<dim3(tiles, hk, batch), 256, 0, s>>>(static_cast<const uint16_t*>(v), v_sb, v_sh, v_st, vstat,
+                                                            hk, t, static_cast<uint8_t*>(v16p),
+                                                            static_cast<uint8_t*>(v8p), static_cast<uint8_t*>(v4p));
+  return check_launch("pack_v");
+}
+
+int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int batch, int hq, int hk, int t,
+                  const void* v16p, const void* v8p, const float* vstat, const void* q8, const void* k8p,
+                  const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
+                  const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                  double scale, void* stream) {
+  g_error.clear();
+  const int tiles = (t + tri::BN - 1) / tri::BN;
+  if (!order || !bands || !v16p || !vstat || !q8 || !k8p || !qa8 || !ka8 || !out)
+    return fail("attention: null buffer");
+  if (batch < 1 || hq < 1 || hk < 1 || t < 1) return fail("attention: empty shape");
+  if (tiles > tri::MAX_TILES) return fail("attention: at most 131072 tokens");
+  if (hq % hk != 0) return fail("attention: q heads not a multiple of kv heads");
+  if (n_order != hq * tiles) return fail("attention: CTA order must have hq*tiles entries");
+  const bool int4 = q4 != nullptr;
+  if (int4 != (k4p != nullptr) || int4 != (qa4 != nullptr) || int4 != (ka4 != nullptr))
+    return fail("attention: INT4 Q/K operands (all or none)");
+  if (out_dtype < 0 || out_dtype > 2) return fail("attention: out dtype must be fp32, bf16 or fp16");
+  const int esz = out_dtype == 0 ? 4 : 2;
+  if (!aligned(out, 16) || (o_st % 4) || (o_sh % 4) || (o_sb % 4))
+    return fail("attention: output [B,Hq,T,128] must be 16-byte aligned with strides a multiple of 4");
+  (void)esz;
+  tri::PrefillArgs a;
+  a.order = order;
+  a.bands = bands;
+  a.v16 = static_cast<const uint8_t*>(v16p);
+  a.v8 = static_cast<const uint8_t*>(v8p);
+  a.vstat = vstat;
+  a.q8 = static_cast<const int8_t*>(q8);
+  a.k8 = static_cast<const uint8_t*>(k8p);
+  a.qa = qa8;
+  a.ka = ka8;
+  a.q4 = static_cast<const uint8_t*>(q4);
+  a.k4 = static_cast<const uint8_t*>(k4p);
+  a.qa4 = qa4;
+  a.ka4 = ka4;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.osb = o_sb;
+  a.osh = o_sh;
+  a.ost = o_st;
+  a.hq = hq;
+  a.hk = hk;
+  a.t = t;
+  a.sm_log2 = (float)(scale * 1.4426950408889634);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tri::prefill_kernel<<<dim3(n_order, batch), 128, 0, s>>>(a);
+  return check_launch("attention");
+}
+
+int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
+               const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
+               const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
+               const float* kstat, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh, int64_t t_st,
+               int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh, const int64_t* step,
+               void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
+               const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max, double scale,
+               void* stream) {
+  g_error.clear();
+  if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
+      !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
+    return fail("decode: null buffer");
+  if (batch < 1 || hq < 1 || hk < 1 || maxn < 1 || per < 1 || tiles_max < 1) return fail("decode: empty shape");
+  if (hq % hk != 0 || hq / hk > tri::MAX_GROUP) return fail("decode: GQA group must divide and be <= 8");
+  if (max_tail < 1 || max_tail > tri::MAX_TAIL) return fail("decode: max_tail must be in [1, 1024]");
+  if ((k4c == nullptr) != (ka4 == nullptr)) return fail("decode: INT4 K records and scales (all or none)");
+  if (out_dtype != 0 && out_dtype != 1) return fail("decode: out dtype must be fp32 or bf16");
+  if (!aligned(q, 8) || (q_sh % 4) || (q_sb % 4)) return fail("decode: q rows must be 8-byte aligned");
+  if (!aligned(po, 16)) return fail("decode: po must be 16-byte aligned");
+  const int splits = std::max(1, (maxn + per - 1) / per);
+  tri::DecodeArgs d;
+  d.q = static_cast<const uint16_t*>(q);
+  d.k8c = static_cast<const uint8_t*>(k8c);
+  d.k4c = static_cast<const uint8_t*>(k4c);
+  d.ka = ka;
+  d.ka4 = ka4;
+  d.entry = entry;
+  d.kinfo = kinfo;
+  d.count = count;
+  d.fmt = fmt;
+  d.slot = slot;
+  d.v8c = static_cast<const uint8_t*>(v8c);
+  d.v4c = static_cast<const uint8_t*>(v4c);
+  d.prompt = prompt;
+  d.pm = pm;
+  d.pl = pl;
+  d.po = po;
+  d.qsb = q_sb;
+  d.qsh = q_sh;
+  d.hq = hq;
+  d.hk = hk;
+  d.maxn = maxn;
+  d.per = per;
+  d.tiles_max = tiles_max;
+  d.splits = splits;
+  d.sm_log2 = (float)(scale * 1.4426950408889634);
+  tri::MergeArgs mg;
+  mg.pm = pm;
+  mg.pl = pl;
+  mg.po = po;
+  mg.vstat = vstat;
+  mg.kstat = kstat;
+  mg.q = static_cast<const uint16_t*>(q);
+  mg.ktail = static_cast<uint16_t*>(ktail);
+  mg.vtail = static_cast<uint16_t*>(vtail);
+  mg.kcur = static_cast<const uint16_t*>(kcur);
+  mg.vcur = static_cast<const uint16_t*>(vcur);
+  mg.step = step;
+  mg.out = out;
+  mg.out_dtype = out_dtype;
+  mg.qsb = q_sb;
+  mg.qsh = q_sh;
+  mg.tsb = t_sb;
+  mg.tsh = t_sh;
+  mg.tst = t_st;
+  mg.csb = c_sb;
+  mg.csh = c_sh;
+  mg.osb = o_sb;
+  mg.osh = o_sh;
+  mg.hq = hq;
+  mg.hk = hk;
+  mg.splits = splits;
+  mg.max_tail = max_tail;
+  mg.sm_log2 = d.sm_log2;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tri::decode_kernel<<<dim3(splits, hk, batch), 64, 0, s>>>(d);
+  tri::decode_merge_kernel<<<dim3(hq, batch), 256, 0, s>>>(mg);
+  return check_launch("decode");
+}
+
+int tri_decode_occupancy(int* blocks) {
+  g_error.clear();
+  if (!blocks) return fail("decode_occupancy: null output");
+  int n = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, tri::decode_kernel, 64, 0);
+  if (e != hipSuccess) return fail("decode_occupancy: %s", hipGetErrorString(e));
+  *blocks = n;
+  return 0;
+}
+
+int tri_device_cus(int* cus) {
+  g_error.clear();
+  if (!cus) return fail("device_cus: null output");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return fail("device_cus: %s", hipGetErrorString(e));
+  return 0;
+}
+
+}  // extern "C"

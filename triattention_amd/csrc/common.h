@@ -1,0 +1,128 @@
+// Shared device helpers for the gfx950 TriAttention kernels.
+//
+// Record layouts (one record = one 64-key tile of one KV head).  Sizes match the
+// reference's record word counts (triattention/kernels/decode.py:7-8,
+// cuda/prefill_sm80.cu:17-22); the byte order inside a record is chosen so that
+// each 1 KiB (512 B for 4-bit records) "fragment" is exactly one operand of a
+// 32x32 MFMA, loaded with one 16-byte (8-byte) access per lane:
+//
+//   K8  8192 B  fragment F = kb*4 + ks (kb: 32-key block, ks: 32-feature step)
+//               lane L byte j  <->  key kb*32 + L%32, feature ks*32 + 16*(L/32) + j
+//   K4  4096 B  fragment F (512 B), lane L holds words w0,w1; K8-layout byte j is
+//               the low nibble of w0 byte j (j<4), high nibble of w0 byte j-4 (j<8),
+//               low nibble of w1 byte j-8 (j<12), high nibble of w1 byte j-12.
+//   V8  8192 B  fragment F = cb*2 + kb (cb: 32-channel block, kb: 32-key block)
+//               lane L byte p  <->  key kb*32 + 8*(p/4) + 4*(L/32) + p%4, channel cb*32 + L%32
+//   V16 16384 B fragment F = (cb*2 + kb)*2 + kh, lane L fp16 element e (0..7)
+//               <->  key kb*32 + 8*(2*kh + e/4) + 4*(L/32) + e%4, channel cb*32 + L%32
+//   V4  4096 B  fragment F = cb*2 + kb (512 B), nibbles of the V8 layout packed as K4.
+//
+// The V orders equal the accumulator order of the QK^T MFMA (key = row of the
+// 32x32 result), so a lane's probabilities feed the PV MFMA without shuffles.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tri {
+
+constexpr int D = 128;
+constexpr int BN = 64;
+constexpr int STAT_BLOCKS = 64;
+constexpr int K8_BYTES = 8192, K4_BYTES = 4096, V16_BYTES = 16384, V8_BYTES = 8192, V4_BYTES = 4096;
+constexpr int K8_WORDS = K8_BYTES / 4, K4_WORDS = K4_BYTES / 4;
+constexpr int V16_WORDS = V16_BYTES / 4, V8_WORDS = V8_BYTES / 4, V4_WORDS = V4_BYTES / 4;
+constexpr float MAGIC = 12582912.0f;      // 1.5 * 2^23
+constexpr uint32_t MAGIC_BITS = 0x4B400000u;
+constexpr float PMAGIC_HALF = 49152.5f;    // P quantizer: byte 1 of fma(e, 255, 49152.5)
+constexpr int MAX_TILES = 2048;            // 131072 tokens (prefill_sm80.cu:23)
+constexpr int MAX_GROUP = 8;               // GQA group bound of the decode kernel
+constexpr int NEAR_V8 = 16;                // decode V recency window (decode.py:9)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  const _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// The path's exp2: clamp to >= -125, split x = n + f with n = rint(x), degree-6
+// polynomial for 2^f in Horner order with fma, scale by 2^n.  The CPU oracle
+// evaluates the identical sequence, so results agree bit for bit.
+__device__ __forceinline__ float texp2(float x) {
+  x = fmaxf(x, -125.0f);
+  const float n = __builtin_rintf(x);
+  const float f = x - n;
+  float p = 0x1.41d32ep-13f;
+  p = __builtin_fmaf(p, f, 0x1.5f456cp-10f);
+  p = __builtin_fmaf(p, f, 0x1.3b2dbcp-7f);
+  p = __builtin_fmaf(p, f, 0x1.c6aed4p-5f);
+  p = __builtin_fmaf(p, f, 0x1.ebfbdap-3f);
+  p = __builtin_fmaf(p, f, 0x1.62e430p-1f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  return __builtin_amdgcn_ldexpf(p, (int)n);
+}
+
+// Sign pattern of the 128-channel rotation (prefill_sm80.cu:95).
+__device__ __forceinline__ bool rot_sign(int c) {
+  const uint32_t s = c < 32 ? 0x9a3b5e71u : c < 64 ? 0x2c6d8f13u : c < 96 ? 0xe41b7a95u : 0x5f02c3d8u;
+  return (s >> (c & 31)) & 1u;
+}
+
+// Rotation of one 128-vector held by 32 consecutive lanes, 4 channels each
+// (channel 4*l + i in lane l of the 32-lane group).  Butterfly stages run over
+// index bits 0..6 in order, (lo, hi) -> (lo + hi, lo - hi).
+__device__ __forceinline__ void rotate128_x4(float (&x)[4], int l32) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (rot_sign(l32 * 4 + i)) x[i] = -x[i];
+  const float a = x[0] + x[1], b = x[0] - x[1], c = x[2] + x[3], d = x[2] - x[3];
+  x[0] = a + c; x[1] = b + d; x[2] = a - c; x[3] = b - d;
+#pragma unroll
+  for (int bit = 1; bit < 32; bit <<= 1) {
+    const bool upper = l32 & bit;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float y = __shfl_xor(x[i], bit, 32);
+      x[i] = upper ? y - x[i] : x[i] + y;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] *= 0.08838834764831845f;
+}
+
+__device__ __forceinline__ float warp32_max(float m) {
+#pragma unroll
+  for (int o = 16; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
+  return m;
+}
+
+// byte 1 of each of four words, packed (P levels out of the 49152.5 magic).
+__device__ __forceinline__ uint32_t pack_byte1(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+  const uint32_t lo = __builtin_amdgcn_perm(w1, w0, 0x0c0c0501u);  // [w0.b1, w1.b1, 0, 0]
+  const uint32_t hi = __builtin_amdgcn_perm(w3, w2, 0x05010c0cu);  // [0, 0, w2.b1, w3.b1]
+  return lo | hi;
+}
+
+// Four packed 4-bit codes in the high halves of bytes (16 * signed code).
+__device__ __forceinline__ uint32_t nib_lo16(uint32_t w) { return (w << 4) & 0xf0f0f0f0u; }
+__device__ __forceinline__ uint32_t nib_hi16(uint32_t w) { return w & 0xf0f0f0f0u; }
+
+__device__ __forceinline__ v16i mfma_i8(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v16f mfma_f16(v8h a, v8h b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace tri

@@ -1,0 +1,322 @@
+// Causal banded quantized attention for gfx950 (one launch for every q-head and
+// query tile; each q-head's band picks per key tile between fp16 P x fp16 V',
+// INT8 QK with u8 P x INT8 V', INT4 QK with u8 P x INT8 V', or skip).
+//
+// Reference semantics: triattention/kernels/cuda/prefill_sm80.cu:244-505
+// (scaled_row_max, tile_base_margin, run_task, unified_kernel).
+//
+// Work decomposition: one workgroup of 2 waves per (batch, q-head, 64-row query
+// tile); wave w owns query rows 32w..32w+31.  Scores are computed transposed,
+// S^T = K Q^T, with v_mfma_i32_32x32x32_i8, so lane L holds the 32 scores of
+// query L%32 for keys {kb*32 + 8*(r/4) + 4*(L/32) + r%4}; the same lane then
+// feeds its probabilities as the B operand of O^T = V^T P^T.  Row statistics
+// need one cross-lane step (lanes L and L^32 share a query).
+#include "common.h"
+
+namespace tri {
+
+struct PrefillArgs {
+  const int32_t* order;
+  const int32_t* bands;
+  const uint8_t* v16;
+  const uint8_t* v8;
+  const float* vstat;
+  const int8_t* q8;
+  const uint8_t* k8;
+  const float* qa;
+  const float* ka;
+  const uint8_t* q4;
+  const uint8_t* k4;
+  const float* qa4;
+  const float* ka4;
+  void* out;
+  int out_dtype;  // 0 = fp32, 1 = bf16, 2 = fp16
+  int64_t osb, osh, ost;
+  int hq, hk, t;
+  float sm_log2;
+};
+
+enum Kind { KF16 = 0, KI8 = 1, KQ4 = 2 };
+
+struct PrefillState {
+  v16f acc[4];     // O^T accumulators, 4 channel blocks of 32
+  float m, den;    // running max (log2 units) and denominator, equal in lanes L and L^32
+};
+
+__device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
+
+template <int KIND>
+__device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState& st, const v4i (&qf)[4], float qs,
+                                             const float* __restrict__ ks, int col, bool masked, int qrow,
+                                             const uint8_t* __restrict__ k_lds, const uint8_t* __restrict__ v_lds) {
+  const int L = threadIdx.x & 63, half = L >> 5;
+  // ---- S^T = K Q^T over 128 features, two 32-key blocks
+  v16i s[2];
+  const int init = KIND == KQ4 ? 0 : (int)MAGIC_BITS;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[kb][r] = init;
+#pragma unroll
+  for (int kstep = 0; kstep < 4; ++kstep)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      s[kb] = mfma_i8(*reinterpret_cast<const v4i*>(k_lds + (kb * 4 + kstep) * 1024 + L * 16), qf[kstep], s[kb]);
+
+  float x[2][16];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = KIND == KQ4 ? (float)s[kb][r] * 0.0625f : __int_as_float(s[kb][r]);
+      if (masked) {
+        const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (key > qrow || key >= a.t) v = -__builtin_inff();
+      }
+      x[kb][r] = v;
+    }
+
+  // ---- scaled row max (prefill_sm80.cu:244-253)
+  float slope[4];
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) slope[gi] = qs * ks[gi];
+  float tile = -__builtin_inff();
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int hg = 0; hg < 2; ++hg) {
+      float mx = x[kb][hg * 8];
+#pragma unroll
+      for (int r = 1; r < 8; ++r) mx = fmaxf(mx, x[kb][hg * 8 + r]);
+      if (mx > -__builtin_inff()) {
+        const float d = KIND == KQ4 ? mx : mx - MAGIC;
+        tile = fmaxf(tile, slope[kb * 2 + hg] * d);
+      }
+    }
+  tile = xor32_max(tile);
+  const float n = fmaxf(st.m, tile);
+  const float alpha = texp2(st.m - n);
+  st.m = n;
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[cb][r] *= alpha;
+  }
+
+  if constexpr (KIND == KF16) {
+    // ---- fp16 P x fp16 V' (prefill_sm80.cu:358-383)
+    st.den *= alpha;
+    float c[4];
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) c[gi] = __builtin_fmaf(-slope[gi], MAGIC, -st.m);
+    v8h p[2][2];
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gi = kb * 2 + (r >> 3);
+        const _Float16 h = (_Float16)texp2(__builtin_fmaf(slope[gi], x[kb][r], c[gi]));
+        p[kb][r >> 3][r & 7] = h;
+        psum += (float)h;
+      }
+    psum += __shfl_xor(psum, 32, 64);
+    st.den += psum;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const v8h vf = *reinterpret_cast<const v8h*>(v_lds + ((cb * 2 + kb) * 2 + kh) * 1024 + L * 16);
+          st.acc[cb] = mfma_f16(vf, p[kb][kh], st.acc[cb]);
+        }
+  } else {
+    // ---- quantized P (u8) x INT8 V' (prefill_sm80.cu:384-449)
+    const float ksmax = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
+    float base = tile > -__builtin_inff() ? tile : st.m;
+    base += __builtin_fmaf(qs * ksmax, 0.75f, fabsf(base) * 2.4e-7f);
+    const float bq = texp2(base - st.m) / 255.f;
+    float c[4];
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi)
+      c[gi] = KIND == KI8 ? __builtin_fmaf(-slope[gi], MAGIC, -base) : -base;
+    uint32_t pw[2][4];
+    uint32_t rs = 0;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        uint32_t y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = qd * 4 + i, gi = kb * 2 + (r >> 3);
+          const float e = texp2(__builtin_fmaf(slope[gi], x[kb][r], c[gi]));
+          y[i] = __float_as_uint(__builtin_fmaf(e, 255.f, PMAGIC_HALF));
+        }
+        const uint32_t w = pack_byte1(y[0], y[1], y[2], y[3]);
+        rs = __builtin_amdgcn_udot4(w, 0x01010101u, rs, false);
+        pw[kb][qd] = w ^ 0x7f7f7f7fu;  // 127 - P as s8
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    st.den = __builtin_fmaf((float)rs, bq, st.den * alpha);
+    const v4i neg127 = {(int)0x81818181u, (int)0x81818181u, (int)0x81818181u, (int)0x81818181u};
+    const v4i b0 = {(int)pw[0][0], (int)pw[0][1], (int)pw[0][2], (int)pw[0][3]};
+    const v4i b1 = {(int)pw[1][0], (int)pw[1][1], (int)pw[1][2], (int)pw[1][3]};
+    const float nbq = -bq;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const v4i va = *reinterpret_cast<const v4i*>(v_lds + (cb * 2 + 0) * 1024 + L * 16);
+      const v4i vb = *reinterpret_cast<const v4i*>(v_lds + (cb * 2 + 1) * 1024 + L * 16);
+      v16i d = {};
+      d = mfma_i8(va, neg127, d);
+      d = mfma_i8(vb, neg127, d);
+      d = mfma_i8(va, b0, d);
+      d = mfma_i8(vb, b1, d);  // = -sum_k P_k v_k
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[cb][r] = __builtin_fmaf((float)d[r], nbq, st.acc[cb][r]);
+    }
+  }
+}
+
+// Global -> LDS staging of one key tile (K unpacked to 16*code bytes for INT4).
+template <int KIND>
+__device__ __forceinline__ void stage_tile(const PrefillArgs& a, int64_t rec, uint8_t* k_lds, uint8_t* v_lds) {
+  const int tid = threadIdx.x;
+  if constexpr (KIND == KQ4) {
+    const uint8_t* src = a.k4 + rec * K4_BYTES;
+#pragma unroll
+    for (int s = tid; s < 512; s += 128) {
+      const uint2 w = *reinterpret_cast<const uint2*>(src + s * 8);
+      *reinterpret_cast<uint4*>(k_lds + s * 16) = make_uint4(nib_lo16(w.x), nib_hi16(w.x), nib_lo16(w.y), nib_hi16(w.y));
+    }
+  } else {
+    const uint8_t* src = a.k8 + rec * K8_BYTES;
+#pragma unroll
+    for (int s = tid; s < 512; s += 128)
+      *reinterpret_cast<uint4*>(k_lds + s * 16) = *reinterpret_cast<const uint4*>(src + s * 16);
+  }
+  if constexpr (KIND == KF16) {
+    const uint8_t* src = a.v16 + rec * V16_BYTES;
+#pragma unroll
+    for (int s = tid; s < 1024; s += 128)
+      *reinterpret_cast<uint4*>(v_lds + s * 16) = *reinterpret_cast<const uint4*>(src + s * 16);
+  } else {
+    const uint8_t* src = a.v8 + rec * V8_BYTES;
+#pragma unroll
+    for (int s = tid; s < 512; s += 128)
+      *reinterpret_cast<uint4*>(v_lds + s * 16) = *reinterpret_cast<const uint4*>(src + s * 16);
+  }
+}
+
+template <int KIND>
+__device__ __forceinline__ void prefill_pass(const PrefillArgs& a, PrefillState& st, const v4i (&qf)[4], float qs,
+                                             const float* __restrict__ kscale, int64_t rec0, int first, int count,
+                                             int step, int qb, int qrow, uint8_t* k_lds, uint8_t* v_lds) {
+  for (int i = 0; i < count; ++i) {
+    const int col = first + i * step;
+    const bool masked = (i == count - 1) && col == qb;
+    __syncthreads();
+    stage_tile<KIND>(a, rec0 + col, k_lds, v_lds);
+    __syncthreads();
+    float ks[4];
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) ks[gi] = kscale[col * 4 + gi];
+    prefill_tile<KIND>(a, st, qf, qs, ks, col, masked, qrow, k_lds, v_lds);
+  }
+}
+
+__global__ __launch_bounds__(128) void prefill_kernel(PrefillArgs a) {
+  __shared__ __align__(16) uint8_t k_lds[K8_BYTES];
+  __shared__ __align__(16) uint8_t v_lds[V16_BYTES];
+  const int rows = (a.t + BN - 1) / BN;
+  const int task = a.order[blockIdx.x], b = blockIdx.y;
+  const int qh = task / rows, qb = task % rows, g = a.hq / a.hk, kh = qh / g;
+  const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
+  const int qrow = qb * BN + wave * 32 + lq;
+  const bool row_ok = qrow < a.t;
+  const int tiles = rows;
+  const int64_t qrow_idx = ((int64_t)b * a.hq + qh) * a.t + qrow;
+  const int64_t rec0 = ((int64_t)b * a.hk + kh) * tiles;
+
+  // band lists (prefill_sm80.cu:280-286)
+  const int w8 = a.bands[2 * qh], w4 = a.bands[2 * qh + 1];
+  const int lo8 = max(1, qb - w8 + 1), n8 = max(0, qb - lo8);
+  const int lo4 = max(1, qb - w4 + 1), n4 = max(0, qb - w8 - lo4 + 1);
+
+  v4i qf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    v4i z = {0, 0, 0, 0};
+    qf[ks] = row_ok ? *reinterpret_cast<const v4i*>(a.q8 + qrow_idx * D + ks * 32 + 16 * half) : z;
+  }
+  const float qs8 = row_ok ? a.qa[qrow_idx] * a.sm_log2 : 1.17549435e-38f;
+  PrefillState st;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st.acc[cb][r] = 0.f;
+  st.m = -3.402823466e38f;
+  st.den = 0.f;
+  const float* ka8 = a.ka + rec0 * 4;
+
+  // F16 pass: tile 0, then the diagonal tile when qb > 0
+  if (qb > 0) prefill_pass<KF16>(a, st, qf, qs8, ka8, rec0, 0, 2, qb, qb, qrow, k_lds, v_lds);
+  else prefill_pass<KF16>(a, st, qf, qs8, ka8, rec0, 0, 1, 1, qb, qrow, k_lds, v_lds);
+  if (n8 > 0) prefill_pass<KI8>(a, st, qf, qs8, ka8, rec0, lo8, n8, 1, qb, qrow, k_lds, v_lds);
+  if (n4 > 0) {
+    // INT4 Q codes, sign-extended to bytes in feature order
+    v4i q4f[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint2 raw = make_uint2(0u, 0u);
+      if (row_ok) raw = *reinterpret_cast<const uint2*>(a.q4 + qrow_idx * (D / 2) + (ks * 32 + 16 * half) / 2);
+      const uint32_t wd[2] = {raw.x, raw.y};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w = wd[j >> 1] >> (16 * (j & 1));
+        uint32_t out = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t nib = (w >> (4 * e)) & 0xfu;
+          out |= ((uint32_t)(((int)(nib ^ 8u)) - 8) & 0xffu) << (8 * e);
+        }
+        o[j] = out;
+      }
+      q4f[ks] = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+    }
+    const float qs4 = row_ok ? a.qa4[qrow_idx] * a.sm_log2 : 1.17549435e-38f;
+    prefill_pass<KQ4>(a, st, q4f, qs4, a.ka4 + rec0 * 4, rec0, lo4, n4, 1, qb, qrow, k_lds, v_lds);
+  }
+
+  // ---- epilogue: out = fma(acc / den, scale, mean) (prefill_sm80.cu:466-487)
+  if (!row_ok) return;
+  const float inv = st.den > 0.f ? 1.f / st.den : 0.f;
+  const float* mean = a.vstat + ((int64_t)b * a.hk + kh) * 3 * D;
+  const float* scale = mean + D;
+  const int64_t obase = b * a.osb + qh * a.osh + (int64_t)qrow * a.ost;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int ch = cb * 32 + 8 * r4 + 4 * half;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(st.acc[cb][r4 * 4 + i] * inv, scale[ch + i], mean[ch + i]);
+      if (a.out_dtype == 0) {
+        *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + ch) = make_float4(v[0], v[1], v[2], v[3]);
+      } else if (a.out_dtype == 1) {
+        const uint32_t lo = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + ch) = make_uint2(lo, hi);
+      } else {
+        const uint32_t lo = f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
+        const uint32_t hi = f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + ch) = make_uint2(lo, hi);
+      }
+    }
+}
+
+}  // namespace tri

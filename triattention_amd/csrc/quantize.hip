@@ -1,0 +1,232 @@
+// Rotate + quantize kernels for gfx950: Q per-token INT8/INT4 codes, per-channel
+// K/V statistics, centred+rotated K records with per-(tile, 16-key group) scales,
+// and the normalised V records.  All arithmetic is IEEE fp32 with the
+// reference's operation order, so codes and scales are bit-exact.
+//
+// Reference semantics: triattention/kernels/cuda/common_device.cuh:1-172.
+#include "common.h"
+
+namespace tri {
+
+// One 128-feature row per 32 lanes, 8 rows per 256-thread block.
+// common_device.cuh:1-28 (quantize_q_kernel).
+__global__ __launch_bounds__(256) void quantize_q_kernel(const uint16_t* __restrict__ q, int64_t sb, int64_t sh,
+                                                         int64_t st, int hq, int t, int8_t* __restrict__ q8,
+                                                         float* __restrict__ qa, uint8_t* __restrict__ q4,
+                                                         float* __restrict__ qa4) {
+  const int l32 = threadIdx.x & 31, row = blockIdx.x * 8 + (threadIdx.x >> 5), h = blockIdx.y, b = blockIdx.z;
+  if (row >= t) return;  // whole 32-lane groups leave together
+  const uint2 raw = *reinterpret_cast<const uint2*>(q + b * sb + h * sh + (int64_t)row * st + l32 * 4);
+  float x[4] = {bf16f(raw.x & 0xffffu), bf16f(raw.x >> 16), bf16f(raw.y & 0xffffu), bf16f(raw.y >> 16)};
+  rotate128_x4(x, l32);
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(x[i]));
+  m = warp32_max(m);
+  const int64_t r = ((int64_t)b * hq + h) * t + row;
+  const float inv = m > 0.f ? 127.f / m : 0.f;
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) word |= ((uint32_t)(int)__builtin_rintf(x[i] * inv) & 0xffu) << (8 * i);
+  reinterpret_cast<uint32_t*>(q8 + r * D)[l32] = word;
+  if (l32 == 0) qa[r] = m / 127.f;
+  if (q4 != nullptr) {
+    const float inv4 = m > 0.f ? 7.f / m : 0.f;
+    uint32_t nib = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nib |= ((uint32_t)(int)__builtin_rintf(x[i] * inv4) & 0xfu) << (4 * i);
+    reinterpret_cast<uint16_t*>(q4 + r * (D / 2))[l32] = (uint16_t)nib;
+    if (l32 == 0) qa4[r] = m / 7.f;
+  }
+}
+
+// Per channel: sequential sum/max/min over tokens t = blk, blk+64, ...
+// common_device.cuh:32-42 (partial_kernel).  partial [B][H][64][3][128].
+__global__ __launch_bounds__(128) void partial_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t sh,
+                                                      int64_t st, int h, int t, float* __restrict__ partial) {
+  const int blk = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, c = threadIdx.x;
+  const uint16_t* base = x + b * sb + hd * sh + c;
+  float sum = 0.f, hi = -3.402823466e38f, lo = 3.402823466e38f;
+  int tk = blk;
+  for (; tk + 3 * STAT_BLOCKS < t; tk += 4 * STAT_BLOCKS) {
+    const float v0 = bf16f(base[(int64_t)tk * st]), v1 = bf16f(base[(int64_t)(tk + STAT_BLOCKS) * st]);
+    const float v2 = bf16f(base[(int64_t)(tk + 2 * STAT_BLOCKS) * st]), v3 = bf16f(base[(int64_t)(tk + 3 * STAT_BLOCKS) * st]);
+    sum += v0; sum += v1; sum += v2; sum += v3;
+    hi = fmaxf(fmaxf(hi, v0), fmaxf(fmaxf(v1, v2), v3));
+    lo = fminf(fminf(lo, v0), fminf(fminf(v1, v2), v3));
+  }
+  for (; tk < t; tk += STAT_BLOCKS) {
+    const float v = bf16f(base[(int64_t)tk * st]);
+    sum += v;
+    hi = fmaxf(hi, v);
+    lo = fminf(lo, v);
+  }
+  float* o = partial + ((((int64_t)b * h + hd) * STAT_BLOCKS + blk) * 3) * D + c;
+  o[0] = sum;
+  o[D] = hi;
+  o[2 * D] = lo;
+}
+
+// mean = (sum of block sums in block order) / T, scale = range/127 (1 if 0),
+// inv = 1/scale; identity mode writes (0, 1, 1).  common_device.cuh:44-56.
+__global__ __launch_bounds__(128) void finalize_kernel(const float* __restrict__ partial, float* __restrict__ stat,
+                                                       int h, int t, int identity) {
+  const int hd = blockIdx.x, b = blockIdx.y, c = threadIdx.x;
+  const int64_t hb = (int64_t)b * h + hd;
+  float mean = 0.f, scale = 1.f;
+  if (!identity) {
+    const float* in = partial + hb * STAT_BLOCKS * 3 * D + c;
+    float sum = 0.f, hi = -3.402823466e38f, lo = 3.402823466e38f;
+    for (int blk = 0; blk < STAT_BLOCKS; ++blk) {
+      sum += in[blk * 3 * D];
+      hi = fmaxf(hi, in[blk * 3 * D + D]);
+      lo = fminf(lo, in[blk * 3 * D + 2 * D]);
+    }
+    mean = sum / (float)t;
+    const float range = fmaxf(hi - mean, mean - lo);
+    scale = range > 0.f ? range / 127.f : 1.f;
+  }
+  stat[hb * 3 * D + c] = mean;
+  stat[hb * 3 * D + D + c] = scale;
+  stat[hb * 3 * D + 2 * D + c] = 1.f / scale;
+}
+
+// y = R(k - mean) for one 64-key tile; wave w owns the 16-key group w.
+// INT8 record + group scale ka, optional INT4 record + ka4.
+// common_device.cuh:58-131 (quantize_k_kernel).
+__global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restrict__ k, int64_t sb, int64_t sh,
+                                                         int64_t st, const float* __restrict__ kstat, int hk, int t,
+                                                         uint8_t* __restrict__ k8, float* __restrict__ ka,
+                                                         uint8_t* __restrict__ k4, float* __restrict__ ka4) {
+  __shared__ __align__(16) uint8_t c8[BN][D];
+  __shared__ __align__(16) uint8_t c4[BN][D];
+  const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+  const int64_t hb = (int64_t)b * hk + hd;
+  const float* mean = kstat + hb * 3 * D;
+  float mc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) mc[i] = mean[l32 * 4 + i];
+  float y[8][4];
+  float cm = 0.f;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = wave * 16 + it * 2 + half, tk = tile * BN + r;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (tk < t) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(k + b * sb + hd * sh + (int64_t)tk * st + l32 * 4);
+      x[0] = bf16f(raw.x & 0xffffu) - mc[0];
+      x[1] = bf16f(raw.x >> 16) - mc[1];
+      x[2] = bf16f(raw.y & 0xffffu) - mc[2];
+      x[3] = bf16f(raw.y >> 16) - mc[3];
+    }
+    rotate128_x4(x, l32);  // every lane of the wave takes part (padded rows rotate zeros)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      y[it][i] = x[i];
+      cm = fmaxf(cm, fabsf(x[i]));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 64));
+  const float inv = cm > 0.f ? 127.f / cm : 0.f, inv4 = cm > 0.f ? 7.f / cm : 0.f;
+  const int64_t si = (hb * tiles + tile) * 4 + wave;
+  if (lane == 0) {
+    ka[si] = cm > 0.f ? cm / 127.f : 1.f;
+    if (k4 != nullptr) ka4[si] = cm > 0.f ? cm / 7.f : 1.f;
+  }
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = wave * 16 + it * 2 + half;
+    uint32_t w8 = 0, w4 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w8 |= ((uint32_t)(int)__builtin_rintf(y[it][i] * inv) & 0xffu) << (8 * i);
+      w4 |= ((uint32_t)(int)__builtin_rintf(y[it][i] * inv4) & 0xfu) << (8 * i);
+    }
+    *reinterpret_cast<uint32_t*>(&c8[r][l32 * 4]) = w8;
+    *reinterpret_cast<uint32_t*>(&c4[r][l32 * 4]) = w4;
+  }
+  __syncthreads();
+  uint8_t* rec8 = k8 + (hb * tiles + tile) * K8_BYTES;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int s = tid + it * 256, F = s >> 6, L = s & 63, kb = F >> 2, ks = F & 3;
+    const int key = kb * 32 + (L & 31), f0 = ks * 32 + 16 * (L >> 5);
+    *reinterpret_cast<uint4*>(rec8 + F * 1024 + L * 16) = *reinterpret_cast<const uint4*>(&c8[key][f0]);
+  }
+  if (k4 == nullptr) return;
+  uint8_t* rec4 = k4 + (hb * tiles + tile) * K4_BYTES;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int s = tid + it * 256, F = s >> 6, L = s & 63, kb = F >> 2, ks = F & 3;
+    const int key = kb * 32 + (L & 31), f0 = ks * 32 + 16 * (L >> 5);
+    const uint4 n = *reinterpret_cast<const uint4*>(&c4[key][f0]);  // one nibble value per byte
+    const uint32_t w0 = n.x | (n.y << 4), w1 = n.z | (n.w << 4);
+    *reinterpret_cast<uint2*>(rec4 + F * 512 + L * 8) = make_uint2(w0, w1);
+  }
+}
+
+// v' = (v - mean) * inv (zero for padded keys) into V16 (fp16), V8 and V4 records.
+// common_device.cuh:132-172 (vnorm, pack_v_kernel).
+__global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict__ v, int64_t sb, int64_t sh,
+                                                     int64_t st, const float* __restrict__ vstat, int hk, int t,
+                                                     uint8_t* __restrict__ v16, uint8_t* __restrict__ v8,
+                                                     uint8_t* __restrict__ v4) {
+  __shared__ float vn[BN][D + 1];
+  const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN, tid = threadIdx.x;
+  const int64_t hb = (int64_t)b * hk + hd;
+  const float* mean = vstat + hb * 3 * D;
+  const float* inv = mean + 2 * D;
+  for (int i = tid; i < BN * D / 4; i += 256) {
+    const int r = i / (D / 4), c0 = (i % (D / 4)) * 4, tk = tile * BN + r;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (tk < t) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(v + b * sb + hd * sh + (int64_t)tk * st + c0);
+      x[0] = (bf16f(raw.x & 0xffffu) - mean[c0]) * inv[c0];
+      x[1] = (bf16f(raw.x >> 16) - mean[c0 + 1]) * inv[c0 + 1];
+      x[2] = (bf16f(raw.y & 0xffffu) - mean[c0 + 2]) * inv[c0 + 2];
+      x[3] = (bf16f(raw.y >> 16) - mean[c0 + 3]) * inv[c0 + 3];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vn[r][c0 + j] = x[j];
+  }
+  __syncthreads();
+  const int64_t rec = hb * tiles + tile;
+  if (v16 != nullptr) {
+    uint8_t* out = v16 + rec * V16_BYTES;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int s = tid + it * 256, F = s >> 6, L = s & 63, kh = F & 1, kb = (F >> 1) & 1, cb = F >> 2;
+      const int ch = cb * 32 + (L & 31), g = L >> 5;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const int k0 = kb * 32 + 8 * (2 * kh + e / 4) + 4 * g + e % 4;
+        w[e / 2] = (uint32_t)f32_to_f16_bits(vn[k0][ch]) | ((uint32_t)f32_to_f16_bits(vn[k0 + 1][ch]) << 16);
+      }
+      *reinterpret_cast<uint4*>(out + F * 1024 + L * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  if (v8 == nullptr && v4 == nullptr) return;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int s = tid + it * 256, F = s >> 6, L = s & 63, kb = F & 1, cb = F >> 1;
+    const int ch = cb * 32 + (L & 31), g = L >> 5;
+    uint32_t b8[4] = {0, 0, 0, 0}, b4[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const float x = vn[kb * 32 + 8 * (p / 4) + 4 * g + p % 4][ch];
+      const int q8 = max(-127, min(127, (int)__builtin_rintf(x)));
+      const int q4 = max(-7, min(7, (int)__builtin_rintf(x * (7.f / 127.f))));
+      b8[p / 4] |= ((uint32_t)q8 & 0xffu) << (8 * (p % 4));
+      b4[p / 4] |= ((uint32_t)q4 & 0xfu) << (8 * (p % 4));
+    }
+    if (v8 != nullptr) *reinterpret_cast<uint4*>(v8 + rec * V8_BYTES + F * 1024 + L * 16) = make_uint4(b8[0], b8[1], b8[2], b8[3]);
+    if (v4 != nullptr)
+      *reinterpret_cast<uint2*>(v4 + rec * V4_BYTES + F * 512 + L * 8) =
+          make_uint2(b4[0] | (b4[1] << 4), b4[2] | (b4[3] << 4));
+  }
+}
+
+}  // namespace tri

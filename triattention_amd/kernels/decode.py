@@ -1,0 +1,186 @@
+"""Decode cache: the quantized prompt records that survive each q-head's band,
+compacted per KV head, plus a bf16 tail for the generated tokens.
+
+Mirrors triattention/kernels/decode.py (codes :17-22, store :24-67,
+__call__ :69-80, advance/stored :82-86).  The metadata rules are the
+reference's: per tile and q-head a state 8 / 4 / 0 from the band, the K
+precision of a (KV head, tile) is the maximum over its GQA group, each q-head
+attends only its own kept tiles (rowmask), and the V format is INT8 for the
+sink tile and the last NEAR_V8 tiles, INT4 elsewhere.
+
+Extension: batches.  One ``store`` holds the B sequences of one Prefill call;
+with ``ragged = True`` successive ``store`` calls for a layer append their
+sequences (e.g. one Prefill per prompt of a different length), and the decode
+op then serves the whole ragged batch in one launch.
+"""
+from __future__ import annotations
+
+import torch
+
+from .prefill import I4, I8
+
+WORDS = {I8: 2048, I4: 1024}
+K8_WORDS, K4_WORDS = 2048, 1024
+NEAR_V8 = 16
+
+
+def tile_states(bands: torch.Tensor, tiles: int) -> torch.Tensor:
+    """state[h, j]: 8 (INT8 K), 4 (INT4 K) or 0 (skipped) for q-head h, tile j (decode.py:27-30)."""
+    b = torch.as_tensor(bands, dtype=torch.int64).cpu().view(-1, 2)
+    j = torch.arange(tiles)
+    w8, w4, d = b[:, :1], b[:, 1:], (tiles - 1) - j[None, :]
+    return torch.where((j[None, :] == 0) | (d < w8), 8, torch.where(d < w4, 4, 0))
+
+
+def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor):
+    """Kept-tile lists and slots of one sequence (host, int64), as decode.py:27-53."""
+    state = tile_states(bands, tiles)
+    hq = state.shape[0]
+    state = state.view(hk, hq // hk, tiles)
+    kv = state.amax(1)
+    rowmask = ((state > 0).to(torch.int64) << torch.arange(state.shape[1])[None, :, None]).sum(1)
+    count = (kv > 0).sum(1)
+    maxn = max(1, int(count.max()))
+    order = torch.argsort((kv == 0).to(torch.int8), dim=1, stable=True)[:, :maxn]
+    valid = torch.arange(maxn)[None, :] < count[:, None]
+    kprec = kv.gather(1, order)
+    is4 = (kprec == 4) & valid
+    is8 = (kprec == 8) & valid
+    rows = torch.arange(hk)[:, None] * tiles + order
+    ragged = lambda select: torch.cumsum(select.flatten(), 0).view(hk, maxn) - 1
+    kslot = torch.where(is4, ragged(is4), torch.where(is8, ragged(is8), 0))
+    kbase = torch.where(valid, (rowmask.gather(1, order) & 0xFF) | (is4.to(torch.int64) << 8), 0)
+    vcode = vcodes[order]
+    vslot = torch.zeros((hk, maxn), dtype=torch.int64)
+    vsel = {}
+    for code in (I8, I4):
+        select = valid & (vcode == code)
+        vslot = torch.where(select, ragged(select), vslot)
+        vsel[code] = select
+    return dict(count=count, maxn=maxn, order=order, valid=valid, is4=is4, is8=is8, rows=rows, kslot=kslot,
+                kbase=kbase, vslot=vslot, vcode=vcode, vsel=vsel)
+
+
+class DecodeCache:
+    def __init__(self, module, max_tail=256):
+        self.module, self.max_tail = module, max_tail
+        self.layers, self.formats, self.step = {}, {}, None
+        self.ragged = False
+        self.out_dtype = None
+
+    def codes(self, rows):
+        if rows not in self.formats:
+            j = torch.arange(rows)
+            codes = torch.where((rows - 1 - j < NEAR_V8) | (j == 0), I8, I4)
+            self.formats[rows] = codes, frozenset(codes.unique().tolist())
+        return self.formats[rows]
+
+    def store(self, layer, prompt, kp, ka, kstat, vstat, packed, codes, bands, k4, ka4):
+        tiles = (prompt + 63) // 64
+        batch = vstat.shape[0]
+        hk, device = vstat.shape[1], ka.device
+        meta = sequence_metadata(bands, tiles, hk, codes)
+        # record indices of every sequence of the batch, sequence-major
+        seq = torch.arange(batch)[:, None] * (hk * tiles)
+        pick = lambda select: (seq + meta["rows"][select][None, :]).flatten().to(device)
+        group = dict(prompt=prompt, batch=batch, hk=hk, tiles=tiles, meta=meta,
+                     n8=int(meta["is8"].sum()), n4=int(meta["is4"].sum()),
+                     nv={code: int(meta["vsel"][code].sum()) for code in (I8, I4)},
+                     fmt=codes.to(torch.int64),
+                     k8=kp.view(batch * hk * tiles, K8_WORDS).index_select(0, pick(meta["is8"])),
+                     k4=(k4.view(batch * hk * tiles, K4_WORDS).index_select(0, pick(meta["is4"]))
+                         if bool(meta["is4"].any()) else None),
+                     v={code: (packed[code].view(batch * hk * tiles, WORDS[code]).index_select(0, pick(meta["vsel"][code]))
+                               if bool(meta["vsel"][code].any()) else None) for code in (I8, I4)},
+                     ka=ka.view(batch, hk, tiles, 4), ka4=ka4.view(batch, hk, tiles, 4) if ka4 is not None else None,
+                     kstat=kstat.view(batch, hk, 3, 128), vstat=vstat.view(batch, hk, 3, 128))
+        if self.step is None:
+            self.step = torch.zeros(1, dtype=torch.int64, device=device)
+        self.step.zero_()
+        entry = self.layers.get(layer)
+        groups = entry["groups"] + [group] if (self.ragged and entry is not None) else [group]
+        self.layers[layer] = self._assemble(groups, device)
+
+    def _assemble(self, groups, device):
+        """Batched metadata and concatenated records over every stored sequence."""
+        hk = groups[0]["hk"]
+        total = sum(g["batch"] for g in groups)
+        tiles_max = max(g["tiles"] for g in groups)
+        maxn = max(g["meta"]["maxn"] for g in groups)
+        entry = torch.zeros((total, hk, maxn), dtype=torch.int64)
+        kinfo = torch.zeros_like(entry)
+        slot = torch.zeros_like(entry)
+        count = torch.zeros((total, hk), dtype=torch.int64)
+        fmt = torch.ones((total, tiles_max), dtype=torch.int64)
+        prompt = torch.zeros(total, dtype=torch.int64)
+        has4 = any(g["k4"] is not None for g in groups)
+        ka = torch.ones((total, hk, tiles_max, 4), dtype=torch.float32, device=device)
+        ka4 = torch.ones_like(ka) if has4 else None
+        kstat = torch.empty((total, hk, 3, 128), dtype=torch.float32, device=device)
+        vstat = torch.empty_like(kstat)
+        k8s, k4s, v8s, v4s = [], [], [], []
+        o8 = o4 = ov8 = ov4 = 0
+        row = 0
+        for g in groups:
+            m, n, b = g["meta"], g["meta"]["maxn"], g["batch"]
+            for s in range(b):
+                r = row + s
+                entry[r, :, :n] = torch.where(m["valid"], m["order"], 0)
+                ks = torch.where(m["is4"], m["kslot"] + o4 + s * g["n4"], m["kslot"] + o8 + s * g["n8"])
+                kinfo[r, :, :n] = torch.where(m["valid"], m["kbase"] | (ks << 9), 0)
+                vs = torch.where(m["vcode"] == I4, m["vslot"] + ov4 + s * g["nv"][I4], m["vslot"] + ov8 + s * g["nv"][I8])
+                slot[r, :, :n] = torch.where(m["valid"], vs, 0)
+                count[r] = m["count"]
+                fmt[r, :g["tiles"]] = g["fmt"] - 1
+                prompt[r] = g["prompt"]
+            ka[row:row + b, :, :g["tiles"]] = g["ka"]
+            if g["ka4"] is not None:
+                ka4[row:row + b, :, :g["tiles"]] = g["ka4"]
+            kstat[row:row + b] = g["kstat"]
+            vstat[row:row + b] = g["vstat"]
+            k8s.append(g["k8"])
+            if g["k4"] is not None:
+                k4s.append(g["k4"])
+            if g["v"][I8] is not None:
+                v8s.append(g["v"][I8])
+            if g["v"][I4] is not None:
+                v4s.append(g["v"][I4])
+            o8 += b * g["n8"]
+            o4 += b * g["n4"]
+            ov8 += b * g["nv"][I8]
+            ov4 += b * g["nv"][I4]
+            row += b
+        cat = lambda parts, words: (torch.cat(parts) if parts else
+                                    torch.zeros((1, words), dtype=torch.uint32, device=device))
+        cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
+            torch.cuda.get_device_properties(device).multi_processor_count
+        wave = cus * max(1, self.module.decode_occupancy())
+        per = max(1, -(-int(count.sum()) // wave))
+        to = lambda x: x.to(torch.int32).to(device)
+        tail_k = torch.zeros((total, hk, self.max_tail, 128), dtype=torch.bfloat16, device=device)
+        return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, fmt=to(fmt), slot=to(slot), entry=to(entry),
+                    kinfo=to(kinfo), count=to(count), k8=cat(k8s, K8_WORDS), k4=cat(k4s, K4_WORDS) if has4 else None,
+                    ka=ka, ka4=ka4, kstat=kstat, vstat=vstat, v={I8: cat(v8s, WORDS[I8]), I4: cat(v4s, WORDS[I4])},
+                    tail_k=tail_k, tail_v=torch.zeros_like(tail_k), batch=total, tiles_max=tiles_max)
+
+    def __call__(self, layer, q, k, v, scale):
+        e = self.layers[layer]
+        hq = q.shape[1]
+        splits = max(1, -(-e["maxn"] // e["per"]))
+        key = ("partials", hq)
+        if key not in e:
+            n = e["batch"] * hq * splits
+            e[key] = (torch.empty(n, device=q.device), torch.empty(n, device=q.device),
+                      torch.empty(n * 128, device=q.device))
+        dtype = self.out_dtype or q.dtype
+        out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        self.module.decode(q, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"],
+                           e["slot"], e["v"][I8], e["v"][I4], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], k, v,
+                           self.step, out, *e[key], e["prompt"], e["per"], scale)
+        return out
+
+    def advance(self):
+        self.step.add_(1)
+
+    def stored(self, layer):
+        return layer in self.layers

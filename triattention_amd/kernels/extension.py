@@ -1,0 +1,228 @@
+"""Loader and torch-facing binding of the gfx950 kernel library.
+
+Replaces triattention/kernels/extension.py (which JIT-built the CUDA sources
+with nvcc).  Here the kernels are prebuilt in-tree by ``build()`` into
+``triattention_amd/_lib/libtriattention_amd.so`` (hipcc, gfx950) and loaded with
+ctypes.  ``load_extension()`` returns a module object whose five ops keep the
+names, argument order and in-place semantics of the reference's pybind module
+(cuda/common_host.cuh:96-102); tensors are handed to the C ABI
+(include/triattention_amd.h) as device pointers with sizes and strides, and
+every op runs on the current torch stream.  Argument errors raise
+RuntimeError, as TORCH_CHECK did in the reference.
+
+Extensions over the reference signatures (batch = 1 is exactly the reference):
+  * a leading batch dimension on every tensor;
+  * ``attention`` also accepts an fp32 ``out`` (parity testing);
+  * ``decode`` takes ragged batches: ``prompt`` may be a device int32 tensor of
+    per-sequence lengths, with per-sequence metadata rows.
+"""
+from __future__ import annotations
+
+import ctypes
+import functools
+import subprocess
+from pathlib import Path
+
+import torch
+
+PACKAGE = Path(__file__).resolve().parent.parent
+CSRC = PACKAGE / "csrc"
+LIBRARY = PACKAGE / "_lib" / "libtriattention_amd.so"
+D = 128
+STAT_BLOCKS = 64
+K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
+
+EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_decode",
+           "tri_decode_occupancy", "tri_device_cus")
+
+
+def build(arch: str = "gfx950") -> Path:
+    """Compile every HIP kernel of the package into the in-tree shared library."""
+    subprocess.run(["make", "-s", "-C", str(CSRC), f"ARCH={arch}"], check=True)
+    return LIBRARY
+
+
+def load_library() -> ctypes.CDLL:
+    """dlopen the kernel library and declare its C ABI (no GPU needed)."""
+    if not LIBRARY.exists():
+        raise RuntimeError(f"TriAttention kernel library missing: {LIBRARY} (run triattention_amd.kernels.extension.build())")
+    lib = ctypes.CDLL(str(LIBRARY))
+    P, I, I64, D_ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
+    lib.tri_last_error.restype = ctypes.c_char_p
+    lib.tri_last_error.argtypes = []
+    lib.tri_prepare_qk.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I,
+                                   P, P, P, P, P, P, P, P, P, P, P]
+    lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P]
+    lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_, P]
+    lib.tri_decode.argtypes = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
+                               P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, D_, P]
+    lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
+    lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
+    for name in EXPORTS:
+        if name != "tri_last_error":
+            getattr(lib, name).restype = ctypes.c_int
+    return lib
+
+
+def arch() -> str:
+    if not torch.cuda.is_available():
+        raise RuntimeError("TriAttention requires an AMD Instinct GPU (ROCm); none is visible.")
+    name = torch.cuda.get_device_properties(0).gcnArchName.split(":")[0]
+    if name != "gfx950":
+        raise RuntimeError(f"TriAttention kernels are built for gfx950 (MI355X); found {name}.")
+    return name
+
+
+def _check(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError(message)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+class Module:
+    """The op set of the reference's extension module, on the gfx950 kernels."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self.lib = lib
+
+    def _call(self, fn, *args):
+        if fn(*args) != 0:
+            raise RuntimeError(self.lib.tri_last_error().decode())
+
+    @staticmethod
+    def _stream(device) -> ctypes.c_void_p:
+        return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+    # -------------------------------------------------------------- prepare_qk
+    def prepare_qk(self, q, k, q8, qa, kp, ka, partial, kstat, q4=None, qa4=None, k4p=None, ka4=None):
+        """Per-token INT8 (and INT4) Q and centred per-block INT8 (and INT4) K operands."""
+        _check(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(3) == D and q.stride(3) == 1 and
+               k.dtype == torch.bfloat16 and k.dim() == 4 and k.size(0) == q.size(0) and k.size(2) == q.size(2) and
+               k.size(3) == D and k.stride(3) == 1, "BF16 Q/K [B,H,T,128] with contiguous features")
+        b, hq, t, _ = q.shape
+        hk = k.size(1)
+        tiles = (t + 63) // 64
+        _check(q8.numel() == b * hq * t * D and qa.numel() == b * hq * t and kp.numel() == b * hk * tiles * K8_WORDS and
+               ka.numel() == b * hk * tiles * 4 and partial.numel() >= b * hk * STAT_BLOCKS * 3 * D and
+               kstat.numel() == b * hk * 3 * D, "Q/K buffers")
+        int4 = q4 is not None
+        _check(int4 == (qa4 is not None) == (k4p is not None) == (ka4 is not None) and
+               (not int4 or (q4.numel() == b * hq * t * D // 2 and qa4.numel() == b * hq * t and
+                             k4p.numel() == b * hk * tiles * K4_WORDS and ka4.numel() == b * hk * tiles * 4)),
+               "INT4 Q/K buffers (all or none)")
+        with torch.cuda.device(q.device):
+            self._call(self.lib.tri_prepare_qk, _ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
+                       k.stride(1), k.stride(2), b, hq, hk, t, _ptr(q8), _ptr(qa), _ptr(kp), _ptr(ka), _ptr(partial),
+                       _ptr(kstat), _ptr(q4), _ptr(qa4), _ptr(k4p), _ptr(ka4), self._stream(q.device))
+
+    # ------------------------------------------------------------------ pack_v
+    def pack_v(self, v, partial, vstat, v16p=None, v8p=None, v4p=None):
+        """Normalised BF16 V' into FP16/INT8/INT4 PV operands."""
+        _check(v.is_cuda and v.dtype == torch.bfloat16 and v.dim() == 4 and v.size(3) == D and v.stride(3) == 1,
+               "BF16 V [B,Hkv,T,128]")
+        b, hk, t, _ = v.shape
+        tiles = (t + 63) // 64
+        _check(partial.numel() >= b * hk * STAT_BLOCKS * 3 * D and vstat.numel() == b * hk * 3 * D,
+               "V statistics buffers")
+        for x, words in ((v16p, V16_WORDS), (v8p, V8_WORDS), (v4p, V4_WORDS)):
+            _check(x is None or (x.dtype == torch.uint32 and x.is_contiguous() and x.numel() == b * hk * tiles * words),
+                   "packed V size")
+        with torch.cuda.device(v.device):
+            self._call(self.lib.tri_pack_v, _ptr(v), v.stride(0), v.stride(1), v.stride(2), b, hk, t, _ptr(partial),
+                       _ptr(vstat), _ptr(v16p), _ptr(v8p), _ptr(v4p), self._stream(v.device))
+
+    # --------------------------------------------------------------- attention
+    def attention(self, order, bands, groups, entries, v16p, v8p, v4p, vstat, q8, k8p, qa8, ka8, q4, k4p, qa4, ka4,
+                  out, scale):
+        """Banded causal attention: per key tile skip / INT8 QK x FP16 or INT8 PV / INT4 QK x INT8 PV."""
+        _check(q8.dtype == torch.int8 and q8.dim() == 4 and q8.size(3) == D and q8.is_contiguous(), "Q8 [B,Hq,T,128]")
+        b, h, t, _ = q8.shape
+        hk = vstat.numel() // (b * 3 * D)
+        tiles = (t + 63) // 64
+        _check(tiles <= 2048, "at most 131072 tokens")
+        _check(hk > 0 and h % hk == 0 and order.dtype == torch.int32 and order.numel() == h * tiles, "CTA order")
+        _check(groups is None and entries is None,
+               "task-table attention (groups/entries) is not provided; pass bands [Hq,2]")
+        _check(bands is not None and bands.dtype == torch.int32 and bands.is_contiguous() and bands.numel() == h * 2,
+               "bands [Hq,2] or task tables")
+        _check((q4 is None) == (k4p is None) == (qa4 is None) == (ka4 is None), "INT4 Q/K operands (all or none)")
+        _check(v16p is not None and v16p.numel() == b * hk * tiles * V16_WORDS, "packed V16")
+        _check(v8p is not None or (q4 is None and _only_f16(bands, tiles)), "packed V8 required by INT8/INT4 bands")
+        _check(out.dim() == 4 and tuple(out.shape) == (b, h, t, D) and out.stride(3) == 1 and
+               out.dtype in (torch.float32, torch.bfloat16, torch.float16), "output [B,Hq,T,128]")
+        dt = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
+        with torch.cuda.device(q8.device):
+            self._call(self.lib.tri_attention, _ptr(order), order.numel(), _ptr(bands), b, h, hk, t, _ptr(v16p),
+                       _ptr(v8p), _ptr(vstat), _ptr(q8), _ptr(k8p), _ptr(qa8), _ptr(ka8), _ptr(q4), _ptr(k4p),
+                       _ptr(qa4), _ptr(ka4), _ptr(out), dt, out.stride(0), out.stride(1), out.stride(2),
+                       float(scale), self._stream(q8.device))
+        return out
+
+    # ------------------------------------------------------------------ decode
+    def decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, kcur,
+               vcur, step, out, pm, pl, po, prompt, per, scale):
+        """Single-token decode over the quantized cache plus the bf16 tail."""
+        _check(q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(2) == 1 and q.size(3) == D and q.stride(3) == 1,
+               "q [B,Hq,1,128]")
+        b, hq = q.size(0), q.size(1)
+        hk = kstat.numel() // (b * 3 * D)
+        max_tail = ktail.size(2)
+        maxn = entry.size(-1)
+        _check(hk > 0 and hq % hk == 0 and hq // hk <= 8 and max_tail <= 1024, "decode geometry")
+        if isinstance(prompt, torch.Tensor):
+            prompt_t = prompt
+        else:
+            prompt_t = torch.full((b,), int(prompt), dtype=torch.int32, device=q.device)
+        tiles_max = fmt.numel() // b
+        splits = max(1, -(-maxn // int(per)))
+        _check(step.dtype == torch.int64 and step.is_cuda and kcur.stride(3) == 1 and
+               entry.dtype == torch.int32 and kinfo.dtype == torch.int32 and count.dtype == torch.int32 and
+               slot.dtype == torch.int32 and fmt.dtype == torch.int32 and prompt_t.dtype == torch.int32 and
+               entry.numel() == b * hk * maxn and kinfo.numel() == entry.numel() and slot.numel() == entry.numel() and
+               count.numel() == b * hk and ka.numel() == b * hk * tiles_max * 4 and
+               k8c.dim() == 2 and k8c.size(1) == K8_WORDS and v8.dim() == 2 and v8.size(1) == V8_WORDS and
+               v4.dim() == 2 and v4.size(1) == V4_WORDS and (k4c is None) == (ka4 is None) and
+               (k4c is None or (k4c.dim() == 2 and k4c.size(1) == K4_WORDS and ka4.numel() == ka.numel())) and
+               pm.numel() >= b * hq * splits and po.numel() >= b * hq * splits * D and
+               out.dtype in (torch.bfloat16, torch.float32) and out.stride(3) == 1,
+               "decode geometry/buffers")
+        kc = kcur.view(b, hk, -1, D) if kcur.dim() == 4 else kcur
+        with torch.cuda.device(q.device):
+            self._call(self.lib.tri_decode, _ptr(q), q.stride(0), q.stride(1), _ptr(k8c), _ptr(k4c), _ptr(ka),
+                       _ptr(ka4), _ptr(entry), _ptr(kinfo), _ptr(count), _ptr(fmt), _ptr(slot), _ptr(v8), _ptr(v4),
+                       _ptr(vstat), _ptr(kstat), _ptr(ktail), _ptr(vtail), ktail.stride(0), ktail.stride(1),
+                       ktail.stride(2), max_tail, _ptr(kc), _ptr(vcur), kc.stride(0), kc.stride(1), _ptr(step),
+                       _ptr(out), 0 if out.dtype == torch.float32 else 1, out.stride(0), out.stride(1), _ptr(pm),
+                       _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, float(scale),
+                       self._stream(q.device))
+        return out
+
+    def decode_occupancy(self) -> int:
+        """Resident decode workgroups per compute unit."""
+        n = ctypes.c_int(0)
+        self._call(self.lib.tri_decode_occupancy, ctypes.byref(n))
+        return int(n.value)
+
+    def device_cus(self) -> int:
+        n = ctypes.c_int(0)
+        self._call(self.lib.tri_device_cus, ctypes.byref(n))
+        return int(n.value)
+
+
+def _only_f16(bands, tiles: int) -> bool:
+    b = bands.detach().to("cpu", torch.int64).view(-1, 2)
+    qb = torch.arange(tiles)[None, :]
+    w8, w4 = b[:, :1], b[:, 1:]
+    n8 = (qb - torch.clamp(qb - w8 + 1, min=1)).clamp(min=0)
+    n4 = (qb - w8 - torch.clamp(qb - w4 + 1, min=1) + 1).clamp(min=0)
+    return not bool((n8 > 0).any() or (n4 > 0).any())
+
+
+@functools.cache
+def load_extension() -> Module:
+    """The gfx950 op module; raises RuntimeError without a gfx950 GPU or without the built library."""
+    arch()
+    return Module(load_library())

@@ -1,0 +1,257 @@
+"""Benchmark of the quantized attention path on one MI355X.
+
+Headline ("C1"): one decode step of 32 sequences,
+Llama-3.2-3B attention shape (24 q-heads / 8 KV heads, head_dim 128), prompt
+4096 held in the quantized cache, 25% INT8 / 75% INT4 KV heads, one new bf16
+token per sequence.  ``value`` = algorithmic HBM bytes of the step / step time
+(GB/s); the step is the split-KV decode kernel plus the merge kernel, inputs
+resident in HBM.  Also reported: tokens/s, the decode kernel's roofline
+(HIP events around that kernel inside the timed region), the CPU oracle timed
+on a bounded sample, and prefill attention TOPS on configs[0] (C0).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+K8, K4, V8, V4 = 8192, 4096, 8192, 4096
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_record_bytes(cache_entry):
+    """Algorithmic record bytes of one decode step: for every kept (sequence, KV head, tile),
+    its K record (8 or 4 KiB), its V record (8 or 4 KiB) and 16 B of group scales."""
+    import torch
+    e = cache_entry
+    kinfo = e["kinfo"].cpu().to(torch.int64)
+    count = e["count"].cpu().to(torch.int64)
+    entry = e["entry"].cpu().to(torch.int64)
+    fmt = e["fmt"].cpu().to(torch.int64)
+    b, hk, maxn = kinfo.shape
+    valid = torch.arange(maxn)[None, None, :] < count[:, :, None]
+    is4 = ((kinfo >> 8) & 1).bool()
+    kbytes = torch.where(is4, K4, K8)
+    vf = torch.gather(fmt[:, None, :].expand(b, hk, fmt.shape[1]), 2, entry)
+    vbytes = torch.where(vf == 1, V8, V4)
+    return int(((kbytes + vbytes + 16) * valid).sum()), int(valid.sum())
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-seqs", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from triattention_amd import synthetic as S
+    from triattention_amd.kernels.decode import DecodeCache
+    from triattention_amd.kernels.extension import load_extension
+    from triattention_amd.kernels.prefill import Prefill
+    from triattention_amd.maps import from_bands
+
+    module = load_extension()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+
+    # ------------------------------------------------------------------ C1 setup
+    log("generating C1 inputs (32 x 4096 tokens)")
+    c1 = S.config1()
+    batch, hq, hk, prompt = len(c1["seqs"]), 24, 8, c1["prompt"]
+    q = torch.cat([s["q"] for s in c1["seqs"]]).to(dev)
+    k = torch.cat([s["k"] for s in c1["seqs"]]).to(dev)
+    v = torch.cat([s["v"] for s in c1["seqs"]]).to(dev)
+    bands = c1["bands"]
+    scale = c1["scale"]
+    total_steps = args.warmup + args.steps + 1
+    cache = DecodeCache(module, max_tail=256)
+    pre = Prefill(module, from_bands({"0": bands.tolist()}), cache)
+    pre(0, q, k, v, scale)
+    torch.cuda.synchronize()
+    del q, k, v
+    e = cache.layers[0]
+    rec_bytes, kept_tiles = decode_record_bytes(e)
+    g = S.gen(4242)
+    toks = [(S.outlier_tensor(g, batch, hq, 1).to(dev), S.outlier_tensor(g, batch, hk, 1).to(dev),
+             S.outlier_tensor(g, batch, hk, 1).to(dev)) for _ in range(total_steps)]
+    log(f"cache: {kept_tiles} kept tiles, {rec_bytes} record bytes/step, per={e['per']}, maxn={e['maxn']}")
+
+    # step 0 output, kept for the parity spot check against the oracle
+    out0 = cache(0, *toks[0], scale).float().cpu()
+    cache.advance()
+
+    splits = max(1, -(-e["maxn"] // e["per"]))
+    n = batch * hq * splits
+    partials = e[("partials", hq)]
+    out = torch.empty((batch, hq, 1, 128), dtype=torch.bfloat16, device=dev)
+
+    def step(i, ev=None):
+        qd, kd, vd = toks[i]
+        argsd = (qd, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"], e["slot"],
+                 e["v"][2], e["v"][3], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], kd, vd, cache.step, out,
+                 *partials, e["prompt"], e["per"], scale)
+        if ev is None:
+            module.decode(*argsd)
+        else:
+            ev[0].record(stream)
+            module.decode(*argsd, phase=1)
+            ev[1].record(stream)
+            module.decode(*argsd, phase=2)
+            ev[2].record(stream)
+        cache.advance()
+
+    log(f"warmup {args.warmup} steps")
+    for i in range(1, 1 + args.warmup):
+        step(i)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    step0 = int(cache.step.item())
+    start.record(stream)
+    for i in range(args.steps):
+        step(1 + args.warmup + i, evs[i])
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    dec_ms = statistics.fmean(ev[0].elapsed_time(ev[1]) for ev in evs)
+    merge_ms = statistics.fmean(ev[1].elapsed_time(ev[2]) for ev in evs)
+    # small algorithmic bytes of a step: q and out (bf16), K mean and V mean/scale per (seq, KV head),
+    # and the bf16 K/V tail read by the merge (mean tail length over the timed steps)
+    mean_tail = min(256, step0 + (args.steps + 1) / 2)
+    small = batch * hq * 256 * 2 + batch * hk * (3 * 128 * 4) + batch * hk * 2 * 256 * mean_tail
+    step_bytes = rec_bytes + small
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = rec_bytes / (dec_ms * 1e-3) / 1e9
+    log(f"decode step {ms_per_step * 1e3:.1f} us (split kernel {dec_ms * 1e3:.1f} us, merge {merge_ms * 1e3:.1f} us)")
+
+    result = {
+        "metric": "prefill int8 TOPS (% MFMA peak); decode KV GB/s (% HBM peak); tokens/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8/int4 codes, fp32 softmax",
+        "data": "synthetic (seeded N(0,1) K/V with 4 outlier channels x20 per head, bf16)",
+        "config": {"workload": "C1 decode: batch 32, Hq 24 / Hk 8, head_dim 128, prompt 4096 in the quantized "
+                               "cache, 25% INT8 / 75% INT4 KV heads, one bf16 token per sequence",
+                   "global_batch": batch, "seq_len": prompt, "parallelism": "single GPU"},
+        "tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
+        "step_bytes": int(step_bytes),
+        "roofline": {"bound": "hbm", "kernel": "decode_kernel", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes": rec_bytes, "avg_us": round(dec_ms * 1e3, 2)},
+        "merge_us": round(merge_ms * 1e3, 2),
+    }
+
+    # ------------------------------------------------------------- CPU baseline
+    if not args.no_cpu:
+        import oracle as O
+        ns = min(args.cpu_seqs, batch)
+        log(f"CPU oracle: codes for {ns} sequences")
+        qd, kd, vd = toks[0]
+        sample = []
+        for b in range(ns):
+            s = c1["seqs"][b]
+            codes = O.prefill_codes(S.bits(s["q"][0]), S.bits(s["k"][0]), S.bits(s["v"][0]), bands.numpy(),
+                                    decode_cache=True)
+            sample.append(codes)
+        zeros = np.zeros((hk, 256, 128), np.uint16)
+        qb, kb, vb = qd.cpu(), kd.cpu(), vd.cpu()
+        times, errs = [], []
+        for rep in range(3):
+            t0 = time.perf_counter()
+            outs = [O.decode(sample[b], bands.numpy(), S.bits(qb[b, :, 0]), prompt, e["per"], scale, zeros, zeros,
+                             S.bits(kb[b, :, 0]), S.bits(vb[b, :, 0]), 0) for b in range(ns)]
+            times.append(time.perf_counter() - t0)
+        for b in range(ns):
+            # GPU step-0 output is bf16; compare within one bf16 ulp of the rounded oracle value
+            ref = torch.from_numpy(outs[b]).to(torch.bfloat16).float()
+            errs.append(float((out0[b, :, 0] - ref).abs().max()))
+        per_seq = statistics.median(times) / ns
+        cpu_step = per_seq * batch
+        result["cpu_baseline"] = {
+            "value": round(step_bytes / cpu_step / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle decode (C, 1 thread) of {ns} of the {batch} sequences at step 0, median of 3, "
+                      f"scaled to the full step",
+            "ms_per_step": round(cpu_step * 1e3, 2), "tokens_per_s": round(batch / cpu_step, 2),
+            "host_cpu_count": os.cpu_count()}
+        result["parity_spot_check"] = {"sequences": ns, "max_abs_vs_oracle_bf16": max(errs)}
+
+    # ----------------------------------------------------------------- prefill
+    if not args.no_prefill:
+        log("prefill C0")
+        c0 = S.config0()
+        q0, k0, v0 = c0["q"].to(dev), c0["k"].to(dev), c0["v"].to(dev)
+        pre0 = Prefill(module, from_bands({"0": c0["bands"].tolist()}))
+        pre0(0, q0, k0, v0, c0["scale"])
+        ops = next(iter(pre0.views.values()))
+        table = next(iter(pre0.tables.values()))
+        out0p = torch.empty((1, 1024, 24, 128), dtype=torch.bfloat16, device=dev).transpose(1, 2)
+        pk = ops["packed"]
+
+        def attn():
+            module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
+                             ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], out0p,
+                             c0["scale"])
+
+        for _ in range(3):
+            attn()
+        reps = 20
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a0.record(stream)
+        for _ in range(reps):
+            attn()
+        a1.record(stream)
+        torch.cuda.synchronize()
+        att_ms = a0.elapsed_time(a1) / reps
+        ops_c0 = 24 * 4 * 128 * (1024 * 1025 // 2)
+        w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0.record(stream)
+        for _ in range(reps):
+            pre0(0, q0, k0, v0, c0["scale"])
+        w1.record(stream)
+        torch.cuda.synchronize()
+        full_ms = w0.elapsed_time(w1) / reps
+        result["prefill"] = {"workload": "C0 prefill: batch 1, Hq 24 / Hk 8, T 1024, 50/50 INT8/INT4 KV heads",
+                             "attention_us": round(att_ms * 1e3, 2), "prefill_call_us": round(full_ms * 1e3, 2),
+                             "algorithmic_ops": ops_c0, "int8_tops": round(ops_c0 / (att_ms * 1e-3) / 1e12, 2),
+                             "frac_int8_peak": round(ops_c0 / (att_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+                             "tokens_per_s": round(1024 / (full_ms * 1e-3), 1)}
+
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -80,6 +80,27 @@ int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const
                const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max, double scale,
                void* stream);
 
+/* The two launches of tri_decode separately, same arguments: the split-KV
+ * kernel (writes pm/pl/po) and the merge with the bf16 tail (writes out and
+ * appends kcur/vcur to the tail).  No reference counterpart; they let a caller
+ * time or schedule the two kernels individually. */
+int tri_decode_partials(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c,
+                        const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
+                        const int32_t* count, const int32_t* fmt, const int32_t* slot, const void* v8c,
+                        const void* v4c, const float* vstat, const float* kstat, void* ktail, void* vtail,
+                        int64_t t_sb, int64_t t_sh, int64_t t_st, int max_tail, const void* kcur, const void* vcur,
+                        int64_t c_sb, int64_t c_sh, const int64_t* step, void* out, int out_dtype, int64_t o_sb,
+                        int64_t o_sh, float* pm, float* pl, float* po, const int32_t* prompt, int batch, int hq,
+                        int hk, int maxn, int per, int tiles_max, double scale, void* stream);
+int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
+                     const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
+                     const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
+                     const float* kstat, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh, int64_t t_st,
+                     int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh,
+                     const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
+                     float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
+                     double scale, void* stream);
+
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */
 int tri_decode_occupancy(int* blocks);

@@ -139,14 +139,14 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
   return check_launch("attention");
 }
 
-int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
-               const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
-               const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
-               const float* kstat, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh, int64_t t_st,
-               int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh, const int64_t* step,
-               void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
-               const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max, double scale,
-               void* stream) {
+static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
+                       const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
+                       const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
+                       const float* kstat, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh, int64_t t_st,
+                       int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh,
+                       const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
+                       float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
+                       double scale, void* stream, int phase) {
   g_error.clear();
   if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
       !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
@@ -214,10 +214,27 @@ int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const
   mg.max_tail = max_tail;
   mg.sm_log2 = d.sm_log2;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  tri::decode_kernel<<<dim3(splits, hk, batch), 64, 0, s>>>(d);
-  tri::decode_merge_kernel<<<dim3(hq, batch), 256, 0, s>>>(mg);
+  if (phase & 1) tri::decode_kernel<<<dim3(splits, hk, batch), 64, 0, s>>>(d);
+  if (phase & 2) tri::decode_merge_kernel<<<dim3(hq, batch), 256, 0, s>>>(mg);
   return check_launch("decode");
 }
+
+#define TRI_DECODE_ARGS                                                                                      \
+  q, q_sb, q_sh, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8c, v4c, vstat, kstat, ktail, vtail, t_sb, t_sh, \
+      t_st, max_tail, kcur, vcur, c_sb, c_sh, step, out, out_dtype, o_sb, o_sh, pm, pl, po, prompt, batch, hq, hk,  \
+      maxn, per, tiles_max, scale, stream
+#define TRI_DECODE_PARAMS                                                                                          \
+  const void *q, int64_t q_sb, int64_t q_sh, const void *k8c, const void *k4c, const float *ka, const float *ka4,  \
+      const int32_t *entry, const int32_t *kinfo, const int32_t *count, const int32_t *fmt, const int32_t *slot,  \
+      const void *v8c, const void *v4c, const float *vstat, const float *kstat, void *ktail, void *vtail,          \
+      int64_t t_sb, int64_t t_sh, int64_t t_st, int max_tail, const void *kcur, const void *vcur, int64_t c_sb,    \
+      int64_t c_sh, const int64_t *step, void *out, int out_dtype, int64_t o_sb, int64_t o_sh, float *pm,          \
+      float *pl, float *po, const int32_t *prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,    \
+      double scale, void *stream
+
+int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
+int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }
+int tri_decode_merge(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 2); }
 
 int tri_decode_occupancy(int* blocks) {
   g_error.clear();

@@ -33,7 +33,7 @@ STAT_BLOCKS = 64
 K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_decode",
-           "tri_decode_occupancy", "tri_device_cus")
+           "tri_decode_partials", "tri_decode_merge", "tri_decode_occupancy", "tri_device_cus")
 
 
 def build(arch: str = "gfx950") -> Path:
@@ -54,8 +54,10 @@ def load_library() -> ctypes.CDLL:
                                    P, P, P, P, P, P, P, P, P, P, P]
     lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P]
     lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_, P]
-    lib.tri_decode.argtypes = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
-                               P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, D_, P]
+    decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
+                   P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, D_, P]
+    for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
+        getattr(lib, name).argtypes = decode_args
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:
@@ -163,8 +165,11 @@ class Module:
 
     # ------------------------------------------------------------------ decode
     def decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, kcur,
-               vcur, step, out, pm, pl, po, prompt, per, scale):
-        """Single-token decode over the quantized cache plus the bf16 tail."""
+               vcur, step, out, pm, pl, po, prompt, per, scale, phase=3):
+        """Single-token decode over the quantized cache plus the bf16 tail.
+
+        ``phase`` (extension): 3 runs both kernels, 1 only the split-KV kernel,
+        2 only the merge (for per-kernel timing)."""
         _check(q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(2) == 1 and q.size(3) == D and q.stride(3) == 1,
                "q [B,Hq,1,128]")
         b, hq = q.size(0), q.size(1)
@@ -191,7 +196,8 @@ class Module:
                "decode geometry/buffers")
         kc = kcur.view(b, hk, -1, D) if kcur.dim() == 4 else kcur
         with torch.cuda.device(q.device):
-            self._call(self.lib.tri_decode, _ptr(q), q.stride(0), q.stride(1), _ptr(k8c), _ptr(k4c), _ptr(ka),
+            fn = {3: self.lib.tri_decode, 1: self.lib.tri_decode_partials, 2: self.lib.tri_decode_merge}[phase]
+            self._call(fn, _ptr(q), q.stride(0), q.stride(1), _ptr(k8c), _ptr(k4c), _ptr(ka),
                        _ptr(ka4), _ptr(entry), _ptr(kinfo), _ptr(count), _ptr(fmt), _ptr(slot), _ptr(v8), _ptr(v4),
                        _ptr(vstat), _ptr(kstat), _ptr(ktail), _ptr(vtail), ktail.stride(0), ktail.stride(1),
                        ktail.stride(2), max_tail, _ptr(kc), _ptr(vcur), kc.stride(0), kc.stride(1), _ptr(step),

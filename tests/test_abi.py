@@ -1,0 +1,44 @@
+"""The C-ABI library loads and exports every symbol include/triattention_amd.h declares (no GPU calls)."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+from triattention_amd.kernels.extension import EXPORTS, LIBRARY, load_library
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def header_symbols():
+    text = (ROOT / "include" / "triattention_amd.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+(tri_\w+)\(", text, re.M)))
+
+
+def test_library_exports_header_symbols():
+    lib = load_library()
+    syms = header_symbols()
+    assert len(syms) >= 8
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert set(syms) == set(EXPORTS)
+
+
+def test_validation_errors_need_no_gpu():
+    lib = load_library()
+    rc = lib.tri_prepare_qk(*([None] + [0] * 3 + [None] + [0] * 3 + [1, 1, 1, 1] + [None] * 11))
+    assert rc != 0 and b"null buffer" in lib.tri_last_error()
+    blocks = None
+    assert lib.tri_decode_occupancy(blocks) != 0 and b"null output" in lib.tri_last_error()
+
+
+def test_oracle_library_loads():
+    import oracle as O
+    assert O.lib().ora_texp2(ctypes.c_float(0.0)) == 1.0
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode == 2 and "one GPU" in r.stderr

@@ -1,0 +1,174 @@
+"""Host-side logic without a GPU: band table, decode metadata, maps, record codec."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from triattention_amd import maps
+from triattention_amd.kernels import records as R
+from triattention_amd.kernels.decode import DecodeCache, sequence_metadata, tile_states
+from triattention_amd.kernels.prefill import F16, I4, I8, Q4, BandTable
+from triattention_amd.synthetic import INF
+
+
+def test_band_table_order_and_formats():
+    bands = torch.tensor([[INF, INF], [1, INF], [2, 4], [3, 3], [1, 1], [2, INF]], dtype=torch.int32)
+    rows, hk = 7, 2
+    t = BandTable.build(bands, rows, hk, "cpu")
+    expect = [qh * rows + qb for kv in range(hk) for qb in reversed(range(rows)) for qh in range(kv * 3, kv * 3 + 3)]
+    assert t.order.tolist() == expect
+    assert t.formats == frozenset(O.formats_for(bands.numpy(), rows))
+    assert BandTable.build(torch.tensor([[INF, INF]] * 2, dtype=torch.int32), 2, 1, "cpu").formats == {F16}
+    assert BandTable.build(torch.tensor([[1, INF]] * 2, dtype=torch.int32), 3, 1, "cpu").formats == {F16, Q4}
+
+
+def brute_metadata(bands, tiles, hk, vcodes):
+    """Enumeration restatement of decode.py:27-53 for one sequence."""
+    hq = len(bands)
+    g = hq // hk
+    out = []
+    c8 = c4 = 0
+    v8 = v4 = 0
+    per_head = []
+    for kh in range(hk):
+        kept = []
+        for j in range(tiles):
+            st = [O.decode_state(*bands[kh * g + r], tiles, j) for r in range(g)]
+            if max(st) > 0:
+                kept.append((j, max(st), sum(1 << r for r in range(g) if st[r] > 0)))
+        per_head.append(kept)
+    for kh in range(hk):
+        rows = []
+        for j, kv, mask in per_head[kh]:
+            if kv == 4:
+                ks, c4 = c4, c4 + 1
+            else:
+                ks, c8 = c8, c8 + 1
+            if vcodes[j] == I8:
+                vs, v8 = v8, v8 + 1
+            else:
+                vs, v4 = v4, v4 + 1
+            rows.append((j, mask | ((kv == 4) << 8) | (ks << 9), vs))
+        out.append(rows)
+    return out
+
+
+@pytest.mark.parametrize("bands", [
+    [[INF, INF], [1, INF], [2, 4], [3, 3], [1, 1], [2, INF]],
+    [[2, 4], [2, 4], [2, 4], [1, 2], [1, 2], [1, 2]],
+    [[0, 0], [1, 1], [5, 5], [1, 3], [INF, INF], [2, 2]],
+])
+def test_decode_metadata_enumeration(bands):
+    tiles, hk = 5, 2
+    vcodes = torch.where((tiles - 1 - torch.arange(tiles) < 16) | (torch.arange(tiles) == 0), I8, I4)
+    vcodes = torch.tensor([I8, I4, I4, I8, I8])  # exercise both V formats
+    m = sequence_metadata(torch.tensor(bands), tiles, hk, vcodes)
+    ref = brute_metadata(bands, tiles, hk, vcodes.tolist())
+    for kh in range(hk):
+        n = int(m["count"][kh])
+        assert n == len(ref[kh])
+        for e, (j, kinfo, vs) in enumerate(ref[kh]):
+            assert int(m["order"][kh, e]) == j
+            assert int(m["kbase"][kh, e] | (m["kslot"][kh, e] << 9)) == kinfo
+            assert int(m["vslot"][kh, e]) == vs
+
+
+def test_tile_states_closed_form():
+    s = tile_states(torch.tensor([[2, 4], [INF, INF], [1, INF], [0, 0]]), 6)
+    assert s.tolist() == [[8, 0, 4, 4, 8, 8], [8] * 6, [8, 4, 4, 4, 4, 8], [8, 0, 0, 0, 0, 0]]
+
+
+class FakeModule:
+    def device_cus(self):
+        return 4
+
+    def decode_occupancy(self):
+        return 2
+
+
+def test_ragged_cache_assembly_slots_are_consistent():
+    cache = DecodeCache(FakeModule(), max_tail=8)
+    cache.ragged = True
+    hk, bands = 2, torch.tensor([[INF, INF], [1, INF], [2, 4], [1, 1]], dtype=torch.int32)
+    rng = torch.Generator().manual_seed(0)
+    seen = []
+    for prompt, batch in ((100, 2), (700, 1), (64, 3)):
+        tiles = (prompt + 63) // 64
+        kp = torch.randint(0, 2 ** 31, (batch * hk * tiles * 2048,), generator=rng).to(torch.uint32)
+        k4 = torch.randint(0, 2 ** 31, (batch * hk * tiles * 1024,), generator=rng).to(torch.uint32)
+        packed = {F16: None, I8: torch.randint(0, 2 ** 31, (batch * hk * tiles * 2048,), generator=rng).to(torch.uint32),
+                  I4: torch.randint(0, 2 ** 31, (batch * hk * tiles * 1024,), generator=rng).to(torch.uint32)}
+        ka = torch.rand(batch * hk * tiles * 4, generator=rng)
+        ka4 = torch.rand(batch * hk * tiles * 4, generator=rng)
+        stat = torch.rand(batch, hk, 3, 128, generator=rng)
+        codes, _ = cache.codes(tiles)
+        cache.store(0, prompt, kp, ka, stat.clone(), stat.clone(), packed, codes, bands, k4, ka4)
+        seen.append((prompt, batch, kp.view(batch, hk, tiles, 2048), k4.view(batch, hk, tiles, 1024),
+                     packed[I8].view(batch, hk, tiles, 2048), packed[I4].view(batch, hk, tiles, 1024)))
+    e = cache.layers[0]
+    assert e["batch"] == 6 and e["prompt"].tolist() == [100, 100, 700, 64, 64, 64]
+    # every kept entry points at the record of its own sequence, head and tile
+    row = 0
+    for prompt, batch, k8, k4, v8, v4 in seen:
+        for s in range(batch):
+            for kh in range(hk):
+                for n in range(int(e["count"][row, kh])):
+                    j = int(e["entry"][row, kh, n])
+                    info = int(e["kinfo"][row, kh, n])
+                    src, dst = (k4, e["k4"]) if (info >> 8) & 1 else (k8, e["k8"])
+                    assert torch.equal(dst[info >> 9], src[s, kh, j])
+                    vsrc, vdst = (v8, e["v"][I8]) if int(e["fmt"][row, j]) == 1 else (v4, e["v"][I4])
+                    assert torch.equal(vdst[int(e["slot"][row, kh, n])], vsrc[s, kh, j])
+            row += 1
+
+
+def test_maps_bundled_and_extension(tmp_path):
+    for name in maps.PRESETS.values():
+        data = json.loads((maps.DATA / f"{name}.json").read_text())
+        assert data["format"] == "triattention-map-v1"
+        fn = maps.load_map(maps.DATA / f"{name}.json")
+        b = fn(0, len(data["bands"]["0"]))
+        assert b.dtype == torch.int32 and b.shape[1] == 2 and fn.bf16(0) == []
+
+    class Cfg:
+        num_hidden_layers, num_attention_heads = 2, 3
+
+    class Model:
+        config = Cfg()
+
+    bands = {"0": [[1, 2]] * 3, "1": [[INF, INF]] * 3}
+    maps.from_bands(bands, Model())
+    with pytest.raises(ValueError):
+        maps.from_bands({"0": [[1, 2]] * 3}, Model())
+    p = tmp_path / "m.json"
+    maps.save_map(p, bands, bf16={1: [0]}, model_type="qwen2")
+    fn = maps.load_map(p)
+    assert fn(1, 3).tolist() == [[INF, INF]] * 3 and fn.bf16(1) == [0] and fn.bf16(0) == []
+    u = maps.uniform(4, 8)
+    assert u(0, 5).tolist() == [[4, 8]] * 5 and u.layer_independent
+
+
+def test_record_codec_round_trip_and_layout():
+    rng = np.random.default_rng(0)
+    codes = rng.integers(-127, 128, (3, 64, 128)).astype(np.int8)
+    assert np.array_equal(R.unpack_k8(R.pack_k8(codes)), codes)
+    assert np.array_equal(R.unpack_v8(R.pack_v8(codes)), codes)
+    c4 = rng.integers(-7, 8, (3, 64, 128)).astype(np.int8)
+    assert np.array_equal(R.unpack_k4(R.pack_k4(c4)), c4)
+    assert np.array_equal(R.unpack_v4(R.pack_v4(c4)), c4)
+    h = rng.integers(0, 65535, (2, 64, 128)).astype(np.uint16)
+    assert np.array_equal(R.unpack_v16(R.pack_v16(h)), h)
+    # layout pins: K8 byte of (key 37, feature 90); V8 byte of (key 13, channel 70)
+    rec = R.pack_k8(codes[:1]).reshape(-1)
+    kb, kk, ks, f = 1, 5, 2, 90 - 64
+    assert rec[(kb * 4 + ks) * 1024 + (kk + 32 * (f // 16)) * 16 + f % 16] == codes[0, 37, 90].view(np.uint8)
+    rec = R.pack_v8(codes[:1]).reshape(-1)
+    key, ch = 13, 70
+    kb, w = key // 32, key % 32
+    p = 4 * (w // 8) + w % 4
+    L = (ch % 32) + 32 * ((w % 8) // 4)
+    assert rec[((ch // 32) * 2 + kb) * 1024 + L * 16 + p] == codes[0, 13, 70].view(np.uint8)

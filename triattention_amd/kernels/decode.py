@@ -134,7 +134,7 @@ class DecodeCache:
                 fmt[r, :g["tiles"]] = g["fmt"] - 1
                 prompt[r] = g["prompt"]
             ka[row:row + b, :, :g["tiles"]] = g["ka"]
-            if g["ka4"] is not None:
+            if g["ka4"] is not None and ka4 is not None:
                 ka4[row:row + b, :, :g["tiles"]] = g["ka4"]
             kstat[row:row + b] = g["kstat"]
             vstat[row:row + b] = g["vstat"]

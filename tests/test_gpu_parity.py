@@ -112,3 +112,17 @@ def test_decode_bands_and_tail_overflow(module):
 def test_decode_short_prompt(module):
     bands = torch.tensor(MIXED, dtype=torch.int32)
     _decode_case(module, 40, bands, steps=2, seed=5200)
+
+
+@pytest.mark.parametrize("hq,hk", [(4, 4), (8, 2), (8, 1), (7, 1)])
+def test_decode_group_sizes(module, hq, hk):
+    g = hq // hk
+    kinds = [[INF, INF], [1, INF], [2, 5], [3, INF], [1, 1], [INF, INF], [1, INF], [2, 2]]
+    bands = torch.tensor([kinds[h % len(kinds)] for h in range(hq)], dtype=torch.int32)
+    _decode_case(module, 777, bands, batch=2, steps=2, max_tail=4, seed=5300 + g, hq=hq, hk=hk)
+
+
+def test_decode_long_tail(module):
+    """Twenty steps with a 24-slot tail: the merge's unrolled tail loops and the tail overwrite."""
+    bands = torch.tensor([[INF, INF], [1, INF], [2, 6], [1, INF], [INF, INF], [3, 3]], dtype=torch.int32)
+    _decode_case(module, 500, bands, batch=2, steps=20, max_tail=24, seed=5400)

@@ -146,7 +146,8 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh,
                        const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                        float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
-                       double scale, void* stream, int phase) {
+                       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, double scale, void* stream,
+                       int phase) {
   g_error.clear();
   if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
       !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
@@ -159,6 +160,10 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   if (!aligned(q, 8) || (q_sh % 4) || (q_sb % 4)) return fail("decode: q rows must be 8-byte aligned");
   if (!aligned(po, 16)) return fail("decode: po must be 16-byte aligned");
   const int splits = std::max(1, (maxn + per - 1) / per);
+  const int64_t lim = (int64_t)1 << 31;
+  if (n_k8 < 1 || n_v8 < 1 || n_v4 < 1 || n_k8 * tri::K8_BYTES >= lim || n_k4 * tri::K4_BYTES >= lim ||
+      n_v8 * tri::V8_BYTES >= lim || n_v4 * tri::V4_BYTES >= lim || (k4c != nullptr && n_k4 < 1))
+    return fail("decode: compacted record arrays must be non-empty and below 2 GiB each");
   tri::DecodeArgs d;
   d.q = static_cast<const uint16_t*>(q);
   d.k8c = static_cast<const uint8_t*>(k8c);
@@ -185,6 +190,10 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   d.tiles_max = tiles_max;
   d.splits = splits;
   d.sm_log2 = (float)(scale * 1.4426950408889634);
+  d.k8_bytes = (int)(n_k8 * tri::K8_BYTES);
+  d.k4_bytes = k4c ? (int)(n_k4 * tri::K4_BYTES) : 0;
+  d.v8_bytes = (int)(n_v8 * tri::V8_BYTES);
+  d.v4_bytes = (int)(n_v4 * tri::V4_BYTES);
   tri::MergeArgs mg;
   mg.pm = pm;
   mg.pl = pl;
@@ -214,7 +223,15 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   mg.max_tail = max_tail;
   mg.sm_log2 = d.sm_log2;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (phase & 1) tri::decode_kernel<<<dim3(splits, hk, batch), 64, 0, s>>>(d);
+  if (phase & 1) {
+    const dim3 grid(splits, hk, batch);
+    switch (std::min(hq / hk, 4)) {
+      case 1: tri::decode_kernel<1><<<grid, 64, 0, s>>>(d); break;
+      case 2: tri::decode_kernel<2><<<grid, 64, 0, s>>>(d); break;
+      case 3: tri::decode_kernel<3><<<grid, 64, 0, s>>>(d); break;
+      default: tri::decode_kernel<4><<<grid, 64, 0, s>>>(d); break;
+    }
+  }
   if (phase & 2) tri::decode_merge_kernel<<<dim3(hq, batch), 256, 0, s>>>(mg);
   return check_launch("decode");
 }
@@ -222,7 +239,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
 #define TRI_DECODE_ARGS                                                                                      \
   q, q_sb, q_sh, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8c, v4c, vstat, kstat, ktail, vtail, t_sb, t_sh, \
       t_st, max_tail, kcur, vcur, c_sb, c_sh, step, out, out_dtype, o_sb, o_sh, pm, pl, po, prompt, batch, hq, hk,  \
-      maxn, per, tiles_max, scale, stream
+      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, scale, stream
 #define TRI_DECODE_PARAMS                                                                                          \
   const void *q, int64_t q_sb, int64_t q_sh, const void *k8c, const void *k4c, const float *ka, const float *ka4,  \
       const int32_t *entry, const int32_t *kinfo, const int32_t *count, const int32_t *fmt, const int32_t *slot,  \
@@ -230,7 +247,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
       int64_t t_sb, int64_t t_sh, int64_t t_st, int max_tail, const void *kcur, const void *vcur, int64_t c_sb,    \
       int64_t c_sh, const int64_t *step, void *out, int out_dtype, int64_t o_sb, int64_t o_sh, float *pm,          \
       float *pl, float *po, const int32_t *prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,    \
-      double scale, void *stream
+      int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, double scale, void *stream
 
 int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
 int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }
@@ -240,7 +257,7 @@ int tri_decode_occupancy(int* blocks) {
   g_error.clear();
   if (!blocks) return fail("decode_occupancy: null output");
   int n = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, tri::decode_kernel, 64, 0);
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, tri::decode_kernel<4>, 64, 0);
   if (e != hipSuccess) return fail("decode_occupancy: %s", hipGetErrorString(e));
   *blocks = n;
   return 0;

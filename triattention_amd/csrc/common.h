@@ -38,6 +38,7 @@ constexpr int MAX_TILES = 2048;            // 131072 tokens (prefill_sm80.cu:23)
 constexpr int MAX_GROUP = 8;               // GQA group bound of the decode kernel
 constexpr int NEAR_V8 = 16;                // decode V recency window (decode.py:9)
 
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));

@@ -34,14 +34,24 @@ struct DecodeArgs {
   int64_t qsb, qsh;
   int hq, hk, maxn, per, tiles_max, splits;
   float sm_log2;
+  int k8_bytes, k4_bytes, v8_bytes, v4_bytes;  // sizes of the compacted record arrays (< 2^31)
 };
 
-__device__ __forceinline__ float dx32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
+constexpr int MAX_TAIL = 1024;
 
-__global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ v4i unpack16(v4i w) {
+  return v4i{(int)nib_lo16((uint32_t)w[0]), (int)nib_hi16((uint32_t)w[0]), (int)nib_lo16((uint32_t)w[1]),
+             (int)nib_hi16((uint32_t)w[1])};
+}
+
+template <int R, int W = (R == 1 ? 3 : 2)>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
   __shared__ __align__(16) int8_t q8s[MAX_GROUP][D];
   __shared__ __align__(16) int8_t q4s[MAX_GROUP][D];
   __shared__ float qsc[MAX_GROUP], qsc4[MAX_GROUP];
+  __shared__ __align__(16) uint8_t pls[MAX_GROUP][BN];
+  __shared__ __align__(16) float rsc[4][MAX_GROUP];  // alpha, base, bq, restore per row
+
   const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int L = threadIdx.x, lq = L & 31, half = L >> 5;
   const int g = a.hq / a.hk;
@@ -79,183 +89,248 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
       qsc4[r] = (r < g && mx > 0.f) ? mx / 7.f * a.sm_log2 : 1.17549435e-38f;
     }
   }
+  for (int i = L; i < MAX_GROUP * BN / 4; i += 64) reinterpret_cast<uint32_t*>(&pls[0][0])[i] = 0u;
   __syncthreads();
-  v4i qf8[4], qf4[4];
+
+  // rows of this lane: 4*half + r (r < R); the owner row of this lane's scalar work: 4*half + (L & 3)
+  const int orow = 4 * half + (L & 3);
+  const bool owner = (L & 3) < R;
+  float m_o = -3.402823466e38f;
+  float den[R], acc[4][R];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    v4i z = {0, 0, 0, 0};
-    qf8[ks] = lq < g ? *reinterpret_cast<const v4i*>(&q8s[lq][ks * 32 + 16 * half]) : z;
-    qf4[ks] = lq < g ? *reinterpret_cast<const v4i*>(&q4s[lq][ks * 32 + 16 * half]) : z;
+  for (int r = 0; r < R; ++r) {
+    den[r] = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[cb][r] = 0.f;
   }
-  const float qs8 = lq < g ? qsc[lq] : 1.17549435e-38f, qs4 = lq < g ? qsc4[lq] : 1.17549435e-38f;
-
-  v16f acc[4];
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[cb][r] = 0.f;
-  float m = -3.402823466e38f, den = 0.f;
   const int64_t mbase = hb * a.maxn;
-
-  for (int e = first; e < last; ++e) {
-    const int j = a.entry[mbase + e], info = a.kinfo[mbase + e];
-    const int is4 = (info >> 8) & 1, kslot = (int)((unsigned)info >> 9);
-    const unsigned rowmask = info & 0xff;
-    const int vs = a.slot[mbase + e], vf = a.fmt[(int64_t)b * a.tiles_max + j];
-    // ---- K fragments
-    v4i kf[8];
+  // Record streams are read through buffer descriptors (uniform base, 32-bit
+  // lane offsets); an out-of-range offset reads zeros instead of faulting.
+  const __amdgpu_buffer_rsrc_t rk8 = __builtin_amdgcn_make_buffer_rsrc((void*)a.k8c, (short)0, a.k8_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rk4 = __builtin_amdgcn_make_buffer_rsrc((void*)a.k4c, (short)0, a.k4_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv8 = __builtin_amdgcn_make_buffer_rsrc((void*)a.v8c, (short)0, a.v8_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv4 = __builtin_amdgcn_make_buffer_rsrc((void*)a.v4c, (short)0, a.v4_bytes, 0x00020000);
+  v4i kf[8], vf8[8];
+  float kav[2], kmax = 0.f;
+  // Scalar metadata of an entry; fetched two entries ahead of use so that the
+  // record loads never wait on it.
+  struct Meta {
+    int info, j, vs, vf;
+  };
+  auto fetch = [&](int e) {
+    Meta m;
+    m.info = a.kinfo[mbase + e];
+    m.j = a.entry[mbase + e];
+    m.vs = a.slot[mbase + e];
+    m.vf = a.fmt[(int64_t)b * a.tiles_max + m.j];
+    return m;
+  };
+  auto load_k = [&](const Meta& m) {
+    const int is4 = (m.info >> 8) & 1, kslot = (int)((unsigned)m.info >> 9);
+    const float4 k4s = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + m.j) * 4);
+    kmax = fmaxf(fmaxf(k4s.x, k4s.y), fmaxf(k4s.z, k4s.w));
+    kav[0] = (lq >> 4) ? k4s.y : k4s.x;
+    kav[1] = (lq >> 4) ? k4s.w : k4s.z;
     if (is4) {
-      const uint8_t* src = a.k4c + (int64_t)kslot * K4_BYTES + L * 8;
 #pragma unroll
       for (int F = 0; F < 8; ++F) {
-        const uint2 w = *reinterpret_cast<const uint2*>(src + F * 512);
-        kf[F] = v4i{(int)nib_lo16(w.x), (int)nib_hi16(w.x), (int)nib_lo16(w.y), (int)nib_hi16(w.y)};
+        const v2i w = __builtin_amdgcn_raw_buffer_load_b64(rk4, L * 8 + F * 512, kslot * K4_BYTES, 0);
+        kf[F] = v4i{w[0], w[1], 0, 0};
       }
     } else {
-      const uint8_t* src = a.k8c + (int64_t)kslot * K8_BYTES + L * 16;
 #pragma unroll
-      for (int F = 0; F < 8; ++F) kf[F] = *reinterpret_cast<const v4i*>(src + F * 1024);
+      for (int F = 0; F < 8; ++F) kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk8, L * 16 + F * 1024, kslot * K8_BYTES, 0);
     }
-    // ---- V fragments (V4 unpacked to 16*code)
-    v4i vfr[8];
-    if (vf == 1) {
-      const uint8_t* src = a.v8c + (int64_t)vs * V8_BYTES + L * 16;
+  };
+  auto load_v = [&](const Meta& m) {
+    if (m.vf == 1) {
 #pragma unroll
-      for (int F = 0; F < 8; ++F) vfr[F] = *reinterpret_cast<const v4i*>(src + F * 1024);
+      for (int F = 0; F < 8; ++F) vf8[F] = __builtin_amdgcn_raw_buffer_load_b128(rv8, L * 16 + F * 1024, m.vs * V8_BYTES, 0);
     } else {
-      const uint8_t* src = a.v4c + (int64_t)vs * V4_BYTES + L * 8;
 #pragma unroll
       for (int F = 0; F < 8; ++F) {
-        const uint2 w = *reinterpret_cast<const uint2*>(src + F * 512);
-        vfr[F] = v4i{(int)nib_lo16(w.x), (int)nib_hi16(w.x), (int)nib_lo16(w.y), (int)nib_hi16(w.y)};
+        const v2i w = __builtin_amdgcn_raw_buffer_load_b64(rv4, L * 8 + F * 512, m.vs * V4_BYTES, 0);
+        vf8[F] = v4i{w[0], w[1], 0, 0};
       }
     }
-    // ---- S^T
+  };
+
+  Meta mc = {0, 0, 0, 1}, mn = mc;
+  if (first < last) {
+    mc = fetch(first);
+    load_k(mc);
+    load_v(mc);
+    mn = first + 1 < last ? fetch(first + 1) : mc;
+  }
+  for (int e = first; e < last; ++e) {
+    const int info = mc.info;
+    const int is4 = (info >> 8) & 1;
+    const unsigned rowmask = info & 0xff;
+    const int j = mc.j;
+    const int vf = mc.vf;
+    const float cur_kmax = kmax;
+    // ---- S = Q K^T
+    v4i qa[4];
+    const int8_t* qsrc = is4 ? &q4s[0][0] : &q8s[0][0];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      v4i z = {0, 0, 0, 0};
+      qa[ks] = lq < MAX_GROUP ? *reinterpret_cast<const v4i*>(qsrc + lq * D + ks * 32 + 16 * half) : z;
+    }
     v16i s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) s[kb] = mfma_i8(kf[kb * 4 + ks], is4 ? qf4[ks] : qf8[ks], s[kb]);
-    const bool row_on = lq < g && ((rowmask >> lq) & 1u);
-    const float qs = is4 ? qs4 : qs8;
-    const float* kt = (is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4;
-    float slope[4];
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) slope[gi] = qs * kt[gi];
-    const float slope1 = qs * fmaxf(fmaxf(kt[0], kt[1]), fmaxf(kt[2], kt[3]));
-    int dot[2][16];
-    bool ok[2][16];
-    float tile = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int hg = 0; hg < 2; ++hg) {
-        bool have = false;
-        int mx = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int r = hg * 8 + i;
-          const int key = j * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int d = is4 ? (s[kb][r] >> 4) : s[kb][r];
-          dot[kb][r] = d;
-          ok[kb][r] = row_on && key < prompt;
-          if (ok[kb][r] && (!have || d > mx)) { mx = d; have = true; }
-        }
-        if (have) tile = fmaxf(tile, slope[kb * 2 + hg] * (float)mx);
-      }
-    tile = dx32_max(tile);
-    const float n = fmaxf(m, tile), alpha = texp2(m - n);
-    m = n;
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
+      for (int ks = 0; ks < 4; ++ks) s[kb] = mfma_i8(qa[ks], is4 ? unpack16(kf[kb * 4 + ks]) : kf[kb * 4 + ks], s[kb]);
     }
-    const float levels = vf == 1 ? 255.f : 15.f;
-    const bool any = tile > -__builtin_inff();
-    float base = any ? tile : n;
-    base += __builtin_fmaf(slope1, 0.75f, fabsf(base) * 2.4e-7f);
-    const float bq = any ? texp2(base - n) / levels : 0.f;
-    const float restore = vf == 1 ? bq : bq * (127.f / 7.f);
-    float c[4];
+    int dot[R][2];
 #pragma unroll
-    for (int gi = 0; gi < 4; ++gi) c[gi] = is4 ? -base : (-slope[gi] * MAGIC) - base;
-    uint32_t pw[2][4];
-    uint32_t rs = 0;
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) dot[r][kb] = is4 ? (s[kb][r] >> 4) : s[kb][r];
+    const float kv0 = kav[0], kv1 = kav[1];
+    if (e + 1 < last) load_k(mn);  // K registers are free again
+    const float kavc[2] = {kv0, kv1};
+    bool ok[R][2];
+    float slope[R][2], trow[R];
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        uint32_t y[4];
+    for (int r = 0; r < R; ++r) {
+      const int q = 4 * half + r;
+      const bool on = q < g && ((rowmask >> q) & 1u);
+      const float qs = is4 ? qsc4[q] : qsc[q];
+      trow[r] = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = qd * 4 + i, gi = kb * 2 + (r >> 3);
-          const int d = dot[kb][r];
-          float arg;
-          uint32_t dith;
-          if (ok[kb][r]) {
-            const float xm = __uint_as_float(MAGIC_BITS + (uint32_t)d);
-            arg = is4 ? __builtin_fmaf(slope[gi], (float)d, c[gi]) : __builtin_fmaf(slope[gi], xm, c[gi]);
-            dith = ((uint32_t)d & 0xffu) | 0x47400000u;
-          } else {
-            arg = -__builtin_inff();
-            dith = 0x47400000u;
-          }
-          y[i] = __float_as_uint(__builtin_fmaf(texp2(arg), levels, __uint_as_float(dith)));
-        }
-        const uint32_t w = pack_byte1(y[0], y[1], y[2], y[3]);
-        rs = __builtin_amdgcn_udot4(w, 0x01010101u, rs, false);
-        pw[kb][qd] = vf == 1 ? (w ^ 0x7f7f7f7fu) : w;
+      for (int kb = 0; kb < 2; ++kb) {
+        ok[r][kb] = on && (j * BN + kb * 32 + lq < prompt);
+        slope[r][kb] = qs * kavc[kb];
+        if (ok[r][kb]) trow[r] = fmaxf(trow[r], slope[r][kb] * (float)dot[r][kb]);
       }
-    rs += __shfl_xor(rs, 32, 64);
-    den = __builtin_fmaf((float)rs, bq, den * alpha);
-    const v4i b0 = {(int)pw[0][0], (int)pw[0][1], (int)pw[0][2], (int)pw[0][3]};
-    const v4i b1 = {(int)pw[1][0], (int)pw[1][1], (int)pw[1][2], (int)pw[1][3]};
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) trow[r] = fmaxf(trow[r], __shfl_xor(trow[r], o, 64));
+    }
+    // ---- per-row scalars on the owner lane (common_device.cuh:222-238)
+    const float levels = vf == 1 ? 255.f : 15.f;
+    {
+      float tile_o = -__builtin_inff();
+#pragma unroll
+      for (int r = 0; r < R; ++r) tile_o = (L & 3) == r ? trow[r] : tile_o;
+      const float qs_o = orow < g ? (is4 ? qsc4[orow] : qsc[orow]) : 1.17549435e-38f;
+      const float n = fmaxf(m_o, tile_o), alpha = texp2(m_o - n);
+      m_o = n;
+      const bool any = tile_o > -__builtin_inff();
+      float base = any ? tile_o : n;
+      base += __builtin_fmaf(qs_o * cur_kmax, 0.75f, fabsf(base) * 2.4e-7f);
+      const float bq = any ? texp2(base - n) / levels : 0.f;
+      const float restore = vf == 1 ? bq : bq * (127.f / 7.f);
+      if (lq < 4 && owner) {
+        rsc[0][orow] = alpha;
+        rsc[1][orow] = base;
+        rsc[2][orow] = bq;
+        rsc[3][orow] = restore;
+      }
+    }
+    __syncthreads();
+    float alpha[R], base[R], bq[R], restore[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      alpha[r] = rsc[0][4 * half + r];
+      base[r] = rsc[1][4 * half + r];
+      bq[r] = rsc[2][4 * half + r];
+      restore[r] = rsc[3][4 * half + r];
+    }
+    bool rescale = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) rescale |= alpha[r] != 1.f;
+    if (__any(rescale)) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        den[r] *= alpha[r];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[cb][r] *= alpha[r];
+      }
+    }
+    // ---- dithered P levels (common_device.cuh:239-246), transposed through LDS
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint32_t psum = 0;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int d = dot[r][kb];
+        float arg = -__builtin_inff();
+        uint32_t dith = 0x47400000u;
+        if (ok[r][kb]) {
+          const float c = is4 ? -base[r] : (-slope[r][kb] * MAGIC) - base[r];
+          arg = is4 ? __builtin_fmaf(slope[r][kb], (float)d, c)
+                    : __builtin_fmaf(slope[r][kb], __uint_as_float(MAGIC_BITS + (uint32_t)d), c);
+          dith |= (uint32_t)d & 0xffu;
+        }
+        const uint32_t y = __float_as_uint(__builtin_fmaf(texp2(arg), levels, __uint_as_float(dith)));
+        const uint32_t p = (y >> 8) & 0xffu;
+        psum += p;
+        pls[4 * half + r][kb * 32 + lq] = (uint8_t)p;
+      }
+      den[r] = __builtin_fmaf((float)psum, bq[r], den[r]);
+    }
+    __syncthreads();
+    // ---- O = P V
+    v4i pa[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      v4i w = {0, 0, 0, 0};
+      if (lq < MAX_GROUP) {
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) w[pp] = *reinterpret_cast<const int*>(&pls[lq][kb * 32 + 8 * pp + 4 * half]);
+      }
+      pa[kb] = w;
+    }
+    const Meta mnn = e + 2 < last ? fetch(e + 2) : mn;
     if (vf == 1) {
       const v4i neg127 = {(int)0x81818181u, (int)0x81818181u, (int)0x81818181u, (int)0x81818181u};
-      const float nr = -restore;
+      const v4i p0 = pa[0] ^ 0x7f7f7f7f, p1 = pa[1] ^ 0x7f7f7f7f;  // 127 - P as s8
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
         v16i d = {};
-        d = mfma_i8(vfr[cb * 2], neg127, d);
-        d = mfma_i8(vfr[cb * 2 + 1], neg127, d);
-        d = mfma_i8(vfr[cb * 2], b0, d);
-        d = mfma_i8(vfr[cb * 2 + 1], b1, d);  // = -sum P v
+        d = mfma_i8(neg127, vf8[cb * 2], d);
+        d = mfma_i8(neg127, vf8[cb * 2 + 1], d);
+        d = mfma_i8(p0, vf8[cb * 2], d);
+        d = mfma_i8(p1, vf8[cb * 2 + 1], d);  // = -sum_k P v
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[cb][r] = __builtin_fmaf((float)d[r], nr, acc[cb][r]);
+        for (int r = 0; r < R; ++r) acc[cb][r] = __builtin_fmaf((float)d[r], -restore[r], acc[cb][r]);
       }
     } else {
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
         v16i d = {};
-        d = mfma_i8(vfr[cb * 2], b0, d);
-        d = mfma_i8(vfr[cb * 2 + 1], b1, d);  // = 16 * sum P v
+        d = mfma_i8(pa[0], unpack16(vf8[cb * 2]), d);
+        d = mfma_i8(pa[1], unpack16(vf8[cb * 2 + 1]), d);  // = 16 * sum_k P v
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[cb][r] = __builtin_fmaf((float)(d[r] >> 4), restore, acc[cb][r]);
+        for (int r = 0; r < R; ++r) acc[cb][r] = __builtin_fmaf((float)(d[r] >> 4), restore[r], acc[cb][r]);
       }
     }
+    if (e + 1 < last) load_v(mn);  // V registers are free again
+    mc = mn;
+    mn = mnn;
   }
+
   // ---- split partials (common_device.cuh:355-370)
-  if (lq < g) {
-    const int64_t idx = ((int64_t)b * a.hq + kh * g + lq) * a.splits + split;
+
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int ch = cb * 32 + 8 * r4 + 4 * half;
-        *reinterpret_cast<float4*>(a.po + idx * D + ch) =
-            make_float4(acc[cb][r4 * 4], acc[cb][r4 * 4 + 1], acc[cb][r4 * 4 + 2], acc[cb][r4 * 4 + 3]);
-      }
-    if (half == 0) {
-      a.pm[idx] = m;
-      a.pl[idx] = den;
+    for (int o = 1; o < 32; o <<= 1) den[r] += __shfl_xor(den[r], o, 64);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int q = 4 * half + r;
+    if (q < g) {
+      const int64_t idx = ((int64_t)b * a.hq + kh * g + q) * a.splits + split;
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) a.po[idx * D + cb * 32 + lq] = acc[cb][r];
+      if (lq == 0) a.pl[idx] = den[r];
     }
   }
+  if (owner && lq < 4 && orow < g) a.pm[((int64_t)b * a.hq + kh * g + orow) * a.splits + split] = m_o;
 }
 
 struct MergeArgs {
@@ -276,8 +351,6 @@ struct MergeArgs {
   int hq, hk, splits, max_tail;
   float sm_log2;
 };
-
-constexpr int MAX_TAIL = 1024;
 
 // LSE merge of the split partials with the exact bf16 tail
 // (common_device.cuh:373-469).  One 256-thread workgroup per (sequence, q-head).
@@ -304,14 +377,32 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
     qv[i] = bf16f(a.q[b * a.qsb + hq * a.qsh + l32 * 4 + i]);
     kmu[i] = a.kstat[hb * 3 * D + l32 * 4 + i];
   }
-  for (int t = wave * 2 + sub; t < tail; t += 8) {
-    const uint16_t* kv = t < prior ? a.ktail + b * a.tsb + kh * a.tsh + (int64_t)t * a.tst : kc;
-    float part = 0.f;
+  // 8 half-waves x 8 tokens in flight per round
+  for (int t0 = (wave * 2 + sub) * 8; t0 < tail; t0 += 64) {
+    uint2 raw[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part = __builtin_fmaf(qv[i], bf16f(kv[l32 * 4 + i]) - kmu[i], part);
+    for (int u = 0; u < 8; ++u) {
+      const int t = min(t0 + u, tail - 1);
+      const uint16_t* kv = t < prior ? a.ktail + b * a.tsb + kh * a.tsh + (int64_t)t * a.tst : kc;
+      raw[u] = *reinterpret_cast<const uint2*>(kv + l32 * 4);
+    }
+    float part[8];
 #pragma unroll
-    for (int o = 16; o; o >>= 1) part += __shfl_xor(part, o, 32);
-    if (l32 == 0) ts[t] = part * a.sm_log2;
+    for (int u = 0; u < 8; ++u) {
+      const float kx[4] = {bf16f(raw[u].x & 0xffffu), bf16f(raw[u].x >> 16), bf16f(raw[u].y & 0xffffu),
+                           bf16f(raw[u].y >> 16)};
+      part[u] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[u] = __builtin_fmaf(qv[i], kx[i] - kmu[i], part[u]);
+    }
+#pragma unroll
+    for (int o = 16; o; o >>= 1)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) part[u] += __shfl_xor(part[u], o, 32);
+    if (l32 == 0)
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (t0 + u < tail) ts[t0 + u] = part[u] * a.sm_log2;
   }
   __syncthreads();
   const int64_t pbase = ((int64_t)b * a.hq + hq) * a.splits;
@@ -345,7 +436,19 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   }
   acc = __builtin_fmaf(acc, vscale[tid], total * vmean[tid]);
   const uint16_t* vt = a.vtail + b * a.tsb + kh * a.tsh + tid;
-  for (int t = 0; t < prior; ++t) {
+  int t = 0;
+  for (; t + 8 <= prior; t += 8) {
+    uint16_t vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) vv[u] = vt[(int64_t)(t + u) * a.tst];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float e = texp2(ts[t + u] - m);
+      total += e;
+      acc = __builtin_fmaf(e, bf16f(vv[u]), acc);
+    }
+  }
+  for (; t < prior; ++t) {
     const float e = texp2(ts[t] - m);
     total += e;
     acc = __builtin_fmaf(e, bf16f(vt[(int64_t)t * a.tst]), acc);

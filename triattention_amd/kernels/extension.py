@@ -55,7 +55,7 @@ def load_library() -> ctypes.CDLL:
     lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P]
     lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
-                   P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, D_, P]
+                   P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
         getattr(lib, name).argtypes = decode_args
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
@@ -202,7 +202,8 @@ class Module:
                        _ptr(vstat), _ptr(kstat), _ptr(ktail), _ptr(vtail), ktail.stride(0), ktail.stride(1),
                        ktail.stride(2), max_tail, _ptr(kc), _ptr(vcur), kc.stride(0), kc.stride(1), _ptr(step),
                        _ptr(out), 0 if out.dtype == torch.float32 else 1, out.stride(0), out.stride(1), _ptr(pm),
-                       _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, float(scale),
+                       _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, k8c.size(0),
+                       0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), float(scale),
                        self._stream(q.device))
         return out
 

@@ -206,45 +206,62 @@ def main():
 
     # ----------------------------------------------------------------- prefill
     if not args.no_prefill:
+        def prefill_case(name, cfg, reps):
+            q0, k0, v0 = cfg["q"].to(dev), cfg["k"].to(dev), cfg["v"].to(dev)
+            b, hq0, t, _ = q0.shape
+            hk0 = k0.shape[1]
+            bf16_kv = [h for h, kind in enumerate(cfg["kinds"]) if kind == "bf16"]
+            fn = from_bands({"0": cfg["bands"].tolist()}, bf16={"0": bf16_kv} if bf16_kv else None)
+            pre0 = Prefill(module, fn)
+            pre0(0, q0, k0, v0, cfg["scale"])
+            ops = next(iter(pre0.views.values()))
+            table = next(iter(pre0.tables.values()))
+            exact = pre0.exact(0, hq0, hk0, dev)
+            outp = torch.empty((b, t, hq0, 128), dtype=torch.bfloat16, device=dev).transpose(1, 2)
+            pk = ops["packed"]
+
+            def attn():
+                module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
+                                 ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], outp,
+                                 cfg["scale"], exact=exact, q=q0, k=k0, v=v0)
+
+            for _ in range(2):
+                attn()
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a0.record(stream)
+            for _ in range(reps):
+                attn()
+            a1.record(stream)
+            torch.cuda.synchronize()
+            att_ms = a0.elapsed_time(a1) / reps
+            w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            w0.record(stream)
+            for _ in range(reps):
+                pre0(0, q0, k0, v0, cfg["scale"])
+            w1.record(stream)
+            torch.cuda.synchronize()
+            full_ms = w0.elapsed_time(w1) / reps
+            # every head keeps all causal pairs here (INT8 / INT4 / bf16 bands skip no tiles)
+            ops_alg = b * hq0 * 4 * 128 * (t * (t + 1) // 2)
+            tops = ops_alg / (att_ms * 1e-3) / 1e12
+            log(f"prefill {name}: attention {att_ms * 1e3:.1f} us = {tops:.1f} int8-TOPS, full call {full_ms * 1e3:.1f} us")
+            return {"attention_us": round(att_ms * 1e3, 2), "prefill_call_us": round(full_ms * 1e3, 2),
+                    "algorithmic_ops": ops_alg, "int8_tops": round(tops, 2),
+                    "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                    "tokens_per_s": round(b * t / (full_ms * 1e-3), 1)}
+
         log("prefill C0")
         c0 = S.config0()
-        q0, k0, v0 = c0["q"].to(dev), c0["k"].to(dev), c0["v"].to(dev)
-        pre0 = Prefill(module, from_bands({"0": c0["bands"].tolist()}))
-        pre0(0, q0, k0, v0, c0["scale"])
-        ops = next(iter(pre0.views.values()))
-        table = next(iter(pre0.tables.values()))
-        out0p = torch.empty((1, 1024, 24, 128), dtype=torch.bfloat16, device=dev).transpose(1, 2)
-        pk = ops["packed"]
-
-        def attn():
-            module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
-                             ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], out0p,
-                             c0["scale"])
-
-        for _ in range(3):
-            attn()
-        reps = 20
-        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        a0.record(stream)
-        for _ in range(reps):
-            attn()
-        a1.record(stream)
-        torch.cuda.synchronize()
-        att_ms = a0.elapsed_time(a1) / reps
-        ops_c0 = 24 * 4 * 128 * (1024 * 1025 // 2)
-        w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        w0.record(stream)
-        for _ in range(reps):
-            pre0(0, q0, k0, v0, c0["scale"])
-        w1.record(stream)
-        torch.cuda.synchronize()
-        full_ms = w0.elapsed_time(w1) / reps
-        result["prefill"] = {"workload": "C0 prefill: batch 1, Hq 24 / Hk 8, T 1024, 50/50 INT8/INT4 KV heads",
-                             "attention_us": round(att_ms * 1e3, 2), "prefill_call_us": round(full_ms * 1e3, 2),
-                             "algorithmic_ops": ops_c0, "int8_tops": round(ops_c0 / (att_ms * 1e-3) / 1e12, 2),
-                             "frac_int8_peak": round(ops_c0 / (att_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
-                             "tokens_per_s": round(1024 / (full_ms * 1e-3), 1)}
+        c0["kinds"] = []
+        r0 = prefill_case("C0", c0, 20)
+        r0["workload"] = "C0 prefill: batch 1, Hq 24 / Hk 8, T 1024, 50/50 INT8/INT4 KV heads"
+        log("prefill C2 (generating 4 x 8192 tokens)")
+        c2 = S.config2()
+        r2 = prefill_case("C2", c2, 5)
+        r2["workload"] = (f"C2 prefill: batch 4, Hq 28 / Hk 4, T 8192, log-uniform channel scales, KV heads "
+                          f"{c2['kinds']}")
+        result["prefill"] = {"C0": r0, "C2": r2}
 
     print(json.dumps(result))
 

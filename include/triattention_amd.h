@@ -53,12 +53,18 @@ int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batc
  * bands int32 [hq][2] = (w8, w4) per q-head, shared by every sequence.
  * out: [batch][hq][t][128] with element strides (o_sb, o_sh, o_st), feature
  * stride 1; out_dtype 0 = fp32, 1 = bf16, 2 = fp16.  scale is the softmax
- * scale; sm_log2 = f32(scale * log2(e)) as in prefill_sm80.cu:538. */
+ * scale; sm_log2 = f32(scale * log2(e)) as in prefill_sm80.cu:538.
+ * exact: NULL, or int32 [hq] flags; a flagged q-head ignores its band and
+ * computes exact causal attention on the raw bf16 qr [batch][hq][t][128]
+ * (strides q_sb, q_sh, q_st) and kr/vr [batch][hk][t][128] (strides k_sb,
+ * k_sh, k_st; rows 16-byte aligned) with fp32 softmax and accumulation
+ * (extension for maps that keep some heads unquantized). */
 int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int batch, int hq, int hk, int t,
                   const void* v16p, const void* v8p, const float* vstat, const void* q8, const void* k8p,
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
-                  double scale, void* stream);
+                  double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                  const void* kr, const void* vr, int64_t k_sb, int64_t k_sh, int64_t k_st, void* stream);
 
 /* Replaces decode (common_host.cuh:47-87), batched and ragged.
  * q bf16 [batch][hq][1][128] (strides q_sb, q_sh); k8c/k4c/v8c/v4c compacted

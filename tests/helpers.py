@@ -15,14 +15,23 @@ from triattention_amd.synthetic import bits
 MAX_ABS, MEAN_ABS = 2e-3, 1e-3
 
 
-def bands_fn_of(bands: torch.Tensor):
+def bands_fn_of(bands: torch.Tensor, bf16_kv=None):
     table = {"0": bands.tolist()}
-    return from_bands(table)
+    return from_bands(table, bf16={"0": list(bf16_kv)} if bf16_kv else None)
 
 
-def run_prefill(module, q, k, v, bands, scale, decode_cache=None, out_dtype=torch.float32):
+def exact_reference(q, k, v, scale):
+    """Causal attention of [B,Hq,T,128] bf16 inputs in float64 on the CPU (torch SDPA math): the
+    mathematically exact result the bf16 heads are held to."""
+    g = q.shape[1] // k.shape[1]
+    kf = k.double().repeat_interleave(g, 1)
+    vf = v.double().repeat_interleave(g, 1)
+    return torch.nn.functional.scaled_dot_product_attention(q.double(), kf, vf, is_causal=True, scale=scale).numpy()
+
+
+def run_prefill(module, q, k, v, bands, scale, decode_cache=None, out_dtype=torch.float32, bf16_kv=None):
     """Prefill on the GPU through the host operator; returns (out cpu, operand views)."""
-    pre = Prefill(module, bands_fn_of(bands), decode_cache, out_dtype=out_dtype)
+    pre = Prefill(module, bands_fn_of(bands, bf16_kv), decode_cache, out_dtype=out_dtype)
     dev = torch.device("cuda")
     out = pre(0, q.to(dev), k.to(dev), v.to(dev), scale)
     torch.cuda.synchronize()

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close, compare_codes, oracle_prefill, run_prefill
+from helpers import assert_close, compare_codes, exact_reference, oracle_prefill, run_prefill
 from triattention_amd import synthetic as S
 from triattention_amd.kernels.decode import DecodeCache
 from triattention_amd.synthetic import INF, bits
@@ -126,3 +126,33 @@ def test_decode_long_tail(module):
     """Twenty steps with a 24-slot tail: the merge's unrolled tail loops and the tail overwrite."""
     bands = torch.tensor([[INF, INF], [1, INF], [2, 6], [1, INF], [INF, INF], [3, 3]], dtype=torch.int32)
     _decode_case(module, 500, bands, batch=2, steps=20, max_tail=24, seed=5400)
+
+
+@pytest.mark.parametrize("t", [37, 64, 333])
+def test_exact_bf16_heads_in_the_same_launch(module, t):
+    """KV head 1 kept bf16: its q-heads match fp32 attention on the raw operands, the others the oracle."""
+    print(f"\n[parity] exact bf16 heads t={t}", flush=True)
+    q, k, v = small(6000 + t, 2, 6, 3, t)
+    bands = torch.tensor([[INF, INF], [INF, INF], [1, INF], [1, INF], [2, 3], [2, 3]], dtype=torch.int32)
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5, bf16_kv=[1])
+    ref, codes = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    ex = exact_reference(q, k, v, 128 ** -0.5)
+    quant = [0, 1, 4, 5]
+    assert_close(out.numpy()[:, quant], ref[:, quant], what="quantized heads")
+    assert_close(out.numpy()[:, 2:4], ex[:, 2:4], what="exact heads")
+
+
+def test_config2_shape_slice(module):
+    """Config 2 recipe (Hq 28 / Hk 4, log-uniform channel scales, one bf16 KV head) at T = 1024, batch 1."""
+    print("\n[parity] config 2 slice (B1 T1024)", flush=True)
+    c = S.config2(batch=1, t=1024)
+    bf16_kv = [h for h, kind in enumerate(c["kinds"]) if kind == "bf16"]
+    out, ops, _ = run_prefill(module, c["q"], c["k"], c["v"], c["bands"], c["scale"], bf16_kv=bf16_kv)
+    ref, codes = oracle_prefill(c["q"], c["k"], c["v"], c["bands"], c["scale"])
+    ex = exact_reference(c["q"], c["k"], c["v"], c["scale"])
+    g = 7
+    exact_q = [h for h in range(28) if h // g in bf16_kv]
+    quant_q = [h for h in range(28) if h // g not in bf16_kv]
+    compare_codes(ops, codes[0], 0, 1, 28, 4, 1024)
+    assert_close(out.numpy()[:, quant_q], ref[:, quant_q], what="config 2 quantized heads")
+    assert_close(out.numpy()[:, exact_q], ex[:, exact_q], what="config 2 exact heads")

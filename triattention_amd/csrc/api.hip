@@ -94,7 +94,8 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
                   const void* v16p, const void* v8p, const float* vstat, const void* q8, const void* k8p,
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
-                  double scale, void* stream) {
+                  double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                  const void* kr, const void* vr, int64_t k_sb, int64_t k_sh, int64_t k_st, void* stream) {
   g_error.clear();
   const int tiles = (t + tri::BN - 1) / tri::BN;
   if (!order || !bands || !v16p || !vstat || !q8 || !k8p || !qa8 || !ka8 || !out)
@@ -111,7 +112,20 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
   if (!aligned(out, 16) || (o_st % 4) || (o_sh % 4) || (o_sb % 4))
     return fail("attention: output [B,Hq,T,128] must be 16-byte aligned with strides a multiple of 4");
   (void)esz;
+  if (exact != nullptr && (!qr || !kr || !vr || !aligned(qr, 16) || !aligned(kr, 16) || !aligned(vr, 16) ||
+                           (q_sb | q_sh | q_st | k_sb | k_sh | k_st) % 8 != 0))
+    return fail("attention: exact heads need 16-byte aligned bf16 q/k/v rows");
   tri::PrefillArgs a;
+  a.exact = exact;
+  a.qr = static_cast<const uint16_t*>(qr);
+  a.kr = static_cast<const uint16_t*>(kr);
+  a.vr = static_cast<const uint16_t*>(vr);
+  a.qsb = q_sb;
+  a.qsh = q_sh;
+  a.qst = q_st;
+  a.ksb = k_sb;
+  a.ksh = k_sh;
+  a.kst = k_st;
   a.order = order;
   a.bands = bands;
   a.v16 = static_cast<const uint8_t*>(v16p);

@@ -34,6 +34,12 @@ struct PrefillArgs {
   int64_t osb, osh, ost;
   int hq, hk, t;
   float sm_log2;
+  // exact (bf16) heads: exact[qh] != 0 selects exact causal attention on the raw bf16 operands
+  const int32_t* exact;
+  const uint16_t* qr;
+  const uint16_t* kr;
+  const uint16_t* vr;
+  int64_t qsb, qsh, qst, ksb, ksh, kst;  // raw q strides; raw k/v share the k strides
 };
 
 enum Kind { KF16 = 0, KI8 = 1, KQ4 = 2 };
@@ -227,12 +233,151 @@ __device__ __forceinline__ void prefill_pass(const PrefillArgs& a, PrefillState&
   }
 }
 
+// Exact attention of one (q-head, 64-row query tile) on the raw bf16 operands:
+// bf16 MFMA for QK^T (fp32 accumulation), fp32 online softmax in log2 units,
+// P split into bf16 high and low parts so that P V keeps ~2^-17 relative
+// precision, fp32 accumulation.  The reference's "exact" attention is
+// scaled_dot_product_attention over bf16 q/k/v (triattention/models.py:45-47).
+__device__ __forceinline__ v8bf load8bf(const uint16_t* p) {
+  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  return __builtin_bit_cast(v8bf, w);
+}
+
+__device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int qh, int qb, uint8_t* lds) {
+  const int g = a.hq / a.hk, kh = qh / g;
+  const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
+  const int qrow = qb * BN + wave * 32 + lq;
+  const bool row_ok = qrow < a.t;
+  uint16_t* vt = reinterpret_cast<uint16_t*>(lds);  // V tile transposed: [128 channels][64 keys] bf16
+  v8bf qf[8];
+  const uint16_t* qp = a.qr + b * a.qsb + qh * a.qsh + (int64_t)(row_ok ? qrow : 0) * a.qst;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    const uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * half) : z;
+    qf[ks] = __builtin_bit_cast(v8bf, w);
+  }
+  const uint16_t* kbase = a.kr + b * a.ksb + kh * a.ksh;
+  const uint16_t* vbase = a.vr + b * a.ksb + kh * a.ksh;
+  v16f acc[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[cb][r] = 0.f;
+  float m = -3.402823466e38f, den = 0.f;
+  for (int col = 0; col <= qb; ++col) {
+    // stage V transposed; pairs of keys per 32-bit LDS word
+    __syncthreads();
+    for (int i = tid; i < 32 * 16; i += 128) {
+      const int kp = i >> 4, c0 = (i & 15) * 8;  // key pair kp (keys 2kp, 2kp+1), channels c0..c0+7
+      const int k0 = col * BN + 2 * kp;
+      uint4 r0 = make_uint4(0, 0, 0, 0), r1 = r0;
+      if (k0 < a.t) r0 = *reinterpret_cast<const uint4*>(vbase + (int64_t)k0 * a.kst + c0);
+      if (k0 + 1 < a.t) r1 = *reinterpret_cast<const uint4*>(vbase + (int64_t)(k0 + 1) * a.kst + c0);
+      const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w}, w1[4] = {r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const uint32_t lo = (w0[h >> 1] >> (16 * (h & 1))) & 0xffffu, hi = (w1[h >> 1] >> (16 * (h & 1))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(vt + (c0 + h) * BN + 2 * kp) = lo | (hi << 16);
+      }
+    }
+    // S^T = K Q^T straight from the row-major K rows (16-byte slices)
+    v16f s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+      const int key = col * BN + kb * 32 + lq;
+      const uint16_t* kp = kbase + (int64_t)min(key, a.t - 1) * a.kst + 8 * half;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) s[kb] = mfma_bf16(load8bf(kp + ks * 16), qf[ks], s[kb]);
+    }
+    const bool masked = col == qb;
+    float tile = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        float x = s[kb][r] * a.sm_log2;
+        if (key >= a.t || (masked && key > qrow)) x = -__builtin_inff();
+        s[kb][r] = x;
+        tile = fmaxf(tile, x);
+      }
+    tile = fmaxf(tile, __shfl_xor(tile, 32, 64));
+    const float n = fmaxf(m, tile), alpha = __builtin_amdgcn_exp2f(m - n);
+    m = n;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
+    }
+    v8bf phi[2][2], plo[2][2];
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(s[kb][r] - n);
+        const __bf16 h = (__bf16)p;
+        const __bf16 l = (__bf16)(p - (float)h);
+        phi[kb][r >> 3][r & 7] = h;
+        plo[kb][r >> 3][r & 7] = l;
+        psum += p;
+      }
+    psum += __shfl_xor(psum, 32, 64);
+    den = __builtin_fmaf(den, alpha, psum);
+    __syncthreads();
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int kh2 = 0; kh2 < 2; ++kh2) {
+          // keys kb*32 + 8*(2*kh2 + e/4) + 4*half + e%4 of channel cb*32 + lq: two runs of four keys
+          const uint16_t* src = vt + (cb * 32 + lq) * BN + kb * 32 + 16 * kh2 + 4 * half;
+          const uint2 w0 = *reinterpret_cast<const uint2*>(src), w1 = *reinterpret_cast<const uint2*>(src + 8);
+          const v8bf vf = __builtin_bit_cast(v8bf, make_uint4(w0.x, w0.y, w1.x, w1.y));
+          acc[cb] = mfma_bf16(vf, phi[kb][kh2], acc[cb]);
+          acc[cb] = mfma_bf16(vf, plo[kb][kh2], acc[cb]);
+        }
+  }
+  if (!row_ok) return;
+  const float inv = 1.f / den;
+  const int64_t obase = b * a.osb + qh * a.osh + (int64_t)qrow * a.ost;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int ch = cb * 32 + 8 * r4 + 4 * half;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = acc[cb][r4 * 4 + i] * inv;
+      if (a.out_dtype == 0) {
+        *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + ch) = make_float4(v[0], v[1], v[2], v[3]);
+      } else if (a.out_dtype == 1) {
+        const uint32_t lo = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + ch) = make_uint2(lo, hi);
+      } else {
+        const uint32_t lo = f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
+        const uint32_t hi = f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + ch) = make_uint2(lo, hi);
+      }
+    }
+}
+
 __global__ __launch_bounds__(128) void prefill_kernel(PrefillArgs a) {
   __shared__ __align__(16) uint8_t k_lds[K8_BYTES];
   __shared__ __align__(16) uint8_t v_lds[V16_BYTES];
   const int rows = (a.t + BN - 1) / BN;
   const int task = a.order[blockIdx.x], b = blockIdx.y;
   const int qh = task / rows, qb = task % rows, g = a.hq / a.hk, kh = qh / g;
+  if (a.exact != nullptr && a.exact[qh]) {
+    prefill_exact(a, b, qh, qb, v_lds);
+    return;
+  }
   const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
   const int qrow = qb * BN + wave * 32 + lq;
   const bool row_ok = qrow < a.t;

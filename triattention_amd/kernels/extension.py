@@ -53,7 +53,8 @@ def load_library() -> ctypes.CDLL:
     lib.tri_prepare_qk.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I,
                                    P, P, P, P, P, P, P, P, P, P, P]
     lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P]
-    lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_, P]
+    lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_,
+                                  P, P, I64, I64, I64, P, P, I64, I64, I64, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
@@ -138,8 +139,12 @@ class Module:
 
     # --------------------------------------------------------------- attention
     def attention(self, order, bands, groups, entries, v16p, v8p, v4p, vstat, q8, k8p, qa8, ka8, q4, k4p, qa4, ka4,
-                  out, scale):
-        """Banded causal attention: per key tile skip / INT8 QK x FP16 or INT8 PV / INT4 QK x INT8 PV."""
+                  out, scale, exact=None, q=None, k=None, v=None):
+        """Banded causal attention: per key tile skip / INT8 QK x FP16 or INT8 PV / INT4 QK x INT8 PV.
+
+        Extension: ``exact`` (int32 [Hq] flags on the device) with the raw bf16
+        ``q`` [B,Hq,T,128] and ``k``/``v`` [B,Hk,T,128] computes the flagged
+        q-heads as exact causal attention on the unquantized operands."""
         _check(q8.dtype == torch.int8 and q8.dim() == 4 and q8.size(3) == D and q8.is_contiguous(), "Q8 [B,Hq,T,128]")
         b, h, t, _ = q8.shape
         hk = vstat.numel() // (b * 3 * D)
@@ -156,11 +161,21 @@ class Module:
         _check(out.dim() == 4 and tuple(out.shape) == (b, h, t, D) and out.stride(3) == 1 and
                out.dtype in (torch.float32, torch.bfloat16, torch.float16), "output [B,Hq,T,128]")
         dt = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
+        if exact is not None:
+            _check(exact.dtype == torch.int32 and exact.numel() == h and exact.is_cuda and
+                   q is not None and k is not None and v is not None and
+                   q.dtype == k.dtype == v.dtype == torch.bfloat16 and tuple(q.shape) == (b, h, t, D) and
+                   tuple(k.shape) == (b, hk, t, D) and k.shape == v.shape and k.stride() == v.stride() and
+                   q.stride(3) == 1 and k.stride(3) == 1, "exact heads: flags [Hq] and bf16 q/k/v")
+        qs = q.stride() if exact is not None else (0, 0, 0)
+        ks = k.stride() if exact is not None else (0, 0, 0)
         with torch.cuda.device(q8.device):
             self._call(self.lib.tri_attention, _ptr(order), order.numel(), _ptr(bands), b, h, hk, t, _ptr(v16p),
                        _ptr(v8p), _ptr(vstat), _ptr(q8), _ptr(k8p), _ptr(qa8), _ptr(ka8), _ptr(q4), _ptr(k4p),
                        _ptr(qa4), _ptr(ka4), _ptr(out), dt, out.stride(0), out.stride(1), out.stride(2),
-                       float(scale), self._stream(q8.device))
+                       float(scale), _ptr(exact), _ptr(q if exact is not None else None), qs[0], qs[1], qs[2],
+                       _ptr(k if exact is not None else None), _ptr(v if exact is not None else None),
+                       ks[0], ks[1], ks[2], self._stream(q8.device))
         return out
 
     # ------------------------------------------------------------------ decode

@@ -62,13 +62,31 @@ class Prefill:
 
     q [B, Hq, T, 128], k/v [B, Hk, T, 128] bf16 -> out [B, Hq, T, 128] with
     token-major strides (kernels/prefill.py:102).  ``out_dtype`` (an extension)
-    selects fp32 output for parity testing; the default is q's dtype.
+    selects fp32 output for parity testing; the default is q's dtype.  Maps
+    whose ``bands_fn.bf16(layer)`` lists KV heads (the map's optional "bf16"
+    key) get exact attention for those heads' q-heads in the same launch.
     """
 
     def __init__(self, module, bands_fn, decode_cache=None, out_dtype=None):
         self.module, self.bands_fn, self.decode_cache = module, bands_fn, decode_cache
         self.out_dtype = out_dtype
         self.tables, self.buffers, self.views, self.layer_buffers = {}, {}, {}, {}
+        self.exact_flags = {}
+
+    def exact(self, layer, heads, kv_heads, device):
+        """int32 [Hq] flags of the q-heads whose KV head the map keeps in bf16 (None if none)."""
+        bf16 = getattr(self.bands_fn, "bf16", None)
+        kv = list(bf16(layer)) if bf16 is not None else []
+        if not kv:
+            return None
+        key = (layer, heads, device)
+        if key not in self.exact_flags:
+            group = heads // kv_heads
+            flags = torch.zeros(heads, dtype=torch.int32)
+            for h in kv:
+                flags[h * group:(h + 1) * group] = 1
+            self.exact_flags[key] = flags.to(device)
+        return self.exact_flags[key]
 
     def table(self, layer, heads, kv_heads, rows, device):
         key = (None if getattr(self.bands_fn, "layer_independent", False) else layer, heads, rows)
@@ -139,8 +157,17 @@ class Prefill:
         self.module.pack_v(v, ops["partial"], vstat, packed[F16], packed[I8], packed[I4])
         dtype = self.out_dtype or q.dtype
         out = torch.empty((batch, t, hq, 128), dtype=dtype, device=device).transpose(1, 2)
-        self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
-                              ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out, scale)
+        exact = self.exact(layer, hq, hk, device)
+        if exact is None:
+            self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
+                                  ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
+                                  scale)
+        else:
+            if decode is not None:
+                raise NotImplementedError("decode caches for maps with bf16 heads")
+            self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
+                                  ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
+                                  scale, exact=exact, q=q, k=k, v=v)
         if decode is not None:
             self.decode_cache.store(layer, t, ops["kp"], ka, kstat, vstat, packed, decode[0], table.host,
                                     ops["k4"], ka4)

@@ -54,6 +54,8 @@ int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batc
  * out: [batch][hq][t][128] with element strides (o_sb, o_sh, o_st), feature
  * stride 1; out_dtype 0 = fp32, 1 = bf16, 2 = fp16.  scale is the softmax
  * scale; sm_log2 = f32(scale * log2(e)) as in prefill_sm80.cu:538.
+ * v16p/v8p/k8p/k4p records and ka8/ka4 scales must be 16-byte aligned; v8p
+ * must be set whenever a band has INT8 or INT4 key tiles (both use INT8 V).
  * exact: NULL, or int32 [hq] flags; a flagged q-head ignores its band and
  * computes exact causal attention on the raw bf16 qr [batch][hq][t][128]
  * (strides q_sb, q_sh, q_st) and kr/vr [batch][hk][t][128] (strides k_sb,

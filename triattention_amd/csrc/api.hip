@@ -108,10 +108,13 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
   if (int4 != (k4p != nullptr) || int4 != (qa4 != nullptr) || int4 != (ka4 != nullptr))
     return fail("attention: INT4 Q/K operands (all or none)");
   if (out_dtype < 0 || out_dtype > 2) return fail("attention: out dtype must be fp32, bf16 or fp16");
-  const int esz = out_dtype == 0 ? 4 : 2;
   if (!aligned(out, 16) || (o_st % 4) || (o_sh % 4) || (o_sb % 4))
     return fail("attention: output [B,Hq,T,128] must be 16-byte aligned with strides a multiple of 4");
-  (void)esz;
+  // records and per-tile K scales are copied to LDS in 16-byte pieces
+  if (!aligned(v16p, 16) || !aligned(k8p, 16) || !aligned(ka8, 16) || (v8p && !aligned(v8p, 16)) ||
+      (int4 && (!aligned(k4p, 16) || !aligned(ka4, 16))))
+    return fail("attention: record and K-scale buffers must be 16-byte aligned");
+  if (int4 && v8p == nullptr) return fail("attention: INT4 key tiles need the INT8 V records");
   if (exact != nullptr && (!qr || !kr || !vr || !aligned(qr, 16) || !aligned(kr, 16) || !aligned(vr, 16) ||
                            (q_sb | q_sh | q_st | k_sb | k_sh | k_st) % 8 != 0))
     return fail("attention: exact heads need 16-byte aligned bf16 q/k/v rows");

@@ -52,9 +52,21 @@ struct PrefillState {
 __device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
 
 template <int KIND>
+__device__ __forceinline__ v4i k_frag(const uint8_t* __restrict__ k_lds, int F, int L) {
+  if constexpr (KIND == KQ4) {
+    // packed 4-bit record in LDS: unpack this lane's 8 bytes to 16 bytes of 16*code
+    const uint2 w = *reinterpret_cast<const uint2*>(k_lds + F * 512 + L * 8);
+    return v4i{(int)nib_lo16(w.x), (int)nib_hi16(w.x), (int)nib_lo16(w.y), (int)nib_hi16(w.y)};
+  } else {
+    return *reinterpret_cast<const v4i*>(k_lds + F * 1024 + L * 16);
+  }
+}
+
+template <int KIND>
 __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState& st, const v4i (&qf)[4], float qs,
-                                             const float* __restrict__ ks, int col, bool masked, int qrow,
-                                             const uint8_t* __restrict__ k_lds, const uint8_t* __restrict__ v_lds) {
+                                             const float (&ks)[4], int col, bool masked, int qrow,
+                                             const uint8_t* __restrict__ k_lds, const uint8_t* __restrict__ v_lds,
+                                             const uint8_t* __restrict__ v_hi = nullptr) {
   const int L = threadIdx.x & 63, half = L >> 5;
   // ---- S^T = K Q^T over 128 features, two 32-key blocks
   v16i s[2];
@@ -66,21 +78,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
   for (int kstep = 0; kstep < 4; ++kstep)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-      s[kb] = mfma_i8(*reinterpret_cast<const v4i*>(k_lds + (kb * 4 + kstep) * 1024 + L * 16), qf[kstep], s[kb]);
+    for (int kb = 0; kb < 2; ++kb) s[kb] = mfma_i8(k_frag<KIND>(k_lds, kb * 4 + kstep, L), qf[kstep], s[kb]);
 
-  float x[2][16];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = KIND == KQ4 ? (float)s[kb][r] * 0.0625f : __int_as_float(s[kb][r]);
-      if (masked) {
-        const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (key > qrow || key >= a.t) v = -__builtin_inff();
-      }
-      x[kb][r] = v;
+  // score of accumulator r of block kb as a float: the magic float for 8-bit
+  // codes (1.5*2^23 + dot), the exact dot for 4-bit codes (MFMA gave 16*dot)
+  auto score = [&](int kb, int r) -> float {
+    float v = KIND == KQ4 ? (float)s[kb][r] * 0.0625f : __int_as_float(s[kb][r]);
+    if (masked) {
+      const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (key > qrow || key >= a.t) v = -__builtin_inff();
     }
+    return v;
+  };
 
   // ---- scaled row max (prefill_sm80.cu:244-253)
   float slope[4];
@@ -91,9 +100,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int hg = 0; hg < 2; ++hg) {
-      float mx = x[kb][hg * 8];
+      float mx = score(kb, hg * 8);
 #pragma unroll
-      for (int r = 1; r < 8; ++r) mx = fmaxf(mx, x[kb][hg * 8 + r]);
+      for (int r = 1; r < 8; ++r) mx = fmaxf(mx, score(kb, hg * 8 + r));
       if (mx > -__builtin_inff()) {
         const float d = KIND == KQ4 ? mx : mx - MAGIC;
         tile = fmaxf(tile, slope[kb * 2 + hg] * d);
@@ -123,7 +132,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int gi = kb * 2 + (r >> 3);
-        const _Float16 h = (_Float16)texp2(__builtin_fmaf(slope[gi], x[kb][r], c[gi]));
+        const _Float16 h = (_Float16)texp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
         p[kb][r >> 3][r & 7] = h;
         psum += (float)h;
       }
@@ -135,7 +144,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-          const v8h vf = *reinterpret_cast<const v8h*>(v_lds + ((cb * 2 + kb) * 2 + kh) * 1024 + L * 16);
+          // fp16 V record: fragments 0..7 in v_lds, 8..15 in v_hi
+          const int F = (cb * 2 + kb) * 2 + kh;
+          const v8h vf = *reinterpret_cast<const v8h*>((F < 8 ? v_lds : v_hi) + (F & 7) * 1024 + L * 16);
           st.acc[cb] = mfma_f16(vf, p[kb][kh], st.acc[cb]);
         }
   } else {
@@ -158,7 +169,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = qd * 4 + i, gi = kb * 2 + (r >> 3);
-          const float e = texp2(__builtin_fmaf(slope[gi], x[kb][r], c[gi]));
+          const float e = texp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
           y[i] = __float_as_uint(__builtin_fmaf(e, 255.f, PMAGIC_HALF));
         }
         const uint32_t w = pack_byte1(y[0], y[1], y[2], y[3]);
@@ -186,51 +197,19 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   }
 }
 
-// Global -> LDS staging of one key tile (K unpacked to 16*code bytes for INT4).
-template <int KIND>
-__device__ __forceinline__ void stage_tile(const PrefillArgs& a, int64_t rec, uint8_t* k_lds, uint8_t* v_lds) {
-  const int tid = threadIdx.x;
-  if constexpr (KIND == KQ4) {
-    const uint8_t* src = a.k4 + rec * K4_BYTES;
-#pragma unroll
-    for (int s = tid; s < 512; s += 128) {
-      const uint2 w = *reinterpret_cast<const uint2*>(src + s * 8);
-      *reinterpret_cast<uint4*>(k_lds + s * 16) = make_uint4(nib_lo16(w.x), nib_hi16(w.x), nib_lo16(w.y), nib_hi16(w.y));
-    }
-  } else {
-    const uint8_t* src = a.k8 + rec * K8_BYTES;
-#pragma unroll
-    for (int s = tid; s < 512; s += 128)
-      *reinterpret_cast<uint4*>(k_lds + s * 16) = *reinterpret_cast<const uint4*>(src + s * 16);
-  }
-  if constexpr (KIND == KF16) {
-    const uint8_t* src = a.v16 + rec * V16_BYTES;
-#pragma unroll
-    for (int s = tid; s < 1024; s += 128)
-      *reinterpret_cast<uint4*>(v_lds + s * 16) = *reinterpret_cast<const uint4*>(src + s * 16);
-  } else {
-    const uint8_t* src = a.v8 + rec * V8_BYTES;
-#pragma unroll
-    for (int s = tid; s < 512; s += 128)
-      *reinterpret_cast<uint4*>(v_lds + s * 16) = *reinterpret_cast<const uint4*>(src + s * 16);
-  }
+// Asynchronous global -> LDS copy of `bytes` (a multiple of 1 KiB) by the two
+// waves of the workgroup, 1 KiB per wave instruction (lane L's 16 bytes land
+// at dst + 16 L); completion is awaited with s_waitcnt + barrier.
+__device__ __forceinline__ void lds_copy_async(const uint8_t* src, uint8_t* dst, int bytes) {
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63;
+  for (int off = wave * 1024; off < bytes; off += 2048)
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + off + L * 16),
+                                     (__attribute__((address_space(3))) void*)(dst + off), 16, 0, 0);
 }
 
-template <int KIND>
-__device__ __forceinline__ void prefill_pass(const PrefillArgs& a, PrefillState& st, const v4i (&qf)[4], float qs,
-                                             const float* __restrict__ kscale, int64_t rec0, int first, int count,
-                                             int step, int qb, int qrow, uint8_t* k_lds, uint8_t* v_lds) {
-  for (int i = 0; i < count; ++i) {
-    const int col = first + i * step;
-    const bool masked = (i == count - 1) && col == qb;
-    __syncthreads();
-    stage_tile<KIND>(a, rec0 + col, k_lds, v_lds);
-    __syncthreads();
-    float ks[4];
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) ks[gi] = kscale[col * 4 + gi];
-    prefill_tile<KIND>(a, st, qf, qs, ks, col, masked, qrow, k_lds, v_lds);
-  }
+__device__ __forceinline__ void lds_wait() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
 }
 
 // Exact attention of one (q-head, 64-row query tile) on the raw bf16 operands:
@@ -243,12 +222,15 @@ __device__ __forceinline__ v8bf load8bf(const uint16_t* p) {
   return __builtin_bit_cast(v8bf, w);
 }
 
-__device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int qh, int qb, uint8_t* lds) {
+__device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int qh, int qb, uint8_t* lds_lo,
+                                              uint8_t* lds_hi) {
   const int g = a.hq / a.hk, kh = qh / g;
   const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
   const int qrow = qb * BN + wave * 32 + lq;
   const bool row_ok = qrow < a.t;
-  uint16_t* vt = reinterpret_cast<uint16_t*>(lds);  // V tile transposed: [128 channels][64 keys] bf16
+  // V tile transposed, [channel][64 keys] bf16: channels 0..63 in lds_lo, 64..127 in lds_hi
+  uint16_t* vt_lo = reinterpret_cast<uint16_t*>(lds_lo);
+  uint16_t* vt_hi = reinterpret_cast<uint16_t*>(lds_hi);
   v8bf qf[8];
   const uint16_t* qp = a.qr + b * a.qsb + qh * a.qsh + (int64_t)(row_ok ? qrow : 0) * a.qst;
 #pragma unroll
@@ -278,7 +260,8 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
 #pragma unroll
       for (int h = 0; h < 8; ++h) {
         const uint32_t lo = (w0[h >> 1] >> (16 * (h & 1))) & 0xffffu, hi = (w1[h >> 1] >> (16 * (h & 1))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(vt + (c0 + h) * BN + 2 * kp) = lo | (hi << 16);
+        const int c = c0 + h;
+        *reinterpret_cast<uint32_t*>((c < 64 ? vt_lo : vt_hi) + (c & 63) * BN + 2 * kp) = lo | (hi << 16);
       }
     }
     // S^T = K Q^T straight from the row-major K rows (16-byte slices)
@@ -336,7 +319,7 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
 #pragma unroll
         for (int kh2 = 0; kh2 < 2; ++kh2) {
           // keys kb*32 + 8*(2*kh2 + e/4) + 4*half + e%4 of channel cb*32 + lq: two runs of four keys
-          const uint16_t* src = vt + (cb * 32 + lq) * BN + kb * 32 + 16 * kh2 + 4 * half;
+          const uint16_t* src = (cb < 2 ? vt_lo : vt_hi) + ((cb & 1) * 32 + lq) * BN + kb * 32 + 16 * kh2 + 4 * half;
           const uint2 w0 = *reinterpret_cast<const uint2*>(src), w1 = *reinterpret_cast<const uint2*>(src + 8);
           const v8bf vf = __builtin_bit_cast(v8bf, make_uint4(w0.x, w0.y, w1.x, w1.y));
           acc[cb] = mfma_bf16(vf, phi[kb][kh2], acc[cb]);
@@ -368,14 +351,18 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
     }
 }
 
-__global__ __launch_bounds__(128) void prefill_kernel(PrefillArgs a) {
-  __shared__ __align__(16) uint8_t k_lds[K8_BYTES];
-  __shared__ __align__(16) uint8_t v_lds[V16_BYTES];
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillArgs a) {
+  // LDS: two K buffers (8 KiB) and two V buffers (8 KiB), distinct objects so
+  // that the compiler can tell a read of one buffer from a load into the other;
+  // an fp16 V record uses both V buffers
+  __shared__ __align__(16) uint8_t k_lds0[K8_BYTES], k_lds1[K8_BYTES];
+  __shared__ __align__(16) uint8_t v_lds0[V8_BYTES], v_lds1[V8_BYTES];
+  __shared__ __align__(16) float ks_lds0[4], ks_lds1[4];  // the tile's 4 K group scales
   const int rows = (a.t + BN - 1) / BN;
-  const int task = a.order[blockIdx.x], b = blockIdx.y;
+  const int task = __builtin_amdgcn_readfirstlane(a.order[blockIdx.x]), b = blockIdx.y;
   const int qh = task / rows, qb = task % rows, g = a.hq / a.hk, kh = qh / g;
   if (a.exact != nullptr && a.exact[qh]) {
-    prefill_exact(a, b, qh, qb, v_lds);
+    prefill_exact(a, b, qh, qb, v_lds0, v_lds1);
     return;
   }
   const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
@@ -405,35 +392,81 @@ __global__ __launch_bounds__(128) void prefill_kernel(PrefillArgs a) {
   st.m = -3.402823466e38f;
   st.den = 0.f;
   const float* ka8 = a.ka + rec0 * 4;
+  const float* ka4p = a.ka4 ? a.ka4 + rec0 * 4 : nullptr;
 
-  // F16 pass: tile 0, then the diagonal tile when qb > 0
-  if (qb > 0) prefill_pass<KF16>(a, st, qf, qs8, ka8, rec0, 0, 2, qb, qb, qrow, k_lds, v_lds);
-  else prefill_pass<KF16>(a, st, qf, qs8, ka8, rec0, 0, 1, 1, qb, qrow, k_lds, v_lds);
-  if (n8 > 0) prefill_pass<KI8>(a, st, qf, qs8, ka8, rec0, lo8, n8, 1, qb, qrow, k_lds, v_lds);
-  if (n4 > 0) {
-    // INT4 Q codes, sign-extended to bytes in feature order
+  // ---- F16 pass: tile 0, then the diagonal tile when qb > 0 (synchronous staging)
+  const int nf16 = qb > 0 ? 2 : 1;
+  for (int i = 0; i < nf16; ++i) {
+    const int col = i == 0 ? 0 : qb;
+    __syncthreads();
+    lds_copy_async(a.k8 + (rec0 + col) * K8_BYTES, k_lds0, K8_BYTES);
+    lds_copy_async(a.v16 + (rec0 + col) * V16_BYTES, v_lds0, V16_BYTES / 2);
+    lds_copy_async(a.v16 + (rec0 + col) * V16_BYTES + V16_BYTES / 2, v_lds1, V16_BYTES / 2);
+    lds_wait();
+    const float ks[4] = {ka8[col * 4], ka8[col * 4 + 1], ka8[col * 4 + 2], ka8[col * 4 + 3]};
+    prefill_tile<KF16>(a, st, qf, qs8, ks, col, i == nf16 - 1 && col == qb, qrow, k_lds0, v_lds0, v_lds1);
+  }
+
+  // ---- INT8 then INT4 passes as one pipelined tile list: the next tile's
+  // records stream into the other LDS buffer while the current one is used
+  const int total = n8 + n4;
+  if (total > 0) {
     v4i q4f[4];
+    float qs4 = 1.17549435e-38f;
+    if (n4 > 0) {
+      // INT4 Q codes, sign-extended to bytes in feature order
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      uint2 raw = make_uint2(0u, 0u);
-      if (row_ok) raw = *reinterpret_cast<const uint2*>(a.q4 + qrow_idx * (D / 2) + (ks * 32 + 16 * half) / 2);
-      const uint32_t wd[2] = {raw.x, raw.y};
-      uint32_t o[4];
+      for (int ks = 0; ks < 4; ++ks) {
+        uint2 raw = make_uint2(0u, 0u);
+        if (row_ok) raw = *reinterpret_cast<const uint2*>(a.q4 + qrow_idx * (D / 2) + (ks * 32 + 16 * half) / 2);
+        const uint32_t wd[2] = {raw.x, raw.y};
+        uint32_t o[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t w = wd[j >> 1] >> (16 * (j & 1));
-        uint32_t out = 0;
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t w = wd[j >> 1] >> (16 * (j & 1));
+          uint32_t out = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t nib = (w >> (4 * e)) & 0xfu;
-          out |= ((uint32_t)(((int)(nib ^ 8u)) - 8) & 0xffu) << (8 * e);
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t nib = (w >> (4 * e)) & 0xfu;
+            out |= ((uint32_t)(((int)(nib ^ 8u)) - 8) & 0xffu) << (8 * e);
+          }
+          o[j] = out;
         }
-        o[j] = out;
+        q4f[ks] = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
       }
-      q4f[ks] = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+      if (row_ok) qs4 = a.qa4[qrow_idx] * a.sm_log2;
     }
-    const float qs4 = row_ok ? a.qa4[qrow_idx] * a.sm_log2 : 1.17549435e-38f;
-    prefill_pass<KQ4>(a, st, q4f, qs4, a.ka4 + rec0 * 4, rec0, lo4, n4, 1, qb, qrow, k_lds, v_lds);
+    auto tile_col = [&](int i) { return i < n8 ? lo8 + i : lo4 + (i - n8); };
+    auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd) {
+      const int col = tile_col(i);
+      if (i < n8) lds_copy_async(a.k8 + (rec0 + col) * K8_BYTES, kd, K8_BYTES);
+      else lds_copy_async(a.k4 + (rec0 + col) * K4_BYTES, kd, K4_BYTES);
+      lds_copy_async(a.v8 + (rec0 + col) * V8_BYTES, vd, V8_BYTES);
+      // the scales ride along in the same kind of copy, so reading them later
+      // waits on nothing but the records' own wait
+      if (tid == 0)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>((i < n8 ? ka8 : ka4p) + col * 4),
+                                         (__attribute__((address_space(3))) void*)sd, 16, 0, 0);
+    };
+    // tile i: wait for its records (and for every wave to finish tile i-1,
+    // whose buffers receive tile i+1), start tile i+1's loads, compute
+    auto step = [&](int i, const uint8_t* kc, const uint8_t* vc, const float* sc, uint8_t* kn, uint8_t* vn,
+                    float* sn) {
+      lds_wait();
+      if (i + 1 < total) issue(i + 1, kn, vn, sn);
+      const int col = tile_col(i);
+      const bool masked = (i == total - 1 || i == n8 - 1) && col == qb;
+      const float4 k4v = *reinterpret_cast<const float4*>(sc);
+      const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
+      if (i < n8) prefill_tile<KI8>(a, st, qf, qs8, ks, col, masked, qrow, kc, vc);
+      else prefill_tile<KQ4>(a, st, q4f, qs4, ks, col, masked, qrow, kc, vc);
+    };
+    __syncthreads();  // every wave is done with the F16 pass's LDS
+    issue(0, k_lds0, v_lds0, ks_lds0);
+    for (int i = 0; i < total; i += 2) {
+      step(i, k_lds0, v_lds0, ks_lds0, k_lds1, v_lds1, ks_lds1);
+      if (i + 1 < total) step(i + 1, k_lds1, v_lds1, ks_lds1, k_lds0, v_lds0, ks_lds0);
+    }
   }
 
   // ---- epilogue: out = fma(acc / den, scale, mean) (prefill_sm80.cu:466-487)

@@ -60,9 +60,30 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 
 // The path's exp2: clamp to >= -125, split x = n + f with n = rint(x), degree-6
 // polynomial for 2^f in Horner order with fma, scale by 2^n.  The CPU oracle
-// evaluates the identical sequence, so results agree bit for bit.
+// evaluates the identical sequence (rint, ldexp), so results agree bit for bit.
+// Here n comes from the 1.5*2^23 shifter (t = x + 1.5*2^23 rounds to nearest
+// even like rint, and its low mantissa bits hold n in two's complement), and
+// 2^n is applied by adding n to the exponent field of p: for x in [-125, 127]
+// the product is a normal float, so this equals ldexp(p, n) exactly.
 __device__ __forceinline__ float texp2(float x) {
   x = fmaxf(x, -125.0f);
+  const float t = x + 12582912.0f;
+  const float n = t - 12582912.0f;
+  const float f = x - n;
+  float p = 0x1.41d32ep-13f;
+  p = __builtin_fmaf(p, f, 0x1.5f456cp-10f);
+  p = __builtin_fmaf(p, f, 0x1.3b2dbcp-7f);
+  p = __builtin_fmaf(p, f, 0x1.c6aed4p-5f);
+  p = __builtin_fmaf(p, f, 0x1.ebfbdap-3f);
+  p = __builtin_fmaf(p, f, 0x1.62e430p-1f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  return __uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
+}
+
+// texp2 without the clamp, for finite x whose result only feeds the 8-bit P
+// quantizer: it equals texp2(x) for x >= -125, and below that both results
+// quantize to level 0 (255 * 2^-125 rounds to 0), so the P levels are the same.
+__device__ __forceinline__ float texp2_p(float x) {
   const float n = __builtin_rintf(x);
   const float f = x - n;
   float p = 0x1.41d32ep-13f;

@@ -81,12 +81,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
     for (int kb = 0; kb < 2; ++kb) s[kb] = mfma_i8(k_frag<KIND>(k_lds, kb * 4 + kstep, L), qf[kstep], s[kb]);
 
   // score of accumulator r of block kb as a float: the magic float for 8-bit
-  // codes (1.5*2^23 + dot), the exact dot for 4-bit codes (MFMA gave 16*dot)
+  // codes (1.5*2^23 + dot), 16*dot for 4-bit codes (the MFMA saw 16*code keys;
+  // the 1/16 is folded into the slope, which is exact).  Only fp16 tiles can
+  // be the diagonal tile or reach past t: INT8/INT4 tiles are never masked.
   auto score = [&](int kb, int r) -> float {
-    float v = KIND == KQ4 ? (float)s[kb][r] * 0.0625f : __int_as_float(s[kb][r]);
-    if (masked) {
-      const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-      if (key > qrow || key >= a.t) v = -__builtin_inff();
+    float v = KIND == KQ4 ? (float)s[kb][r] : __int_as_float(s[kb][r]);
+    if constexpr (KIND == KF16) {
+      if (masked) {
+        const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (key > qrow || key >= a.t) v = -__builtin_inff();
+      }
     }
     return v;
   };
@@ -94,7 +98,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   // ---- scaled row max (prefill_sm80.cu:244-253)
   float slope[4];
 #pragma unroll
-  for (int gi = 0; gi < 4; ++gi) slope[gi] = qs * ks[gi];
+  for (int gi = 0; gi < 4; ++gi) slope[gi] = KIND == KQ4 ? qs * ks[gi] * 0.0625f : qs * ks[gi];
   float tile = -__builtin_inff();
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
@@ -169,7 +173,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = qd * 4 + i, gi = kb * 2 + (r >> 3);
-          const float e = texp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
+          const float e = texp2_p(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
           y[i] = __float_as_uint(__builtin_fmaf(e, 255.f, PMAGIC_HALF));
         }
         const uint32_t w = pack_byte1(y[0], y[1], y[2], y[3]);
@@ -455,11 +459,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
       lds_wait();
       if (i + 1 < total) issue(i + 1, kn, vn, sn);
       const int col = tile_col(i);
-      const bool masked = (i == total - 1 || i == n8 - 1) && col == qb;
       const float4 k4v = *reinterpret_cast<const float4*>(sc);
       const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
-      if (i < n8) prefill_tile<KI8>(a, st, qf, qs8, ks, col, masked, qrow, kc, vc);
-      else prefill_tile<KQ4>(a, st, q4f, qs4, ks, col, masked, qrow, kc, vc);
+      if (i < n8) prefill_tile<KI8>(a, st, qf, qs8, ks, col, false, qrow, kc, vc);
+      else prefill_tile<KQ4>(a, st, q4f, qs4, ks, col, false, qrow, kc, vc);
     };
     __syncthreads();  // every wave is done with the F16 pass's LDS
     issue(0, k_lds0, v_lds0, ks_lds0);

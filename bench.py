@@ -216,14 +216,15 @@ def main():
             pre0(0, q0, k0, v0, cfg["scale"])
             ops = next(iter(pre0.views.values()))
             table = next(iter(pre0.tables.values()))
-            exact = pre0.exact(0, hq0, hk0, dev)
+            exact, nx = pre0.exact(0, hq0, hk0, dev)
+            kx, vx = pre0.records if exact is not None else (None, None)
             outp = torch.empty((b, t, hq0, 128), dtype=torch.bfloat16, device=dev).transpose(1, 2)
             pk = ops["packed"]
 
             def attn():
                 module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
                                  ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], outp,
-                                 cfg["scale"], exact=exact, q=q0, k=k0, v=v0)
+                                 cfg["scale"], exact=exact, q=q0, kx=kx, vx=vx, nx=nx)
 
             for _ in range(2):
                 attn()

@@ -56,17 +56,28 @@ int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batc
  * scale; sm_log2 = f32(scale * log2(e)) as in prefill_sm80.cu:538.
  * v16p/v8p/k8p/k4p records and ka8/ka4 scales must be 16-byte aligned; v8p
  * must be set whenever a band has INT8 or INT4 key tiles (both use INT8 V).
- * exact: NULL, or int32 [hq] flags; a flagged q-head ignores its band and
- * computes exact causal attention on the raw bf16 qr [batch][hq][t][128]
- * (strides q_sb, q_sh, q_st) and kr/vr [batch][hk][t][128] (strides k_sb,
- * k_sh, k_st; rows 16-byte aligned) with fp32 softmax and accumulation
- * (extension for maps that keep some heads unquantized). */
+ * exact: NULL, or int32 [hq] on the device: 0 for a quantized q-head, else
+ * 1 + the record slot (< nx) of its KV head.  Such a q-head ignores its band
+ * and computes exact causal attention of the raw bf16 qr [batch][hq][t][128]
+ * (strides q_sb, q_sh, q_st; rows 16-byte aligned) against the KX/VX records
+ * [batch][nx][tiles] that tri_pack_exact wrote, with fp32 softmax and
+ * accumulation (extension for maps that keep some heads unquantized). */
 int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int batch, int hq, int hk, int t,
                   const void* v16p, const void* v8p, const float* vstat, const void* q8, const void* k8p,
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
                   double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
-                  const void* kr, const void* vr, int64_t k_sb, int64_t k_sh, int64_t k_st, void* stream);
+                  const void* kx, const void* vx, int nx, void* stream);
+
+/* No counterpart in the reference: the bf16 records of the exact heads that
+ * tri_attention reads (extension).  k/v bf16 [batch][hk][t][128] with element
+ * strides (rows 16-byte aligned); exact int32 [hq] as for tri_attention; the
+ * KV head of q-head h*(hq/hk) with exact value s > 0 is written to slot s-1 of
+ * kx/vx, 16 KiB per (sequence, slot, tile), keys at or past t zero.  Other KV
+ * heads are not read. */
+int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb,
+                   int64_t v_sh, int64_t v_st, int batch, int hq, int hk, int t, const int32_t* exact, int nx,
+                   void* kx, void* vx, void* stream);
 
 /* Replaces decode (common_host.cuh:47-87), batched and ragged.
  * q bf16 [batch][hq][1][128] (strides q_sb, q_sh); k8c/k4c/v8c/v4c compacted

@@ -34,6 +34,21 @@ def test_validation_errors_need_no_gpu():
     assert lib.tri_decode_occupancy(blocks) != 0 and b"null output" in lib.tri_last_error()
 
 
+def test_exact_head_validation_needs_no_gpu():
+    lib = load_library()
+    fake = ctypes.c_void_p(4096)  # aligned, never dereferenced: validation fails before any launch
+    rc = lib.tri_pack_exact(None, 0, 0, 0, None, 0, 0, 0, 1, 4, 2, 64, None, 1, None, None, None)
+    assert rc != 0 and b"pack_exact: null buffer" in lib.tri_last_error()
+    rc = lib.tri_pack_exact(fake, 0, 0, 0, fake, 0, 0, 0, 1, 4, 2, 64, fake, 3, fake, fake, None)
+    assert rc != 0 and b"nx must be in [1, hk]" in lib.tri_last_error()
+    rc = lib.tri_pack_exact(fake, 0, 0, 12, fake, 0, 0, 128, 1, 4, 2, 64, fake, 1, fake, fake, None)
+    assert rc != 0 and b"16-byte aligned" in lib.tri_last_error()
+    # attention with exact heads but no records
+    rc = lib.tri_attention(fake, 4, fake, 1, 4, 2, 64, fake, fake, fake, fake, fake, fake, fake, None, None, None, None,
+                           fake, 0, 0, 0, 0, 0.125, fake, fake, 0, 0, 0, fake, fake, 0, None)
+    assert rc != 0 and b"KX/VX records" in lib.tri_last_error()
+
+
 def test_oracle_library_loads():
     import oracle as O
     assert O.lib().ora_texp2(ctypes.c_float(0.0)) == 1.0

@@ -128,18 +128,20 @@ def test_decode_long_tail(module):
     _decode_case(module, 500, bands, batch=2, steps=20, max_tail=24, seed=5400)
 
 
-@pytest.mark.parametrize("t", [37, 64, 333])
-def test_exact_bf16_heads_in_the_same_launch(module, t):
-    """KV head 1 kept bf16: its q-heads match fp32 attention on the raw operands, the others the oracle."""
-    print(f"\n[parity] exact bf16 heads t={t}", flush=True)
+@pytest.mark.parametrize("t,bf16_kv", [(37, [1]), (64, [1]), (333, [1]), (200, [0, 2]), (129, [0, 1, 2])])
+def test_exact_bf16_heads_in_the_same_launch(module, t, bf16_kv):
+    """KV heads kept bf16: their q-heads match float64 attention on the raw operands, the others the oracle."""
+    print(f"\n[parity] exact bf16 heads t={t} kv={bf16_kv}", flush=True)
     q, k, v = small(6000 + t, 2, 6, 3, t)
     bands = torch.tensor([[INF, INF], [INF, INF], [1, INF], [1, INF], [2, 3], [2, 3]], dtype=torch.int32)
-    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5, bf16_kv=[1])
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5, bf16_kv=bf16_kv)
     ref, codes = oracle_prefill(q, k, v, bands, 128 ** -0.5)
     ex = exact_reference(q, k, v, 128 ** -0.5)
-    quant = [0, 1, 4, 5]
-    assert_close(out.numpy()[:, quant], ref[:, quant], what="quantized heads")
-    assert_close(out.numpy()[:, 2:4], ex[:, 2:4], what="exact heads")
+    exact_q = [h for h in range(6) if h // 2 in bf16_kv]
+    quant = [h for h in range(6) if h // 2 not in bf16_kv]
+    if quant:
+        assert_close(out.numpy()[:, quant], ref[:, quant], what="quantized heads")
+    assert_close(out.numpy()[:, exact_q], ex[:, exact_q], what="exact heads")
 
 
 def test_config2_shape_slice(module):

@@ -95,7 +95,7 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
                   double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
-                  const void* kr, const void* vr, int64_t k_sb, int64_t k_sh, int64_t k_st, void* stream) {
+                  const void* kx, const void* vx, int nx, void* stream) {
   g_error.clear();
   const int tiles = (t + tri::BN - 1) / tri::BN;
   if (!order || !bands || !v16p || !vstat || !q8 || !k8p || !qa8 || !ka8 || !out)
@@ -115,20 +115,19 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
       (int4 && (!aligned(k4p, 16) || !aligned(ka4, 16))))
     return fail("attention: record and K-scale buffers must be 16-byte aligned");
   if (int4 && v8p == nullptr) return fail("attention: INT4 key tiles need the INT8 V records");
-  if (exact != nullptr && (!qr || !kr || !vr || !aligned(qr, 16) || !aligned(kr, 16) || !aligned(vr, 16) ||
-                           (q_sb | q_sh | q_st | k_sb | k_sh | k_st) % 8 != 0))
-    return fail("attention: exact heads need 16-byte aligned bf16 q/k/v rows");
+  if (exact != nullptr && (!qr || !aligned(qr, 16) || (q_sb | q_sh | q_st) % 8 != 0))
+    return fail("attention: exact heads need 16-byte aligned bf16 q rows");
+  if (exact != nullptr && (nx < 1 || nx > hk || !kx || !vx || !aligned(kx, 16) || !aligned(vx, 16)))
+    return fail("attention: exact heads need 16-byte aligned KX/VX records of 1..hk KV heads");
   tri::PrefillArgs a;
   a.exact = exact;
   a.qr = static_cast<const uint16_t*>(qr);
-  a.kr = static_cast<const uint16_t*>(kr);
-  a.vr = static_cast<const uint16_t*>(vr);
   a.qsb = q_sb;
   a.qsh = q_sh;
   a.qst = q_st;
-  a.ksb = k_sb;
-  a.ksh = k_sh;
-  a.kst = k_st;
+  a.kx = static_cast<const uint8_t*>(kx);
+  a.vx = static_cast<const uint8_t*>(vx);
+  a.nx = nx;
   a.order = order;
   a.bands = bands;
   a.v16 = static_cast<const uint8_t*>(v16p);
@@ -154,6 +153,39 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
   hipStream_t s = static_cast<hipStream_t>(stream);
   tri::prefill_kernel<<<dim3(n_order, batch), 128, 0, s>>>(a);
   return check_launch("attention");
+}
+
+int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb,
+                   int64_t v_sh, int64_t v_st, int batch, int hq, int hk, int t, const int32_t* exact, int nx,
+                   void* kx, void* vx, void* stream) {
+  g_error.clear();
+  const int tiles = (t + tri::BN - 1) / tri::BN;
+  if (!k || !v || !exact || !kx || !vx) return fail("pack_exact: null buffer");
+  if (batch < 1 || hq < 1 || hk < 1 || t < 1) return fail("pack_exact: empty shape");
+  if (tiles > tri::MAX_TILES) return fail("pack_exact: at most 131072 tokens");
+  if (hq % hk != 0) return fail("pack_exact: q heads not a multiple of kv heads");
+  if (nx < 1 || nx > hk) return fail("pack_exact: nx must be in [1, hk]");
+  if (!aligned(k, 16) || !aligned(v, 16) || (k_sb | k_sh | k_st | v_sb | v_sh | v_st) % 8 != 0)
+    return fail("pack_exact: K/V rows must be 16-byte aligned");
+  if (!aligned(kx, 16) || !aligned(vx, 16)) return fail("pack_exact: KX/VX records must be 16-byte aligned");
+  tri::ExactPackArgs a;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.ksb = k_sb;
+  a.ksh = k_sh;
+  a.kst = k_st;
+  a.vsb = v_sb;
+  a.vsh = v_sh;
+  a.vst = v_st;
+  a.exact = exact;
+  a.kx = static_cast<uint8_t*>(kx);
+  a.vx = static_cast<uint8_t*>(vx);
+  a.hq = hq;
+  a.hk = hk;
+  a.t = t;
+  a.nx = nx;
+  tri::pack_exact_kernel<<<dim3(tiles, hk, batch), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch("pack_exact");
 }
 
 static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,

@@ -29,6 +29,7 @@ constexpr int D = 128;
 constexpr int BN = 64;
 constexpr int STAT_BLOCKS = 64;
 constexpr int K8_BYTES = 8192, K4_BYTES = 4096, V16_BYTES = 16384, V8_BYTES = 8192, V4_BYTES = 4096;
+constexpr int KX_BYTES = 16384;            // bf16 K or V of one tile, exact heads
 constexpr int K8_WORDS = K8_BYTES / 4, K4_WORDS = K4_BYTES / 4;
 constexpr int V16_WORDS = V16_BYTES / 4, V8_WORDS = V8_BYTES / 4, V4_WORDS = V4_BYTES / 4;
 constexpr float MAGIC = 12582912.0f;      // 1.5 * 2^23

@@ -34,12 +34,14 @@ struct PrefillArgs {
   int64_t osb, osh, ost;
   int hq, hk, t;
   float sm_log2;
-  // exact (bf16) heads: exact[qh] != 0 selects exact causal attention on the raw bf16 operands
+  // exact (bf16) heads: exact[qh] = 1 + record slot of the q-head's KV head
+  // (0: quantized) selects exact causal attention on the raw bf16 operands
   const int32_t* exact;
   const uint16_t* qr;
-  const uint16_t* kr;
-  const uint16_t* vr;
-  int64_t qsb, qsh, qst, ksb, ksh, kst;  // raw q strides; raw k/v share the k strides
+  int64_t qsb, qsh, qst;  // raw q strides (elements)
+  const uint8_t* kx;      // KX records [batch][nx][tiles]
+  const uint8_t* vx;      // VX records [batch][nx][tiles]
+  int nx;
 };
 
 enum Kind { KF16 = 0, KI8 = 1, KQ4 = 2 };
@@ -221,20 +223,67 @@ __device__ __forceinline__ void lds_wait() {
 // P split into bf16 high and low parts so that P V keeps ~2^-17 relative
 // precision, fp32 accumulation.  The reference's "exact" attention is
 // scaled_dot_product_attention over bf16 q/k/v (triattention/models.py:45-47).
-__device__ __forceinline__ v8bf load8bf(const uint16_t* p) {
-  const uint4 w = *reinterpret_cast<const uint4*>(p);
-  return __builtin_bit_cast(v8bf, w);
+//
+// Keys stream in 32-key steps: step s covers half kb = s & 1 of tile s >> 1,
+// whose K and V records are 8 KiB each (KX/VX layouts below) and land in the
+// LDS buffers of parity kb while step s - 1 computes.
+__device__ __forceinline__ void exact_step(const PrefillArgs& a, int col, int kb, bool masked, int qrow,
+                                           const v8bf (&qf)[8], v16f (&acc)[4], float& m, float& den,
+                                           const uint8_t* __restrict__ kl, const uint8_t* __restrict__ vl) {
+  const int L = threadIdx.x & 63, half = L >> 5;
+  // S^T = K Q^T for 32 keys x 32 queries
+  v16f s = {};
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks)
+    s = mfma_bf16(*reinterpret_cast<const v8bf*>(kl + ks * 1024 + L * 16), qf[ks], s);
+  float tile = -__builtin_inff();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = s[r] * a.sm_log2;
+    if (masked) {
+      const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (key > qrow || key >= a.t) x = -__builtin_inff();
+    }
+    s[r] = x;
+    tile = fmaxf(tile, x);
+  }
+  tile = fmaxf(tile, __shfl_xor(tile, 32, 64));
+  const float n = fmaxf(m, tile), alpha = __builtin_amdgcn_exp2f(m - n);
+  m = n;
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
+  }
+  v8bf phi[2], plo[2];
+  float psum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float p = __builtin_amdgcn_exp2f(s[r] - n);
+    const __bf16 h = (__bf16)p;
+    phi[r >> 3][r & 7] = h;
+    plo[r >> 3][r & 7] = (__bf16)(p - (float)h);
+    psum += p;
+  }
+  psum += __shfl_xor(psum, 32, 64);
+  den = __builtin_fmaf(den, alpha, psum);
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      const v8bf vf = *reinterpret_cast<const v8bf*>(vl + (cb * 2 + kh) * 1024 + L * 16);
+      acc[cb] = mfma_bf16(vf, phi[kh], acc[cb]);
+      acc[cb] = mfma_bf16(vf, plo[kh], acc[cb]);
+    }
 }
 
-__device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int qh, int qb, uint8_t* lds_lo,
-                                              uint8_t* lds_hi) {
-  const int g = a.hq / a.hk, kh = qh / g;
+__device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int qh, int qb, uint8_t* k0, uint8_t* k1,
+                                              uint8_t* v0, uint8_t* v1) {
+  const int tiles = (a.t + BN - 1) / BN;
   const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
   const int qrow = qb * BN + wave * 32 + lq;
   const bool row_ok = qrow < a.t;
-  // V tile transposed, [channel][64 keys] bf16: channels 0..63 in lds_lo, 64..127 in lds_hi
-  uint16_t* vt_lo = reinterpret_cast<uint16_t*>(lds_lo);
-  uint16_t* vt_hi = reinterpret_cast<uint16_t*>(lds_hi);
   v8bf qf[8];
   const uint16_t* qp = a.qr + b * a.qsb + qh * a.qsh + (int64_t)(row_ok ? qrow : 0) * a.qst;
 #pragma unroll
@@ -243,92 +292,30 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
     const uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * half) : z;
     qf[ks] = __builtin_bit_cast(v8bf, w);
   }
-  const uint16_t* kbase = a.kr + b * a.ksb + kh * a.ksh;
-  const uint16_t* vbase = a.vr + b * a.ksb + kh * a.ksh;
+  const int64_t rec0 = ((int64_t)b * a.nx + (a.exact[qh] - 1)) * tiles;
+  const uint8_t* kx = a.kx + rec0 * KX_BYTES;
+  const uint8_t* vx = a.vx + rec0 * KX_BYTES;
   v16f acc[4];
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[cb][r] = 0.f;
   float m = -3.402823466e38f, den = 0.f;
-  for (int col = 0; col <= qb; ++col) {
-    // stage V transposed; pairs of keys per 32-bit LDS word
-    __syncthreads();
-    for (int i = tid; i < 32 * 16; i += 128) {
-      const int kp = i >> 4, c0 = (i & 15) * 8;  // key pair kp (keys 2kp, 2kp+1), channels c0..c0+7
-      const int k0 = col * BN + 2 * kp;
-      uint4 r0 = make_uint4(0, 0, 0, 0), r1 = r0;
-      if (k0 < a.t) r0 = *reinterpret_cast<const uint4*>(vbase + (int64_t)k0 * a.kst + c0);
-      if (k0 + 1 < a.t) r1 = *reinterpret_cast<const uint4*>(vbase + (int64_t)(k0 + 1) * a.kst + c0);
-      const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w}, w1[4] = {r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-      for (int h = 0; h < 8; ++h) {
-        const uint32_t lo = (w0[h >> 1] >> (16 * (h & 1))) & 0xffffu, hi = (w1[h >> 1] >> (16 * (h & 1))) & 0xffffu;
-        const int c = c0 + h;
-        *reinterpret_cast<uint32_t*>((c < 64 ? vt_lo : vt_hi) + (c & 63) * BN + 2 * kp) = lo | (hi << 16);
-      }
-    }
-    // S^T = K Q^T straight from the row-major K rows (16-byte slices)
-    v16f s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-      const int key = col * BN + kb * 32 + lq;
-      const uint16_t* kp = kbase + (int64_t)min(key, a.t - 1) * a.kst + 8 * half;
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) s[kb] = mfma_bf16(load8bf(kp + ks * 16), qf[ks], s[kb]);
-    }
-    const bool masked = col == qb;
-    float tile = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        float x = s[kb][r] * a.sm_log2;
-        if (key >= a.t || (masked && key > qrow)) x = -__builtin_inff();
-        s[kb][r] = x;
-        tile = fmaxf(tile, x);
-      }
-    tile = fmaxf(tile, __shfl_xor(tile, 32, 64));
-    const float n = fmaxf(m, tile), alpha = __builtin_amdgcn_exp2f(m - n);
-    m = n;
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
-    }
-    v8bf phi[2][2], plo[2][2];
-    float psum = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(s[kb][r] - n);
-        const __bf16 h = (__bf16)p;
-        const __bf16 l = (__bf16)(p - (float)h);
-        phi[kb][r >> 3][r & 7] = h;
-        plo[kb][r >> 3][r & 7] = l;
-        psum += p;
-      }
-    psum += __shfl_xor(psum, 32, 64);
-    den = __builtin_fmaf(den, alpha, psum);
-    __syncthreads();
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int kh2 = 0; kh2 < 2; ++kh2) {
-          // keys kb*32 + 8*(2*kh2 + e/4) + 4*half + e%4 of channel cb*32 + lq: two runs of four keys
-          const uint16_t* src = (cb < 2 ? vt_lo : vt_hi) + ((cb & 1) * 32 + lq) * BN + kb * 32 + 16 * kh2 + 4 * half;
-          const uint2 w0 = *reinterpret_cast<const uint2*>(src), w1 = *reinterpret_cast<const uint2*>(src + 8);
-          const v8bf vf = __builtin_bit_cast(v8bf, make_uint4(w0.x, w0.y, w1.x, w1.y));
-          acc[cb] = mfma_bf16(vf, phi[kb][kh2], acc[cb]);
-          acc[cb] = mfma_bf16(vf, plo[kb][kh2], acc[cb]);
-        }
+  const int steps = 2 * (qb + 1);
+  auto issue = [&](int st, uint8_t* kd, uint8_t* vd) {
+    const int64_t off = (int64_t)(st >> 1) * KX_BYTES + (st & 1) * (KX_BYTES / 2);
+    lds_copy_async(kx + off, kd, KX_BYTES / 2);
+    lds_copy_async(vx + off, vd, KX_BYTES / 2);
+  };
+  issue(0, k0, v0);
+  for (int st = 0; st < steps; st += 2) {
+    const int col = st >> 1;
+    lds_wait();  // half 0 of tile col landed; every wave is done with half 1 of tile col-1
+    issue(st + 1, k1, v1);
+    exact_step(a, col, 0, col == qb, qrow, qf, acc, m, den, k0, v0);
+    lds_wait();  // half 1 landed; every wave is done with half 0
+    if (st + 2 < steps) issue(st + 2, k0, v0);
+    exact_step(a, col, 1, col == qb, qrow, qf, acc, m, den, k1, v1);
   }
   if (!row_ok) return;
   const float inv = 1.f / den;
@@ -355,6 +342,67 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
     }
 }
 
+// Packs the K and V of every exact KV head into KX / VX records (one workgroup
+// per (tile, KV head, sequence); other heads return at once).  Keys at or past
+// t are zero.  Per 64-key tile, 16 KiB each, 32-key half kb at byte kb*8192:
+//   KX fragment F = ks (16-feature step), lane L 16 bytes = bf16 K[key kb*32 + L%32]
+//      [features ks*16 + 8*(L/32) .. +7]      (A operand of S^T = K Q^T)
+//   VX fragment F = cb*2 + kh, lane L element e = bf16 V[key kb*32 + 16*kh + 8*(e/4)
+//      + 4*(L/32) + e%4][channel cb*32 + L%32] (A operand of O^T = V^T P^T)
+struct ExactPackArgs {
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t ksb, ksh, kst, vsb, vsh, vst;
+  const int32_t* exact;  // [hq]: 1 + record slot of the q-head's KV head, 0 if quantized
+  uint8_t* kx;
+  uint8_t* vx;
+  int hq, hk, t, nx;
+};
+
+__global__ __launch_bounds__(256) void pack_exact_kernel(ExactPackArgs a) {
+  const int tile = blockIdx.x, kh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int slot = a.exact[kh * (a.hq / a.hk)] - 1;
+  if (slot < 0) return;
+  const int tiles = gridDim.x;
+  const int64_t rec = ((int64_t)b * a.nx + slot) * tiles + tile;
+  uint8_t* kd = a.kx + rec * KX_BYTES;
+  uint8_t* vd = a.vx + rec * KX_BYTES;
+  const uint16_t* kbase = a.k + b * a.ksb + kh * a.ksh;
+  const uint16_t* vbase = a.v + b * a.vsb + kh * a.vsh;
+  constexpr int VP = D + 8;  // padded LDS row (bf16 elements)
+  __shared__ __align__(16) uint16_t vt[BN * VP];
+  // K: 1024 16-byte pieces in source order (key, 8-feature piece)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, key = c >> 4, f0 = (c & 15) * 8;
+    const int tok = tile * BN + key;
+    uint4 w = make_uint4(0, 0, 0, 0), u = w;
+    if (tok < a.t) {
+      w = *reinterpret_cast<const uint4*>(kbase + (int64_t)tok * a.kst + f0);
+      u = *reinterpret_cast<const uint4*>(vbase + (int64_t)tok * a.vst + f0);
+    }
+    const int kb = key >> 5, lk = key & 31, ks = f0 >> 4, h = (f0 >> 3) & 1;
+    *reinterpret_cast<uint4*>(kd + kb * (KX_BYTES / 2) + ks * 1024 + (h * 32 + lk) * 16) = w;
+    *reinterpret_cast<uint4*>(vt + key * VP + f0) = u;
+  }
+  __syncthreads();
+  // V: 1024 output pieces in destination order
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, F = c >> 6, L = c & 63;  // F = kb*8 + cb*2 + kh
+    const int kb = F >> 3, cb = (F >> 1) & 3, khalf = F & 1, ch = cb * 32 + (L & 31), h = L >> 5;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e0 = 2 * j, e1 = 2 * j + 1;
+      const int k0 = kb * 32 + 16 * khalf + 8 * (e0 >> 2) + 4 * h + (e0 & 3);
+      const int k1 = kb * 32 + 16 * khalf + 8 * (e1 >> 2) + 4 * h + (e1 & 3);
+      w[j] = (uint32_t)vt[k0 * VP + ch] | ((uint32_t)vt[k1 * VP + ch] << 16);
+    }
+    *reinterpret_cast<uint4*>(vd + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillArgs a) {
   // LDS: two K buffers (8 KiB) and two V buffers (8 KiB), distinct objects so
   // that the compiler can tell a read of one buffer from a load into the other;
@@ -365,8 +413,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int rows = (a.t + BN - 1) / BN;
   const int task = __builtin_amdgcn_readfirstlane(a.order[blockIdx.x]), b = blockIdx.y;
   const int qh = task / rows, qb = task % rows, g = a.hq / a.hk, kh = qh / g;
-  if (a.exact != nullptr && a.exact[qh]) {
-    prefill_exact(a, b, qh, qb, v_lds0, v_lds1);
+  if (a.exact != nullptr && a.exact[qh] > 0) {
+    prefill_exact(a, b, qh, qb, k_lds0, k_lds1, v_lds0, v_lds1);
     return;
   }
   const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;

@@ -13,6 +13,9 @@ RuntimeError, as TORCH_CHECK did in the reference.
 Extensions over the reference signatures (batch = 1 is exactly the reference):
   * a leading batch dimension on every tensor;
   * ``attention`` also accepts an fp32 ``out`` (parity testing);
+  * ``attention`` computes the q-heads flagged in ``exact`` as exact bf16
+    attention over records written by ``pack_exact`` (maps that keep some KV
+    heads unquantized);
   * ``decode`` takes ragged batches: ``prompt`` may be a device int32 tensor of
     per-sequence lengths, with per-sequence metadata rows.
 """
@@ -32,8 +35,9 @@ D = 128
 STAT_BLOCKS = 64
 K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
-EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_decode",
+EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
            "tri_decode_partials", "tri_decode_merge", "tri_decode_occupancy", "tri_device_cus")
+KX_BYTES = 16384
 
 
 def build(arch: str = "gfx950") -> Path:
@@ -54,7 +58,8 @@ def load_library() -> ctypes.CDLL:
                                    P, P, P, P, P, P, P, P, P, P, P]
     lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P]
     lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_,
-                                  P, P, I64, I64, I64, P, P, I64, I64, I64, P]
+                                  P, P, I64, I64, I64, P, P, I, P]
+    lib.tri_pack_exact.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I, P, I, P, P, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
@@ -139,12 +144,13 @@ class Module:
 
     # --------------------------------------------------------------- attention
     def attention(self, order, bands, groups, entries, v16p, v8p, v4p, vstat, q8, k8p, qa8, ka8, q4, k4p, qa4, ka4,
-                  out, scale, exact=None, q=None, k=None, v=None):
+                  out, scale, exact=None, q=None, kx=None, vx=None, nx=0):
         """Banded causal attention: per key tile skip / INT8 QK x FP16 or INT8 PV / INT4 QK x INT8 PV.
 
-        Extension: ``exact`` (int32 [Hq] flags on the device) with the raw bf16
-        ``q`` [B,Hq,T,128] and ``k``/``v`` [B,Hk,T,128] computes the flagged
-        q-heads as exact causal attention on the unquantized operands."""
+        Extension: ``exact`` (int32 [Hq] on the device, 0 or 1 + record slot
+        of the q-head's KV head) with the raw bf16 ``q`` [B,Hq,T,128] and the
+        ``kx``/``vx`` records of ``pack_exact`` computes the flagged q-heads as
+        exact causal attention on the unquantized operands."""
         _check(q8.dtype == torch.int8 and q8.dim() == 4 and q8.size(3) == D and q8.is_contiguous(), "Q8 [B,Hq,T,128]")
         b, h, t, _ = q8.shape
         hk = vstat.numel() // (b * 3 * D)
@@ -163,20 +169,34 @@ class Module:
         dt = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
         if exact is not None:
             _check(exact.dtype == torch.int32 and exact.numel() == h and exact.is_cuda and
-                   q is not None and k is not None and v is not None and
-                   q.dtype == k.dtype == v.dtype == torch.bfloat16 and tuple(q.shape) == (b, h, t, D) and
-                   tuple(k.shape) == (b, hk, t, D) and k.shape == v.shape and k.stride() == v.stride() and
-                   q.stride(3) == 1 and k.stride(3) == 1, "exact heads: flags [Hq] and bf16 q/k/v")
+                   q is not None and q.dtype == torch.bfloat16 and tuple(q.shape) == (b, h, t, D) and
+                   q.stride(3) == 1, "exact heads: flags [Hq] and bf16 q [B,Hq,T,128]")
+            _check(1 <= nx <= hk and kx is not None and vx is not None and
+                   kx.numel() * kx.element_size() >= b * nx * tiles * KX_BYTES and
+                   vx.numel() * vx.element_size() >= b * nx * tiles * KX_BYTES, "exact heads: KX/VX records")
         qs = q.stride() if exact is not None else (0, 0, 0)
-        ks = k.stride() if exact is not None else (0, 0, 0)
         with torch.cuda.device(q8.device):
             self._call(self.lib.tri_attention, _ptr(order), order.numel(), _ptr(bands), b, h, hk, t, _ptr(v16p),
                        _ptr(v8p), _ptr(vstat), _ptr(q8), _ptr(k8p), _ptr(qa8), _ptr(ka8), _ptr(q4), _ptr(k4p),
                        _ptr(qa4), _ptr(ka4), _ptr(out), dt, out.stride(0), out.stride(1), out.stride(2),
                        float(scale), _ptr(exact), _ptr(q if exact is not None else None), qs[0], qs[1], qs[2],
-                       _ptr(k if exact is not None else None), _ptr(v if exact is not None else None),
-                       ks[0], ks[1], ks[2], self._stream(q8.device))
+                       _ptr(kx if exact is not None else None), _ptr(vx if exact is not None else None),
+                       int(nx) if exact is not None else 0, self._stream(q8.device))
         return out
+
+    def pack_exact(self, k, v, exact, nx, kx, vx):
+        """bf16 K/V of the exact KV heads -> KX/VX records [B][nx][tiles] (16 KiB each; extension)."""
+        _check(k.dtype == v.dtype == torch.bfloat16 and k.dim() == 4 and k.shape == v.shape and k.size(3) == D and
+               k.stride(3) == 1 and v.stride(3) == 1, "K/V bf16 [B,Hk,T,128]")
+        b, hk, t, _ = k.shape
+        h = exact.numel()
+        tiles = (t + 63) // 64
+        _check(exact.dtype == torch.int32 and exact.is_cuda and h % hk == 0, "exact flags [Hq]")
+        _check(1 <= nx <= hk and kx.numel() * kx.element_size() >= b * nx * tiles * KX_BYTES and
+               vx.numel() * vx.element_size() >= b * nx * tiles * KX_BYTES, "KX/VX records [B][nx][tiles]")
+        with torch.cuda.device(k.device):
+            self._call(self.lib.tri_pack_exact, _ptr(k), *k.stride()[:3], _ptr(v), *v.stride()[:3], b, h, hk, t,
+                       _ptr(exact), int(nx), _ptr(kx), _ptr(vx), self._stream(k.device))
 
     # ------------------------------------------------------------------ decode
     def decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, kcur,

@@ -13,6 +13,7 @@ import torch
 
 SKIP, F16, I8, I4, Q4 = 0, 1, 2, 3, 4
 WORDS = {F16: 4096, I8: 2048, I4: 1024}
+KX_BYTES = 16384  # bf16 K (or V) record of one tile of an exact KV head
 
 
 def tile_counts(bands: torch.Tensor, rows: int):
@@ -72,21 +73,35 @@ class Prefill:
         self.out_dtype = out_dtype
         self.tables, self.buffers, self.views, self.layer_buffers = {}, {}, {}, {}
         self.exact_flags = {}
+        self.records = None
 
     def exact(self, layer, heads, kv_heads, device):
-        """int32 [Hq] flags of the q-heads whose KV head the map keeps in bf16 (None if none)."""
+        """(int32 [Hq] device flags, nx) for the KV heads the map keeps in bf16, or (None, 0).
+
+        A flagged q-head holds 1 + the record slot of its KV head (slots in
+        increasing KV-head order); unflagged q-heads hold 0."""
         bf16 = getattr(self.bands_fn, "bf16", None)
-        kv = list(bf16(layer)) if bf16 is not None else []
+        kv = sorted(set(int(h) for h in bf16(layer))) if bf16 is not None else []
         if not kv:
-            return None
+            return None, 0
+        if not all(0 <= h < kv_heads for h in kv):
+            raise ValueError(f"bf16 KV heads {kv} out of range for {kv_heads} KV heads")
         key = (layer, heads, device)
         if key not in self.exact_flags:
             group = heads // kv_heads
             flags = torch.zeros(heads, dtype=torch.int32)
-            for h in kv:
-                flags[h * group:(h + 1) * group] = 1
-            self.exact_flags[key] = flags.to(device)
+            for slot, h in enumerate(kv):
+                flags[h * group:(h + 1) * group] = slot + 1
+            self.exact_flags[key] = flags.to(device), len(kv)
         return self.exact_flags[key]
+
+    def exact_records(self, nbytes, device):
+        """KX/VX record buffers of the exact heads (grown on demand, reused across calls)."""
+        cur = self.records
+        if cur is None or cur[0].numel() < nbytes or cur[0].device != device:
+            cur = self.records = (torch.empty(nbytes, dtype=torch.uint8, device=device),
+                                  torch.empty(nbytes, dtype=torch.uint8, device=device))
+        return cur[0][:nbytes], cur[1][:nbytes]
 
     def table(self, layer, heads, kv_heads, rows, device):
         key = (None if getattr(self.bands_fn, "layer_independent", False) else layer, heads, rows)
@@ -157,7 +172,7 @@ class Prefill:
         self.module.pack_v(v, ops["partial"], vstat, packed[F16], packed[I8], packed[I4])
         dtype = self.out_dtype or q.dtype
         out = torch.empty((batch, t, hq, 128), dtype=dtype, device=device).transpose(1, 2)
-        exact = self.exact(layer, hq, hk, device)
+        exact, nx = self.exact(layer, hq, hk, device)
         if exact is None:
             self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
                                   ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
@@ -165,9 +180,11 @@ class Prefill:
         else:
             if decode is not None:
                 raise NotImplementedError("decode caches for maps with bf16 heads")
+            kx, vx = self.exact_records(batch * nx * rows * KX_BYTES, device)
+            self.module.pack_exact(k, v, exact, nx, kx, vx)
             self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
                                   ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
-                                  scale, exact=exact, q=q, k=k, v=v)
+                                  scale, exact=exact, q=q, kx=kx, vx=vx, nx=nx)
         if decode is not None:
             self.decode_cache.store(layer, t, ops["kp"], ka, kstat, vstat, packed, decode[0], table.host,
                                     ops["k4"], ka4)

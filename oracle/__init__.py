@@ -49,6 +49,7 @@ def lib():
         L.ora_texp2.restype = F
         L.ora_texp2.argtypes = [F]
         L.ora_texp2_batch.argtypes = [P, P, I64]
+        L.ora_texp2_shifter_batch.argtypes = [P, P, I64]
         L.ora_rotate128.argtypes = [P]
         L.ora_f32_to_f16.restype = ctypes.c_uint16
         L.ora_f32_to_f16.argtypes = [F]
@@ -87,6 +88,14 @@ def texp2(x):
     x = _c(x, np.float32)
     y = np.empty_like(x)
     lib().ora_texp2_batch(_p(x), _p(y), x.size)
+    return y
+
+
+def texp2_shifter(x):
+    """texp2 in the GPU kernels' form (shifter + exponent-field add); equal to texp2 by construction."""
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    lib().ora_texp2_shifter_batch(_p(x), _p(y), x.size)
     return y
 
 

@@ -23,8 +23,10 @@
  *  - ora_texp2 is the one exp2 of the path: x clamped to >= -125, n = rint(x),
  *    f = x - n, a degree-6 polynomial for 2^f evaluated by fmaf in Horner
  *    order, scaled by 2^n.  Max error 0.93 ulp over [-125, 0].  The GPU
- *    kernels evaluate the identical operation sequence, so quantized P levels
- *    (which are discrete functions of exp2) agree bit for bit.
+ *    kernels compute the same function, so quantized P levels (discrete
+ *    functions of exp2) agree bit for bit; they obtain n from the 1.5*2^23
+ *    shifter and add it to the exponent field instead of calling rint/ldexp.
+ *    ora_texp2_shifter restates that form so tests can pin the equality.
  *  - Per-element expressions that decide discrete values (codes, P levels,
  *    fp16 probabilities) follow the reference's operation sequence literally,
  *    including the 1.5*2^23 "magic" offset in the 8-bit score argument
@@ -72,6 +74,23 @@ float ora_texp2(float x) {
 
 void ora_texp2_batch(const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = ora_texp2(x[i]);
+}
+
+/* The GPU kernels' form of texp2 (csrc/common.h): t = x + 1.5*2^23 rounds to
+ * nearest even and holds n = rint(x) in its low mantissa bits; 2^n is applied
+ * by adding (bits(t) << 23) to the bits of the polynomial. */
+float ora_texp2_shifter(float x) {
+  x = fmaxf(x, -125.0f);
+  volatile float t = x + MAGIC_F;
+  const float n = t - MAGIC_F;
+  const float f = x - n;
+  float p = EXP2_C[6];
+  for (int k = 5; k >= 0; --k) p = fmaf(p, f, EXP2_C[k]);
+  return bitsf(fbits(p) + (fbits(t) << 23));
+}
+
+void ora_texp2_shifter_batch(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = ora_texp2_shifter(x[i]);
 }
 
 /* ------------------------------------------------------- fp16 / bf16 RNE */

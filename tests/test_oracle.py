@@ -43,6 +43,17 @@ def test_texp2_special_values():
     assert np.all(O.texp2(np.float32([-np.inf, -200.0, -125.0])) == lo)
 
 
+def test_texp2_gpu_form_equals_rint_ldexp_form():
+    """The kernels add n = rint(x) to the exponent field via the 1.5*2^23 shifter; a dense sample of
+    every float pattern in [-200, 127] (stride 997) plus the specials must give identical bits."""
+    pos = np.arange(0, np.float32(127.0).view(np.uint32) + 1, 997, dtype=np.uint32)
+    neg = np.arange(0, np.float32(200.0).view(np.uint32) + 1, 997, dtype=np.uint32) | np.uint32(0x80000000)
+    x = np.concatenate([pos, neg]).view(np.float32)
+    x = np.concatenate([x, np.float32([-np.inf, np.inf, np.nan, -125.0, -124.5, -0.5, 0.5, 126.5, -0.0])])
+    a, b = O.texp2(x).view(np.uint32), O.texp2_shifter(x).view(np.uint32)
+    assert np.array_equal(a, b), x[a != b][:5]
+
+
 # -------------------------------------------------------------- rotation
 def walsh(i, j):
     return -1.0 if bin(i & j).count("1") % 2 else 1.0

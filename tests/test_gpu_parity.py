@@ -1,7 +1,9 @@
 """GPU parity: the gfx950 kernels through the C ABI against the CPU oracle.
 
 Bar: quantized codes, scales and statistics bit-exact; attention outputs (fp32)
-within 2e-3 max-abs and 1e-3 mean-abs of the oracle.
+within 2e-3 max-abs and 1e-3 mean-abs of the oracle.  Exact (bf16) heads are held
+to float64 attention over the same bf16 inputs: mean-abs 1e-3, max-abs 2e-3 or
+torch fp32 SDPA's own max-abs error on those inputs, whichever is larger.
 """
 from __future__ import annotations
 
@@ -10,7 +12,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close, compare_codes, exact_reference, oracle_prefill, run_prefill
+from helpers import assert_close, compare_codes, exact_max_abs_bar, exact_reference, oracle_prefill, run_prefill
 from triattention_amd import synthetic as S
 from triattention_amd.kernels.decode import DecodeCache
 from triattention_amd.synthetic import INF, bits
@@ -141,7 +143,8 @@ def test_exact_bf16_heads_in_the_same_launch(module, t, bf16_kv):
     quant = [h for h in range(6) if h // 2 not in bf16_kv]
     if quant:
         assert_close(out.numpy()[:, quant], ref[:, quant], what="quantized heads")
-    assert_close(out.numpy()[:, exact_q], ex[:, exact_q], what="exact heads")
+    bar = exact_max_abs_bar(q, k, v, 128 ** -0.5, exact_q, ex)
+    assert_close(out.numpy()[:, exact_q], ex[:, exact_q], max_abs=bar, what="exact heads")
 
 
 def test_config2_shape_slice(module):
@@ -157,4 +160,6 @@ def test_config2_shape_slice(module):
     quant_q = [h for h in range(28) if h // g not in bf16_kv]
     compare_codes(ops, codes[0], 0, 1, 28, 4, 1024)
     assert_close(out.numpy()[:, quant_q], ref[:, quant_q], what="config 2 quantized heads")
-    assert_close(out.numpy()[:, exact_q], ex[:, exact_q], what="config 2 exact heads")
+    bar = exact_max_abs_bar(c["q"], c["k"], c["v"], c["scale"], exact_q, ex)
+    mx, _ = assert_close(out.numpy()[:, exact_q], ex[:, exact_q], max_abs=bar, what="config 2 exact heads")
+    print(f"config2 exact heads: max abs {mx:.3e}, bar {bar:.3e} (fp32 SDPA vs float64)")

@@ -115,7 +115,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
       }
     }
   tile = xor32_max(tile);
-  const float n = fmaxf(st.m, tile);
+  // Running reference max.  fp16 tiles need the exact running max (their P
+  // is relative to it).  INT8/INT4 P levels are relative to the tile's own
+  // base, so the reference max only scales acc and den alike and acc/den does
+  // not depend on it: those tiles move it only when a tile exceeds it by more
+  // than 64, which skips most rescales.  Headroom: bq <= 2^(64 + margin)/255
+  // and |PV| < 2^21 per tile, so acc stays below 2^(64 + 21 + 11) over 2048
+  // tiles, far inside fp32.
+  const float n = KIND == KF16 ? fmaxf(st.m, tile) : (tile > st.m + 64.f ? tile : st.m);
   const float alpha = texp2(st.m - n);
   st.m = n;
   if (__any(alpha != 1.f)) {
@@ -203,14 +210,22 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   }
 }
 
-// Asynchronous global -> LDS copy of `bytes` (a multiple of 1 KiB) by the two
+// Asynchronous global -> LDS copy of BYTES (a multiple of 2 KiB) by the two
 // waves of the workgroup, 1 KiB per wave instruction (lane L's 16 bytes land
-// at dst + 16 L); completion is awaited with s_waitcnt + barrier.
-__device__ __forceinline__ void lds_copy_async(const uint8_t* src, uint8_t* dst, int bytes) {
-  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63;
-  for (int off = wave * 1024; off < bytes; off += 2048)
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + off + L * 16),
+// at dst + 16 L); completion is awaited with s_waitcnt + barrier.  The wave
+// index is uniform, so src + off stays in scalar registers and each copy is
+// one instruction with a 32-bit lane offset.
+template <int BYTES>
+__device__ __forceinline__ void lds_copy_async(const uint8_t* src, uint8_t* dst) {
+  static_assert(BYTES % 2048 == 0, "copies move 2 KiB per step");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = (threadIdx.x & 63) * 16;
+#pragma unroll
+  for (int i = 0; i < BYTES / 2048; ++i) {
+    const int off = i * 2048 + wave * 1024;
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + off + lane),
                                      (__attribute__((address_space(3))) void*)(dst + off), 16, 0, 0);
+  }
 }
 
 __device__ __forceinline__ void lds_wait() {
@@ -227,47 +242,55 @@ __device__ __forceinline__ void lds_wait() {
 // Keys stream in 32-key steps: step s covers half kb = s & 1 of tile s >> 1,
 // whose K and V records are 8 KiB each (KX/VX layouts below) and land in the
 // LDS buffers of parity kb while step s - 1 computes.
-__device__ __forceinline__ void exact_step(const PrefillArgs& a, int col, int kb, bool masked, int qrow,
-                                           const v8bf (&qf)[8], v16f (&acc)[4], float& m, float& den,
-                                           const uint8_t* __restrict__ kl, const uint8_t* __restrict__ vl) {
+template <bool MASKED>
+__device__ __forceinline__ void exact_step(const PrefillArgs& a, int col, int kb, int qrow, const v8bf (&qf)[8],
+                                           v16f (&acc)[4], float& m, float& den, const uint8_t* __restrict__ kl,
+                                           const uint8_t* __restrict__ vl) {
   const int L = threadIdx.x & 63, half = L >> 5;
   // S^T = K Q^T for 32 keys x 32 queries
   v16f s = {};
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks)
     s = mfma_bf16(*reinterpret_cast<const v8bf*>(kl + ks * 1024 + L * 16), qf[ks], s);
-  float tile = -__builtin_inff();
+  if constexpr (MASKED) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    float x = s[r] * a.sm_log2;
-    if (masked) {
+    for (int r = 0; r < 16; ++r) {
       const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-      if (key > qrow || key >= a.t) x = -__builtin_inff();
+      if (key > qrow || key >= a.t) s[r] = -__builtin_inff();
     }
-    s[r] = x;
-    tile = fmaxf(tile, x);
   }
-  tile = fmaxf(tile, __shfl_xor(tile, 32, 64));
-  const float n = fmaxf(m, tile), alpha = __builtin_amdgcn_exp2f(m - n);
-  m = n;
-  if (__any(alpha != 1.f)) {
+  // row max on the raw dot products (the scale is positive), in log2 units after
+  float mx = s[0];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float tile = mx * a.sm_log2;
+  // Reference max for P = 2^(x - m): acc and den scale alike, so m only needs
+  // to keep P in range; it moves when a step exceeds it by more than 16.
+  const float n = tile > m + 16.f ? tile : m;
+  if (n != m) {
+    const float alpha = __builtin_amdgcn_exp2f(m - n);
+    m = n;
+    den *= alpha;
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
+    }
   }
   v8bf phi[2], plo[2];
   float psum = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const float p = __builtin_amdgcn_exp2f(s[r] - n);
+    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.sm_log2, -m));
     const __bf16 h = (__bf16)p;
     phi[r >> 3][r & 7] = h;
     plo[r >> 3][r & 7] = (__bf16)(p - (float)h);
     psum += p;
   }
   psum += __shfl_xor(psum, 32, 64);
-  den = __builtin_fmaf(den, alpha, psum);
+  den += psum;
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
@@ -301,22 +324,27 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[cb][r] = 0.f;
   float m = -3.402823466e38f, den = 0.f;
-  const int steps = 2 * (qb + 1);
   auto issue = [&](int st, uint8_t* kd, uint8_t* vd) {
     const int64_t off = (int64_t)(st >> 1) * KX_BYTES + (st & 1) * (KX_BYTES / 2);
-    lds_copy_async(kx + off, kd, KX_BYTES / 2);
-    lds_copy_async(vx + off, vd, KX_BYTES / 2);
+    lds_copy_async<KX_BYTES / 2>(kx + off, kd);
+    lds_copy_async<KX_BYTES / 2>(vx + off, vd);
   };
   issue(0, k0, v0);
-  for (int st = 0; st < steps; st += 2) {
-    const int col = st >> 1;
+  // tiles before the diagonal: no mask
+  for (int col = 0; col < qb; ++col) {
     lds_wait();  // half 0 of tile col landed; every wave is done with half 1 of tile col-1
-    issue(st + 1, k1, v1);
-    exact_step(a, col, 0, col == qb, qrow, qf, acc, m, den, k0, v0);
+    issue(2 * col + 1, k1, v1);
+    exact_step<false>(a, col, 0, qrow, qf, acc, m, den, k0, v0);
     lds_wait();  // half 1 landed; every wave is done with half 0
-    if (st + 2 < steps) issue(st + 2, k0, v0);
-    exact_step(a, col, 1, col == qb, qrow, qf, acc, m, den, k1, v1);
+    issue(2 * col + 2, k0, v0);
+    exact_step<false>(a, col, 1, qrow, qf, acc, m, den, k1, v1);
   }
+  // the diagonal tile qb, masked
+  lds_wait();
+  issue(2 * qb + 1, k1, v1);
+  exact_step<true>(a, qb, 0, qrow, qf, acc, m, den, k0, v0);
+  lds_wait();
+  exact_step<true>(a, qb, 1, qrow, qf, acc, m, den, k1, v1);
   if (!row_ok) return;
   const float inv = 1.f / den;
   const int64_t obase = b * a.osb + qh * a.osh + (int64_t)qrow * a.ost;
@@ -451,9 +479,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int i = 0; i < nf16; ++i) {
     const int col = i == 0 ? 0 : qb;
     __syncthreads();
-    lds_copy_async(a.k8 + (rec0 + col) * K8_BYTES, k_lds0, K8_BYTES);
-    lds_copy_async(a.v16 + (rec0 + col) * V16_BYTES, v_lds0, V16_BYTES / 2);
-    lds_copy_async(a.v16 + (rec0 + col) * V16_BYTES + V16_BYTES / 2, v_lds1, V16_BYTES / 2);
+    lds_copy_async<K8_BYTES>(a.k8 + (rec0 + col) * K8_BYTES, k_lds0);
+    lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES, v_lds0);
+    lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES + V16_BYTES / 2, v_lds1);
     lds_wait();
     const float ks[4] = {ka8[col * 4], ka8[col * 4 + 1], ka8[col * 4 + 2], ka8[col * 4 + 3]};
     prefill_tile<KF16>(a, st, qf, qs8, ks, col, i == nf16 - 1 && col == qb, qrow, k_lds0, v_lds0, v_lds1);
@@ -491,9 +519,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     auto tile_col = [&](int i) { return i < n8 ? lo8 + i : lo4 + (i - n8); };
     auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd) {
       const int col = tile_col(i);
-      if (i < n8) lds_copy_async(a.k8 + (rec0 + col) * K8_BYTES, kd, K8_BYTES);
-      else lds_copy_async(a.k4 + (rec0 + col) * K4_BYTES, kd, K4_BYTES);
-      lds_copy_async(a.v8 + (rec0 + col) * V8_BYTES, vd, V8_BYTES);
+      if (i < n8) lds_copy_async<K8_BYTES>(a.k8 + (rec0 + col) * K8_BYTES, kd);
+      else lds_copy_async<K4_BYTES>(a.k4 + (rec0 + col) * K4_BYTES, kd);
+      lds_copy_async<V8_BYTES>(a.v8 + (rec0 + col) * V8_BYTES, vd);
       // the scales ride along in the same kind of copy, so reading them later
       // waits on nothing but the records' own wait
       if (tid == 0)

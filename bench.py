@@ -10,6 +10,12 @@ resident in HBM.  Also reported: tokens/s, the decode kernel's roofline
 on a bounded sample, and prefill attention TOPS on configs[0] (C0).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+       python bench.py --copy-probe   (a plain 256 MiB device copy, five times: the
+       known-size kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)
+
+``roofline.traffic`` is the decode kernel's HBM bytes per launch measured with
+those counters; it is read from profiles/decode_kernel_C1_traffic.md, which
+holds the commands and the raw counter values (null when that file is absent).
 """
 from __future__ import annotations
 
@@ -51,6 +57,31 @@ def decode_record_bytes(cache_entry):
     return int(((kbytes + vbytes + 16) * valid).sum()), int(valid.sum())
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_kernel_C1_traffic.md"
+COPY_PROBE_BYTES = 256 << 20
+
+
+def measured_traffic():
+    """HBM bytes per decode_kernel launch from the committed counter summary, or None."""
+    if not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def copy_probe():
+    import torch
+    n = COPY_PROBE_BYTES // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(f"copy probe: 5 x torch.neg over {COPY_PROBE_BYTES} B in, {COPY_PROBE_BYTES} B out", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -59,7 +90,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
+    ap.add_argument("--copy-probe", action="store_true")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
@@ -167,7 +202,8 @@ def main():
         "step_bytes": int(step_bytes),
         "roofline": {"bound": "hbm", "kernel": "decode_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes": rec_bytes, "avg_us": round(dec_ms * 1e3, 2)},
+                     "traffic": measured_traffic(), "algorithmic_bytes": rec_bytes,
+                     "avg_us": round(dec_ms * 1e3, 2)},
     }
 
     # ------------------------------------------------------------- CPU baseline

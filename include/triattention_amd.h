@@ -90,7 +90,12 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * out [batch][hq][1][128] (strides o_sb, o_sh), out_dtype 0 = fp32, 1 = bf16;
  * pm/pl f32 [batch][hq][splits], po f32 [batch][hq][splits][128] with
  * splits = max(1, ceil(maxn / per)); n_k8/n_k4/n_v8/n_v4 are the record
- * counts of the compacted arrays (each array below 2 GiB). */
+ * counts of the compacted arrays (each array below 2 GiB).
+ * Exact (bf16) KV heads (extension): xslot NULL, or int32 [batch][hk] with -1
+ * for a quantized head and otherwise the index of the head's first KX/VX
+ * record in kxc/vxc (tri_pack_exact layout, n_kx records of 16 KiB each); such
+ * a head keeps every prompt tile (count = tiles, entry[e] = e) and attends
+ * exactly over its bf16 prompt and tail. */
 int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -98,7 +103,8 @@ int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const
                int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh, const int64_t* step,
                void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
                const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
-               int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, double scale, void* stream);
+               int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
+               const void* vxc, int64_t n_kx, double scale, void* stream);
 
 /* The two launches of tri_decode separately, same arguments: the split-KV
  * kernel (writes pm/pl/po) and the merge with the bf16 tail (writes out and
@@ -112,7 +118,8 @@ int tri_decode_partials(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                         int64_t c_sb, int64_t c_sh, const int64_t* step, void* out, int out_dtype, int64_t o_sb,
                         int64_t o_sh, float* pm, float* pl, float* po, const int32_t* prompt, int batch, int hq,
                         int hk, int maxn, int per, int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8,
-                        int64_t n_v4, double scale, void* stream);
+                        int64_t n_v4, const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
+                        double scale, void* stream);
 int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                      const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                      const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -120,7 +127,8 @@ int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c,
                      int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh,
                      const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                      float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
-                     int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, double scale, void* stream);
+                     int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
+                     const void* vxc, int64_t n_kx, double scale, void* stream);
 
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */

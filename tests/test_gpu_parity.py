@@ -130,6 +130,58 @@ def test_decode_long_tail(module):
     _decode_case(module, 500, bands, batch=2, steps=20, max_tail=24, seed=5400)
 
 
+def _attend64(q, keys, values, scale):
+    """float64 and float32 attention of one query per head over explicit key/value lists:
+    q [Hq,128], keys/values [Hk,L,128] (GQA groups adjacent)."""
+    g = q.shape[0] // keys.shape[0]
+    outs = []
+    for dt in (torch.float64, torch.float32):
+        k = keys.to(dt).repeat_interleave(g, 0)
+        v = values.to(dt).repeat_interleave(g, 0)
+        w = torch.softmax(torch.einsum("hd,hld->hl", q.to(dt), k) * scale, dim=-1)
+        outs.append(torch.einsum("hl,hld->hd", w, v).numpy())
+    return outs
+
+
+@pytest.mark.parametrize("prompt,bf16_kv,batch", [(300, [1], 2), (64, [0, 2], 1), (1500, [2], 2)])
+def test_decode_with_exact_heads(module, prompt, bf16_kv, batch):
+    """Maps with bf16 KV heads through Prefill + DecodeCache: quantized heads match the oracle, exact heads
+    match float64 attention over the raw bf16 prompt and tail."""
+    print(f"\n[parity] decode with exact heads prompt={prompt} kv={bf16_kv} batch={batch}", flush=True)
+    hq, hk, steps, max_tail = 6, 3, 4, 8
+    q, k, v = small(7000 + prompt, batch, hq, hk, prompt)
+    bands = torch.tensor([[2, 4], [1, INF], [INF, INF], [1, 1], [3, 6], [2, 2]], dtype=torch.int32)
+    scale = 128 ** -0.5
+    cache = DecodeCache(module, max_tail=max_tail)
+    cache.out_dtype = torch.float32
+    run_prefill(module, q, k, v, bands, scale, decode_cache=cache, bf16_kv=bf16_kv)
+    ref_codes = [O.prefill_codes(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), decode_cache=True)
+                 for b in range(batch)]
+    per = cache.layers[0]["per"]
+    g = S.gen(7100 + prompt)
+    ktail = np.zeros((batch, hk, max_tail, 128), np.uint16)
+    vtail = np.zeros_like(ktail)
+    keys, values = k.clone(), v.clone()
+    exact_q = [h for h in range(hq) if h // 2 in bf16_kv]
+    quant_q = [h for h in range(hq) if h // 2 not in bf16_kv]
+    dev = torch.device("cuda")
+    for step in range(steps):
+        qd, kd, vd = S.outlier_tensor(g, batch, hq, 1), S.outlier_tensor(g, batch, hk, 1), S.outlier_tensor(g, batch, hk, 1)
+        out = cache(0, qd.to(dev), kd.to(dev), vd.to(dev), scale).float().cpu().numpy()
+        keys, values = torch.cat([keys, kd], 2), torch.cat([values, vd], 2)
+        for b in range(batch):
+            if quant_q:
+                ref = O.decode(ref_codes[b], bands.numpy(), bits(qd[b, :, 0]), prompt, per, scale, ktail[b],
+                               vtail[b], bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
+                assert_close(out[b, quant_q, 0], ref[quant_q], what=f"quantized heads step {step} seq {b}")
+            r64, r32 = _attend64(qd[b, :, 0], keys[b], values[b], scale)
+            bar = max(2e-3, float(np.abs(r32[exact_q] - r64[exact_q]).max()))
+            assert_close(out[b, exact_q, 0], r64[exact_q], max_abs=bar, what=f"exact heads step {step} seq {b}")
+            ktail[b, :, step] = bits(kd[b, :, 0])
+            vtail[b, :, step] = bits(vd[b, :, 0])
+        cache.advance()
+
+
 @pytest.mark.parametrize("t,bf16_kv", [(37, [1]), (64, [1]), (333, [1]), (200, [0, 2]), (129, [0, 1, 2])])
 def test_exact_bf16_heads_in_the_same_launch(module, t, bf16_kv):
     """KV heads kept bf16: their q-heads match float64 attention on the raw operands, the others the oracle."""

@@ -126,6 +126,48 @@ def test_ragged_cache_assembly_slots_are_consistent():
             row += 1
 
 
+def test_exact_heads_in_a_ragged_cache():
+    """bf16 KV heads keep every tile, select no quantized record, and xslot points at their own KX records."""
+    cache = DecodeCache(FakeModule(), max_tail=8)
+    cache.ragged = True
+    hk, bands = 3, torch.tensor([[2, 4], [1, INF], [INF, INF], [1, 1], [3, 3], [1, 2]], dtype=torch.int32)
+    exact_kv = [0, 2]
+    rng = torch.Generator().manual_seed(1)
+    seen = []
+    for prompt, batch in ((300, 2), (64, 1)):
+        tiles = (prompt + 63) // 64
+        kp = torch.randint(0, 2 ** 31, (batch * hk * tiles * 2048,), generator=rng).to(torch.uint32)
+        k4 = torch.randint(0, 2 ** 31, (batch * hk * tiles * 1024,), generator=rng).to(torch.uint32)
+        packed = {F16: None, I8: torch.randint(0, 2 ** 31, (batch * hk * tiles * 2048,), generator=rng).to(torch.uint32),
+                  I4: torch.randint(0, 2 ** 31, (batch * hk * tiles * 1024,), generator=rng).to(torch.uint32)}
+        ka = torch.rand(batch * hk * tiles * 4, generator=rng)
+        stat = torch.rand(batch, hk, 3, 128, generator=rng)
+        kx = torch.randint(0, 256, (batch * 2 * tiles * 16384 + 999,), generator=rng).to(torch.uint8)
+        vx = torch.randint(0, 256, kx.shape, generator=rng).to(torch.uint8)
+        codes, _ = cache.codes(tiles)
+        cache.store(0, prompt, kp, ka, stat.clone(), stat.clone(), packed, codes, bands, k4, ka.clone(), exact_kv,
+                    kx, vx)
+        seen.append((prompt, batch, tiles, kx[:batch * 2 * tiles * 16384].view(batch, 2, tiles, 16384),
+                     vx[:batch * 2 * tiles * 16384].view(batch, 2, tiles, 16384)))
+    e = cache.layers[0]
+    kxs, vxs = e["kx"].view(-1, 16384), e["vx"].view(-1, 16384)
+    row = 0
+    for prompt, batch, tiles, kx, vx in seen:
+        for s in range(batch):
+            assert int(e["xslot"][row, 1]) == -1
+            for slot, h in enumerate(exact_kv):
+                assert int(e["count"][row, h]) == tiles
+                assert e["entry"][row, h, :tiles].tolist() == list(range(tiles))
+                x0 = int(e["xslot"][row, h])
+                for j in range(tiles):
+                    assert torch.equal(kxs[x0 + j], kx[s, slot, j]) and torch.equal(vxs[x0 + j], vx[s, slot, j])
+            row += 1
+    # only KV head 1 selects quantized records
+    n8 = sum(int(sequence_metadata(bands, (p + 63) // 64, hk, cache.codes((p + 63) // 64)[0], exact_kv)["is8"].sum()) * b
+             for p, b, *_ in seen)
+    assert e["k8"].shape[0] == n8
+
+
 def test_maps_bundled_and_extension(tmp_path):
     for name in maps.PRESETS.values():
         data = json.loads((maps.DATA / f"{name}.json").read_text())

@@ -195,8 +195,8 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh,
                        const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                        float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
-                       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, double scale, void* stream,
-                       int phase) {
+                       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
+                       const void* kxc, const void* vxc, int64_t n_kx, double scale, void* stream, int phase) {
   g_error.clear();
   if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
       !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
@@ -213,7 +213,16 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   if (n_k8 < 1 || n_v8 < 1 || n_v4 < 1 || n_k8 * tri::K8_BYTES >= lim || n_k4 * tri::K4_BYTES >= lim ||
       n_v8 * tri::V8_BYTES >= lim || n_v4 * tri::V4_BYTES >= lim || (k4c != nullptr && n_k4 < 1))
     return fail("decode: compacted record arrays must be non-empty and below 2 GiB each");
+  if (xslot != nullptr && (!kxc || !vxc || n_kx < 1 || n_kx * tri::KX_BYTES >= lim || !aligned(kxc, 16) ||
+                           !aligned(vxc, 16)))
+    return fail("decode: exact heads need 16-byte aligned KX/VX record arrays, non-empty and below 2 GiB");
   tri::DecodeArgs d;
+  d.xslot = xslot;
+  d.kxc = static_cast<const uint8_t*>(kxc);
+  d.vxc = static_cast<const uint8_t*>(vxc);
+  d.kx_bytes = xslot ? (int)(n_kx * tri::KX_BYTES) : 0;
+  d.kstat = kstat;
+  d.vstat = vstat;
   d.q = static_cast<const uint16_t*>(q);
   d.k8c = static_cast<const uint8_t*>(k8c);
   d.k4c = static_cast<const uint8_t*>(k4c);
@@ -274,11 +283,21 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (phase & 1) {
     const dim3 grid(splits, hk, batch);
-    switch (std::min(hq / hk, 4)) {
-      case 1: tri::decode_kernel<1><<<grid, 64, 0, s>>>(d); break;
-      case 2: tri::decode_kernel<2><<<grid, 64, 0, s>>>(d); break;
-      case 3: tri::decode_kernel<3><<<grid, 64, 0, s>>>(d); break;
-      default: tri::decode_kernel<4><<<grid, 64, 0, s>>>(d); break;
+    const int rows = std::min(hq / hk, 4);
+    if (xslot == nullptr) {
+      switch (rows) {
+        case 1: tri::decode_kernel<1><<<grid, 64, 0, s>>>(d); break;
+        case 2: tri::decode_kernel<2><<<grid, 64, 0, s>>>(d); break;
+        case 3: tri::decode_kernel<3><<<grid, 64, 0, s>>>(d); break;
+        default: tri::decode_kernel<4><<<grid, 64, 0, s>>>(d); break;
+      }
+    } else {
+      switch (rows) {
+        case 1: tri::decode_kernel<1, true><<<grid, 64, 0, s>>>(d); break;
+        case 2: tri::decode_kernel<2, true><<<grid, 64, 0, s>>>(d); break;
+        case 3: tri::decode_kernel<3, true><<<grid, 64, 0, s>>>(d); break;
+        default: tri::decode_kernel<4, true><<<grid, 64, 0, s>>>(d); break;
+      }
     }
   }
   if (phase & 2) tri::decode_merge_kernel<<<dim3(hq, batch), 256, 0, s>>>(mg);
@@ -288,7 +307,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
 #define TRI_DECODE_ARGS                                                                                      \
   q, q_sb, q_sh, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8c, v4c, vstat, kstat, ktail, vtail, t_sb, t_sh, \
       t_st, max_tail, kcur, vcur, c_sb, c_sh, step, out, out_dtype, o_sb, o_sh, pm, pl, po, prompt, batch, hq, hk,  \
-      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, scale, stream
+      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, xslot, kxc, vxc, n_kx, scale, stream
 #define TRI_DECODE_PARAMS                                                                                          \
   const void *q, int64_t q_sb, int64_t q_sh, const void *k8c, const void *k4c, const float *ka, const float *ka4,  \
       const int32_t *entry, const int32_t *kinfo, const int32_t *count, const int32_t *fmt, const int32_t *slot,  \
@@ -296,7 +315,8 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
       int64_t t_sb, int64_t t_sh, int64_t t_st, int max_tail, const void *kcur, const void *vcur, int64_t c_sb,    \
       int64_t c_sh, const int64_t *step, void *out, int out_dtype, int64_t o_sb, int64_t o_sh, float *pm,          \
       float *pl, float *po, const int32_t *prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,    \
-      int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, double scale, void *stream
+      int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t *xslot, const void *kxc,           \
+      const void *vxc, int64_t n_kx, double scale, void *stream
 
 int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
 int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }

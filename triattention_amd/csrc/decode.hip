@@ -35,6 +35,15 @@ struct DecodeArgs {
   int hq, hk, maxn, per, tiles_max, splits;
   float sm_log2;
   int k8_bytes, k4_bytes, v8_bytes, v4_bytes;  // sizes of the compacted record arrays (< 2^31)
+  // exact (bf16) KV heads: xslot[B][Hk] = first KX/VX record of the (sequence,
+  // KV head) whose tiles are all kept (record of tile j at xslot + j), or -1
+  // for a quantized head; xslot may be null when no head is exact
+  const int32_t* xslot;
+  const uint8_t* kxc;
+  const uint8_t* vxc;
+  const float* kstat;   // [B][Hk][3][128]: K mean (the frame of the merge's tail scores)
+  const float* vstat;   // [B][Hk][3][128]: V mean, scale, 1/scale
+  int kx_bytes;
 };
 
 constexpr int MAX_TAIL = 1024;
@@ -44,7 +53,126 @@ __device__ __forceinline__ v4i unpack16(v4i w) {
              (int)nib_hi16((uint32_t)w[1])};
 }
 
-template <int R, int W = (R == 1 ? 3 : 2)>
+// Split partials of an exact (bf16) KV head over its prompt tiles [first, last):
+// S^T = K Q^T with bf16 MFMA (the g q-heads are the columns), scores
+// (q.k - q.kmean) * sm_log2 in the frame of the merge's tail scores, fp32 online
+// softmax, P split into bf16 high and low parts, O^T = V^T P^T.  The partials
+// use the quantized heads' convention: m in log2 units, l = sum p, o = sum p v'
+// with v' = (v - mean) / scale, so the merge treats every head alike.
+__device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh, int split) {
+  // Q as the B operand, kept in LDS: column lq = q-head kh*g + lq, features ks*16 + 8*half + e
+  __shared__ __align__(16) uint16_t qx[32][D];
+  const int L = threadIdx.x, lq = L & 31, half = L >> 5;
+  const int g = a.hq / a.hk, prompt = a.prompt[b];
+  const int64_t hb = (int64_t)b * a.hk + kh;
+  const int cnt = a.count[hb], first = split * a.per, last = min(cnt, first + a.per);
+  const int x0 = a.xslot[hb];
+  float cq = 0.f;
+  const float* kmean = a.kstat + hb * 3 * D;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (lq < g) w = *reinterpret_cast<const uint4*>(a.q + b * a.qsb + (int64_t)(kh * g + lq) * a.qsh + ks * 16 + 8 * half);
+    *reinterpret_cast<uint4*>(&qx[lq][ks * 16 + 8 * half]) = w;
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      cq = __builtin_fmaf(bf16f((ww[e >> 1] >> (16 * (e & 1))) & 0xffffu), kmean[ks * 16 + 8 * half + e], cq);
+  }
+  cq += __shfl_xor(cq, 32, 64);
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)a.kxc, (short)0, a.kx_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)a.vxc, (short)0, a.kx_bytes, 0x00020000);
+  v16f acc[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[cb][r] = 0.f;
+  float m = -3.402823466e38f, den = 0.f;
+  v4i kf[8], vf[8];
+  // half step hs covers keys 32*(hs & 1) .. +31 of tile first + hs / 2; the
+  // next half's K streams in after the QK MFMAs, its V after the PV MFMAs
+  auto off_of = [&](int hs) { return (x0 + first + (hs >> 1)) * KX_BYTES + (hs & 1) * (KX_BYTES / 2); };
+  auto load_k = [&](int hs) {
+#pragma unroll
+    for (int F = 0; F < 8; ++F) kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, L * 16 + F * 1024, off_of(hs), 0);
+  };
+  auto load_v = [&](int hs) {
+#pragma unroll
+    for (int F = 0; F < 8; ++F) vf[F] = __builtin_amdgcn_raw_buffer_load_b128(rv, L * 16 + F * 1024, off_of(hs), 0);
+  };
+  const int steps = 2 * max(0, last - first);
+  if (steps > 0) {
+    load_k(0);
+    load_v(0);
+  }
+  for (int hs = 0; hs < steps; ++hs) {
+    v16f sc = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      sc = mfma_bf16(__builtin_bit_cast(v8bf, kf[ks]), *reinterpret_cast<const v8bf*>(&qx[lq][ks * 16 + 8 * half]),
+                     sc);
+    if (hs + 1 < steps) load_k(hs + 1);
+    const int key0 = (first + (hs >> 1)) * BN + (hs & 1) * 32;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
+      sc[r] = key < prompt ? (sc[r] - cq) * a.sm_log2 : -__builtin_inff();
+      mx = fmaxf(mx, sc[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float n = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - n);
+    m = n;
+    den *= alpha;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
+    v8bf phi[2], plo[2];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = __builtin_amdgcn_exp2f(sc[r] - n);
+      const __bf16 h = (__bf16)p;
+      phi[r >> 3][r & 7] = h;
+      plo[r >> 3][r & 7] = (__bf16)(p - (float)h);
+      psum += p;
+    }
+    den += psum + __shfl_xor(psum, 32, 64);
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int kh2 = 0; kh2 < 2; ++kh2) {
+        const v8bf v = __builtin_bit_cast(v8bf, vf[cb * 2 + kh2]);
+        acc[cb] = mfma_bf16(v, phi[kh2], acc[cb]);
+        acc[cb] = mfma_bf16(v, plo[kh2], acc[cb]);
+      }
+    if (hs + 1 < steps) load_v(hs + 1);
+  }
+  if (lq >= g) return;
+  const int64_t idx = ((int64_t)b * a.hq + kh * g + lq) * a.splits + split;
+  const float* vmean = a.vstat + hb * 3 * D;
+  const float* vinv = vmean + 2 * D;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int ch = cb * 32 + 8 * r4 + 4 * half;
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (acc[cb][r4 * 4 + i] - vmean[ch + i] * den) * vinv[ch + i];
+      *reinterpret_cast<float4*>(a.po + idx * D + ch) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  if (half == 0) {
+    a.pl[idx] = den;
+    a.pm[idx] = m;
+  }
+}
+
+// R: q-head rows per lane half (min(group, 4)); EXACT: the launch holds exact
+// (bf16) KV heads, whose path is compiled in only then (it needs 2 waves/SIMD).
+template <int R, bool EXACT = false, int W = (R == 1 && !EXACT ? 3 : 2)>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
   __shared__ __align__(16) int8_t q8s[MAX_GROUP][D];
   __shared__ __align__(16) int8_t q4s[MAX_GROUP][D];
@@ -53,6 +181,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   __shared__ __align__(16) float rsc[4][MAX_GROUP];  // alpha, base, bq, restore per row
 
   const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  if constexpr (EXACT) {
+    if (a.xslot[(int64_t)b * a.hk + kh] >= 0) {
+      decode_exact(a, b, kh, split);
+      return;
+    }
+  }
   const int L = threadIdx.x, lq = L & 31, half = L >> 5;
   const int g = a.hq / a.hk;
   const int prompt = a.prompt[b];

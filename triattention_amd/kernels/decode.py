@@ -8,6 +8,10 @@ precision of a (KV head, tile) is the maximum over its GQA group, each q-head
 attends only its own kept tiles (rowmask), and the V format is INT8 for the
 sink tile and the last NEAR_V8 tiles, INT4 elsewhere.
 
+Extension: exact (bf16) KV heads (the map's optional "bf16" key) keep every
+prompt tile as bf16 KX/VX records and attend exactly; the same launch serves
+both kinds of head.
+
 Extension: batches.  One ``store`` holds the B sequences of one Prefill call;
 with ``ragged = True`` successive ``store`` calls for a layer append their
 sequences (e.g. one Prefill per prompt of a different length), and the decode
@@ -21,6 +25,7 @@ from .prefill import I4, I8
 
 WORDS = {I8: 2048, I4: 1024}
 K8_WORDS, K4_WORDS = 2048, 1024
+KX_BYTES = 16384
 NEAR_V8 = 16
 
 
@@ -32,11 +37,18 @@ def tile_states(bands: torch.Tensor, tiles: int) -> torch.Tensor:
     return torch.where((j[None, :] == 0) | (d < w8), 8, torch.where(d < w4, 4, 0))
 
 
-def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor):
-    """Kept-tile lists and slots of one sequence (host, int64), as decode.py:27-53."""
+def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor, exact_kv=()):
+    """Kept-tile lists and slots of one sequence (host, int64), as decode.py:27-53.
+
+    Extension: KV heads in ``exact_kv`` keep every tile (count = tiles, entry
+    j = j) and select no quantized record; the kernel reads their bf16 KX/VX
+    records instead."""
     state = tile_states(bands, tiles)
     hq = state.shape[0]
     state = state.view(hk, hq // hk, tiles)
+    exact = torch.zeros(hk, dtype=torch.bool)
+    exact[list(exact_kv)] = True
+    state[exact] = 8
     kv = state.amax(1)
     rowmask = ((state > 0).to(torch.int64) << torch.arange(state.shape[1])[None, :, None]).sum(1)
     count = (kv > 0).sum(1)
@@ -44,8 +56,9 @@ def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor):
     order = torch.argsort((kv == 0).to(torch.int8), dim=1, stable=True)[:, :maxn]
     valid = torch.arange(maxn)[None, :] < count[:, None]
     kprec = kv.gather(1, order)
-    is4 = (kprec == 4) & valid
-    is8 = (kprec == 8) & valid
+    quant = valid & ~exact[:, None]
+    is4 = (kprec == 4) & quant
+    is8 = (kprec == 8) & quant
     rows = torch.arange(hk)[:, None] * tiles + order
     ragged = lambda select: torch.cumsum(select.flatten(), 0).view(hk, maxn) - 1
     kslot = torch.where(is4, ragged(is4), torch.where(is8, ragged(is8), 0))
@@ -54,11 +67,11 @@ def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor):
     vslot = torch.zeros((hk, maxn), dtype=torch.int64)
     vsel = {}
     for code in (I8, I4):
-        select = valid & (vcode == code)
+        select = quant & (vcode == code)
         vslot = torch.where(select, ragged(select), vslot)
         vsel[code] = select
     return dict(count=count, maxn=maxn, order=order, valid=valid, is4=is4, is8=is8, rows=rows, kslot=kslot,
-                kbase=kbase, vslot=vslot, vcode=vcode, vsel=vsel)
+                kbase=kbase, vslot=vslot, vcode=vcode, vsel=vsel, exact=exact)
 
 
 class DecodeCache:
@@ -75,11 +88,17 @@ class DecodeCache:
             self.formats[rows] = codes, frozenset(codes.unique().tolist())
         return self.formats[rows]
 
-    def store(self, layer, prompt, kp, ka, kstat, vstat, packed, codes, bands, k4, ka4):
+    def store(self, layer, prompt, kp, ka, kstat, vstat, packed, codes, bands, k4, ka4, exact_kv=(), kx=None,
+              vx=None):
+        """Keep one Prefill call's records (decode.py:24-67).  Extension: ``exact_kv``
+        lists the KV heads kept in bf16, whose KX/VX records ``kx``/``vx``
+        ([B][len(exact_kv)][tiles], tri_pack_exact layout) are copied whole."""
         tiles = (prompt + 63) // 64
         batch = vstat.shape[0]
         hk, device = vstat.shape[1], ka.device
-        meta = sequence_metadata(bands, tiles, hk, codes)
+        exact_kv = sorted(set(int(h) for h in exact_kv))
+        meta = sequence_metadata(bands, tiles, hk, codes, exact_kv)
+        nbytes = batch * len(exact_kv) * tiles * KX_BYTES
         # record indices of every sequence of the batch, sequence-major
         seq = torch.arange(batch)[:, None] * (hk * tiles)
         pick = lambda select: (seq + meta["rows"][select][None, :]).flatten().to(device)
@@ -93,7 +112,9 @@ class DecodeCache:
                      v={code: (packed[code].view(batch * hk * tiles, WORDS[code]).index_select(0, pick(meta["vsel"][code]))
                                if bool(meta["vsel"][code].any()) else None) for code in (I8, I4)},
                      ka=ka.view(batch, hk, tiles, 4), ka4=ka4.view(batch, hk, tiles, 4) if ka4 is not None else None,
-                     kstat=kstat.view(batch, hk, 3, 128), vstat=vstat.view(batch, hk, 3, 128))
+                     kstat=kstat.view(batch, hk, 3, 128), vstat=vstat.view(batch, hk, 3, 128), exact=exact_kv,
+                     kx=kx.reshape(-1)[:nbytes].clone() if exact_kv else None,
+                     vx=vx.reshape(-1)[:nbytes].clone() if exact_kv else None)
         if self.step is None:
             self.step = torch.zeros(1, dtype=torch.int64, device=device)
         self.step.zero_()
@@ -118,8 +139,9 @@ class DecodeCache:
         ka4 = torch.ones_like(ka) if has4 else None
         kstat = torch.empty((total, hk, 3, 128), dtype=torch.float32, device=device)
         vstat = torch.empty_like(kstat)
-        k8s, k4s, v8s, v4s = [], [], [], []
-        o8 = o4 = ov8 = ov4 = 0
+        k8s, k4s, v8s, v4s, kxs, vxs = [], [], [], [], [], []
+        xslot = torch.full((total, hk), -1, dtype=torch.int64)
+        o8 = o4 = ov8 = ov4 = ox = 0
         row = 0
         for g in groups:
             m, n, b = g["meta"], g["meta"]["maxn"], g["batch"]
@@ -133,6 +155,8 @@ class DecodeCache:
                 count[r] = m["count"]
                 fmt[r, :g["tiles"]] = g["fmt"] - 1
                 prompt[r] = g["prompt"]
+                for xs, h in enumerate(g["exact"]):
+                    xslot[r, h] = ox + (s * len(g["exact"]) + xs) * g["tiles"]
             ka[row:row + b, :, :g["tiles"]] = g["ka"]
             if g["ka4"] is not None and ka4 is not None:
                 ka4[row:row + b, :, :g["tiles"]] = g["ka4"]
@@ -145,6 +169,10 @@ class DecodeCache:
                 v8s.append(g["v"][I8])
             if g["v"][I4] is not None:
                 v4s.append(g["v"][I4])
+            if g["exact"]:
+                kxs.append(g["kx"])
+                vxs.append(g["vx"])
+                ox += b * len(g["exact"]) * g["tiles"]
             o8 += b * g["n8"]
             o4 += b * g["n4"]
             ov8 += b * g["nv"][I8]
@@ -161,7 +189,9 @@ class DecodeCache:
         return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, fmt=to(fmt), slot=to(slot), entry=to(entry),
                     kinfo=to(kinfo), count=to(count), k8=cat(k8s, K8_WORDS), k4=cat(k4s, K4_WORDS) if has4 else None,
                     ka=ka, ka4=ka4, kstat=kstat, vstat=vstat, v={I8: cat(v8s, WORDS[I8]), I4: cat(v4s, WORDS[I4])},
-                    tail_k=tail_k, tail_v=torch.zeros_like(tail_k), batch=total, tiles_max=tiles_max)
+                    tail_k=tail_k, tail_v=torch.zeros_like(tail_k), batch=total, tiles_max=tiles_max,
+                    xslot=to(xslot) if kxs else None, kx=torch.cat(kxs) if kxs else None,
+                    vx=torch.cat(vxs) if vxs else None)
 
     def __call__(self, layer, q, k, v, scale):
         e = self.layers[layer]
@@ -176,7 +206,8 @@ class DecodeCache:
         out = torch.empty(q.shape, dtype=dtype, device=q.device)
         self.module.decode(q, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"],
                            e["slot"], e["v"][I8], e["v"][I4], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], k, v,
-                           self.step, out, *e[key], e["prompt"], e["per"], scale)
+                           self.step, out, *e[key], e["prompt"], e["per"], scale, xslot=e["xslot"], kxc=e["kx"],
+                           vxc=e["vx"])
         return out
 
     def advance(self):

@@ -61,7 +61,8 @@ def load_library() -> ctypes.CDLL:
                                   P, P, I64, I64, I64, P, P, I, P]
     lib.tri_pack_exact.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I, P, I, P, P, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
-                   P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64, D_, P]
+                   P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64,
+                   P, P, P, I64, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
         getattr(lib, name).argtypes = decode_args
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
@@ -200,11 +201,13 @@ class Module:
 
     # ------------------------------------------------------------------ decode
     def decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, kcur,
-               vcur, step, out, pm, pl, po, prompt, per, scale, phase=3):
+               vcur, step, out, pm, pl, po, prompt, per, scale, phase=3, xslot=None, kxc=None, vxc=None):
         """Single-token decode over the quantized cache plus the bf16 tail.
 
         ``phase`` (extension): 3 runs both kernels, 1 only the split-KV kernel,
-        2 only the merge (for per-kernel timing)."""
+        2 only the merge (for per-kernel timing).  ``xslot`` (extension, int32
+        [B,Hk], -1 = quantized head) with the KX/VX record arrays ``kxc``/``vxc``
+        makes the listed KV heads attend exactly over their bf16 prompt."""
         _check(q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(2) == 1 and q.size(3) == D and q.stride(3) == 1,
                "q [B,Hq,1,128]")
         b, hq = q.size(0), q.size(1)
@@ -218,6 +221,10 @@ class Module:
             prompt_t = torch.full((b,), int(prompt), dtype=torch.int32, device=q.device)
         tiles_max = fmt.numel() // b
         splits = max(1, -(-maxn // int(per)))
+        if xslot is not None:
+            _check(xslot.dtype == torch.int32 and xslot.is_cuda and xslot.numel() == b * hk and kxc is not None and
+                   vxc is not None and kxc.numel() * kxc.element_size() % KX_BYTES == 0 and
+                   kxc.numel() * kxc.element_size() == vxc.numel() * vxc.element_size(), "exact heads: xslot / KX / VX")
         _check(step.dtype == torch.int64 and step.is_cuda and kcur.stride(3) == 1 and
                entry.dtype == torch.int32 and kinfo.dtype == torch.int32 and count.dtype == torch.int32 and
                slot.dtype == torch.int32 and fmt.dtype == torch.int32 and prompt_t.dtype == torch.int32 and
@@ -238,7 +245,8 @@ class Module:
                        ktail.stride(2), max_tail, _ptr(kc), _ptr(vcur), kc.stride(0), kc.stride(1), _ptr(step),
                        _ptr(out), 0 if out.dtype == torch.float32 else 1, out.stride(0), out.stride(1), _ptr(pm),
                        _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, k8c.size(0),
-                       0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), float(scale),
+                       0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), _ptr(xslot), _ptr(kxc),
+                       _ptr(vxc), 0 if kxc is None else kxc.numel() * kxc.element_size() // KX_BYTES, float(scale),
                        self._stream(q.device))
         return out
 

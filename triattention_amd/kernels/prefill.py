@@ -178,14 +178,13 @@ class Prefill:
                                   ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
                                   scale)
         else:
-            if decode is not None:
-                raise NotImplementedError("decode caches for maps with bf16 heads")
             kx, vx = self.exact_records(batch * nx * rows * KX_BYTES, device)
             self.module.pack_exact(k, v, exact, nx, kx, vx)
             self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
                                   ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
                                   scale, exact=exact, q=q, kx=kx, vx=vx, nx=nx)
         if decode is not None:
+            exact_kv = sorted(set(int(h) for h in self.bands_fn.bf16(layer))) if exact is not None else []
             self.decode_cache.store(layer, t, ops["kp"], ka, kstat, vstat, packed, decode[0], table.host,
-                                    ops["k4"], ka4)
+                                    ops["k4"], ka4, exact_kv, *(self.records if exact is not None else (None, None)))
         return out

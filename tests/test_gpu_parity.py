@@ -130,6 +130,43 @@ def test_decode_long_tail(module):
     _decode_case(module, 500, bands, batch=2, steps=20, max_tail=24, seed=5400)
 
 
+def test_ragged_decode_batch(module):
+    """Ragged cache: four prompts of different lengths stored by separate Prefill calls, served by one
+    decode launch per step; every sequence matches the oracle."""
+    print("\n[parity] ragged decode, prompts 100/700/64/2000", flush=True)
+    hq, hk, max_tail, steps = 8, 2, 4, 3
+    bands = torch.tensor([[INF, INF], [1, INF], [2, 5], [1, 1], [3, INF], [1, 2], [INF, INF], [2, 2]],
+                         dtype=torch.int32)
+    scale = 128 ** -0.5
+    cache = DecodeCache(module, max_tail=max_tail)
+    cache.ragged = True
+    cache.out_dtype = torch.float32
+    prompts = [100, 700, 64, 2000]
+    codes = []
+    for i, n in enumerate(prompts):
+        q, k, v = small(8000 + i, 1, hq, hk, n)
+        run_prefill(module, q, k, v, bands, scale, decode_cache=cache)
+        codes.append(O.prefill_codes(bits(q[0]), bits(k[0]), bits(v[0]), bands.numpy(), decode_cache=True))
+    e = cache.layers[0]
+    assert e["batch"] == len(prompts)
+    per = e["per"]
+    g = S.gen(8100)
+    ktail = np.zeros((len(prompts), hk, max_tail, 128), np.uint16)
+    vtail = np.zeros_like(ktail)
+    dev = torch.device("cuda")
+    for step in range(steps):
+        qd, kd, vd = (S.outlier_tensor(g, len(prompts), hq, 1), S.outlier_tensor(g, len(prompts), hk, 1),
+                      S.outlier_tensor(g, len(prompts), hk, 1))
+        out = cache(0, qd.to(dev), kd.to(dev), vd.to(dev), scale).float().cpu().numpy()
+        for b, n in enumerate(prompts):
+            ref = O.decode(codes[b], bands.numpy(), bits(qd[b, :, 0]), n, per, scale, ktail[b], vtail[b],
+                           bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
+            assert_close(out[b, :, 0], ref, what=f"ragged step {step} seq {b} (prompt {n})")
+            ktail[b, :, step] = bits(kd[b, :, 0])
+            vtail[b, :, step] = bits(vd[b, :, 0])
+        cache.advance()
+
+
 def _attend64(q, keys, values, scale):
     """float64 and float32 attention of one query per head over explicit key/value lists:
     q [Hq,128], keys/values [Hk,L,128] (GQA groups adjacent)."""

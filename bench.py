@@ -7,9 +7,10 @@ token per sequence.  ``value`` = algorithmic HBM bytes of the step / step time
 (GB/s); the step is the split-KV decode kernel plus the merge kernel, inputs
 resident in HBM.  Also reported: tokens/s, the decode kernel's roofline
 (HIP events around that kernel inside the timed region), the CPU oracle timed
-on a bounded sample, and prefill attention TOPS on configs[0] (C0).
+on a bounded sample, prefill attention TOPS on configs[0] and configs[2] (C0, C2),
+and the ragged decode of configs[3] (C3).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-c3]
        python bench.py --copy-probe   (a plain 256 MiB device copy, five times: the
        known-size kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)
 
@@ -82,6 +83,66 @@ def copy_probe():
     print(f"copy probe: 5 x torch.neg over {COPY_PROBE_BYTES} B in, {COPY_PROBE_BYTES} B out", flush=True)
 
 
+def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
+    """one ragged decode step of 64 sequences (Hq 32 / Hk 8) whose prompts of
+    log-uniform length in [512, 32768] sit in one quantized cache.  The prompts' K/V are drawn
+    on the device and stored with Prefill.store_only (quantize + pack, no prompt attention);
+    the timed region is the decode op (split-KV kernel + merge) plus the step advance."""
+    import torch
+    lengths = S.config3_lengths()
+    kinds, bands = S.config3_map()
+    hq, hk = 32, 8
+    log(f"C3: storing {len(lengths)} ragged prompts ({sum(lengths)} tokens)")
+    gdev = torch.Generator(device=dev).manual_seed(1003)
+    cache = DecodeCache(module, max_tail=256)
+    cache.ragged = True
+    pre = Prefill(module, from_bands({"0": bands.tolist()}), cache)
+    for n in lengths:
+        k = S.outlier_tensor_device(gdev, 1, hk, n)
+        v = S.outlier_tensor_device(gdev, 1, hk, n)
+        pre.store_only(0, k, v, hq)
+    del pre
+    torch.cuda.synchronize()
+    e = cache.layers[0]
+    rec_bytes, kept = decode_record_bytes(e)
+    batch = len(lengths)
+    steps, warmup = max(5, args.steps // 2), max(2, args.warmup // 2)
+    toks = [(S.outlier_tensor_device(gdev, batch, hq, 1), S.outlier_tensor_device(gdev, batch, hk, 1),
+             S.outlier_tensor_device(gdev, batch, hk, 1)) for _ in range(steps + warmup)]
+    log(f"C3 cache: {kept} kept tiles, {rec_bytes} record bytes/step, per={e['per']}, maxn={e['maxn']}")
+    for i in range(warmup):
+        cache(0, *toks[i], 128 ** -0.5)
+        cache.advance()
+    out = torch.empty((batch, hq, 1, 128), dtype=torch.bfloat16, device=dev)
+    plan = cache.plan(0, toks[0][0], toks[0][1], out, 128 ** -0.5)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        qd, kd, vd = toks[warmup + i]
+        evs[i][0].record(stream)
+        plan.run(qd, kd, vd, out, 1)
+        evs[i][1].record(stream)
+        plan.run(qd, kd, vd, out, 2)
+        cache.advance()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    dec_ms = statistics.fmean(ev[0].elapsed_time(ev[1]) for ev in evs)
+    log(f"C3 decode step {ms * 1e3:.1f} us (split-KV kernel {dec_ms * 1e3:.1f} us)")
+    return {"workload": "C3 ragged decode: batch 64, Hq 32 / Hk 8, prompts log-uniform in [512, 32768] "
+                        f"(total {sum(lengths)} tokens), KV heads {kinds}",
+            "data": "synthetic, drawn on the device (seeded torch.Generator on cuda)",
+            "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
+            "record_bytes_per_step": rec_bytes, "kept_tiles": kept,
+            "decode_kv_gbs": round(rec_bytes / (ms * 1e-3) / 1e9, 2),
+            "split_kernel_us": round(dec_ms * 1e3, 2),
+            "split_kernel_gbs": round(rec_bytes / (dec_ms * 1e-3) / 1e9, 2),
+            "frac_hbm_peak": round(rec_bytes / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(batch / (ms * 1e-3), 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,6 +152,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seqs", type=int, default=8)
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--no-c3", action="store_true")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
@@ -140,24 +202,40 @@ def main():
     out0 = cache(0, *toks[0], scale).float().cpu()
     cache.advance()
 
-    partials = e[("partials", hq)]
     out = torch.empty((batch, hq, 1, 128), dtype=torch.bfloat16, device=dev)
+
+    plan = cache.plan(0, toks[0][0], toks[0][1], out, scale)
 
     def step(i, ev=None):
         # one decode step: the split-KV kernel, the merge kernel, the step counter update
         qd, kd, vd = toks[i]
-        argsd = (qd, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"], e["slot"],
-                 e["v"][2], e["v"][3], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], kd, vd, cache.step, out,
-                 *partials, e["prompt"], e["per"], scale)
         if ev is None:
-            module.decode(*argsd)
+            plan.run(qd, kd, vd, out)
         else:
             ev[0].record(stream)
-            module.decode(*argsd, phase=1)
+            plan.run(qd, kd, vd, out, 1)
             ev[1].record(stream)
-            module.decode(*argsd, phase=2)
+            plan.run(qd, kd, vd, out, 2)
         cache.advance()
 
+    # A GPU that has been idle runs well below its working clocks until it has carried a compute
+    # load for about a second: a decode step measured 110 us right after setup and 54.5 us after
+    # one second of bf16 GEMMs, steady for the next 30 s, and decode steps alone did not lift it.
+    # So before the W warmup steps: ~1.5 s of untimed GEMMs, then ~0.5 s of decode steps.
+    log("device warm-up: ~1.5 s of bf16 GEMMs and ~0.5 s of untimed decode steps")
+    mat = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 1.5:
+        mat = (mat @ mat).clamp_(-1.0, 1.0)
+        torch.cuda.synchronize()
+    del mat
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.5:
+        for _ in range(200):
+            step(1)
+        torch.cuda.synchronize()
+    # C1 is one token after the prompt: restart the step counter (the bf16 tail length)
+    cache.step.fill_(1)
     log(f"warmup {args.warmup} steps")
     for i in range(1, 1 + args.warmup):
         step(i)
@@ -299,6 +377,10 @@ def main():
         r2["workload"] = (f"C2 prefill: batch 4, Hq 28 / Hk 4, T 8192, log-uniform channel scales, KV heads "
                           f"{c2['kinds']}")
         result["prefill"] = {"C0": r0, "C2": r2}
+
+    # ------------------------------------------------------- C3 ragged decode
+    if not args.no_c3:
+        result["c3_decode"] = c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands)
 
     print(json.dumps(result))
 

@@ -15,6 +15,8 @@ import oracle as O
 from helpers import assert_close, compare_codes, exact_max_abs_bar, exact_reference, oracle_prefill, run_prefill
 from triattention_amd import synthetic as S
 from triattention_amd.kernels.decode import DecodeCache
+from triattention_amd.kernels.prefill import Prefill
+from triattention_amd.maps import from_bands
 from triattention_amd.synthetic import INF, bits
 
 pytestmark = pytest.mark.gpu
@@ -165,6 +167,36 @@ def test_ragged_decode_batch(module):
             ktail[b, :, step] = bits(kd[b, :, 0])
             vtail[b, :, step] = bits(vd[b, :, 0])
         cache.advance()
+
+
+def test_store_only_builds_the_same_cache(module):
+    """Prefill.store_only (no attention launch) stores the same records and metadata as a full Prefill
+    call, and decode returns identical bits from either cache."""
+    print("\n[parity] store_only vs Prefill cache", flush=True)
+    hq, hk, t = 6, 3, 333
+    q, k, v = small(8500, 2, hq, hk, t)
+    bands = torch.tensor([[INF, INF], [1, INF], [2, 5], [1, 1], [3, INF], [2, 2]], dtype=torch.int32)
+    dev = torch.device("cuda")
+    caches = []
+    for full in (True, False):
+        cache = DecodeCache(module, max_tail=4)
+        pre = Prefill(module, from_bands({"0": bands.tolist()}, bf16={"0": [1]}), cache)
+        if full:
+            pre(0, q.to(dev), k.to(dev), v.to(dev), 128 ** -0.5)
+        else:
+            pre.store_only(0, k.to(dev), v.to(dev), hq)
+        caches.append(cache)
+    a, b = (c.layers[0] for c in caches)
+    for key in ("k8", "k4", "ka", "ka4", "kstat", "vstat", "entry", "kinfo", "count", "slot", "fmt", "xslot", "kx",
+                "vx"):
+        assert torch.equal(a[key], b[key]), key
+    for code in a["v"]:
+        assert torch.equal(a["v"][code], b["v"][code])
+    g = S.gen(8600)
+    qd, kd, vd = (S.outlier_tensor(g, 2, hq, 1).to(dev), S.outlier_tensor(g, 2, hk, 1).to(dev),
+                  S.outlier_tensor(g, 2, hk, 1).to(dev))
+    outs = [c(0, qd, kd, vd, 128 ** -0.5) for c in caches]
+    assert torch.equal(outs[0], outs[1])
 
 
 def _attend64(q, keys, values, scale):

@@ -204,11 +204,20 @@ class DecodeCache:
                       torch.empty(n * 128, device=q.device))
         dtype = self.out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=dtype, device=q.device)
-        self.module.decode(q, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"],
-                           e["slot"], e["v"][I8], e["v"][I4], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], k, v,
-                           self.step, out, *e[key], e["prompt"], e["per"], scale, xslot=e["xslot"], kxc=e["kx"],
-                           vxc=e["vx"])
+        self.plan(layer, q, k, out, scale).run(q, k, v, out)
         return out
+
+    def plan(self, layer, q, k, out, scale):
+        """The layer's validated decode call for q / k / out of these shapes (built once, then reused)."""
+        e = self.layers[layer]
+        key = ("plan", tuple(q.shape), q.stride(), tuple(k.shape), k.stride(), out.dtype, out.stride(), float(scale))
+        if key not in e:
+            hq = q.shape[1]
+            e[key] = self.module.plan_decode(
+                q, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"], e["slot"],
+                e["v"][I8], e["v"][I4], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], k, k, self.step, out,
+                *e[("partials", hq)], e["prompt"], e["per"], scale, e["xslot"], e["kx"], e["vx"])
+        return e[key]
 
     def advance(self):
         self.step.add_(1)

@@ -208,6 +208,16 @@ class Module:
         2 only the merge (for per-kernel timing).  ``xslot`` (extension, int32
         [B,Hk], -1 = quantized head) with the KX/VX record arrays ``kxc``/``vxc``
         makes the listed KV heads attend exactly over their bf16 prompt."""
+        plan = self.plan_decode(q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail,
+                                vtail, kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot, kxc, vxc)
+        plan.run(q, kcur, vcur, out, phase)
+        return out
+
+    def plan_decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail,
+                    kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot=None, kxc=None, vxc=None):
+        """Validate and marshal every argument of ``decode`` once (extension).  The returned
+        plan's ``run(q, kcur, vcur, out, phase)`` launches with new q / k / v / out tensors of the
+        planned shapes and strides and the same cache, at a few microseconds of host time."""
         _check(q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(2) == 1 and q.size(3) == D and q.stride(3) == 1,
                "q [B,Hq,1,128]")
         b, hq = q.size(0), q.size(1)
@@ -237,18 +247,17 @@ class Module:
                out.dtype in (torch.bfloat16, torch.float32) and out.stride(3) == 1,
                "decode geometry/buffers")
         kc = kcur.view(b, hk, -1, D) if kcur.dim() == 4 else kcur
-        with torch.cuda.device(q.device):
-            fn = {3: self.lib.tri_decode, 1: self.lib.tri_decode_partials, 2: self.lib.tri_decode_merge}[phase]
-            self._call(fn, _ptr(q), q.stride(0), q.stride(1), _ptr(k8c), _ptr(k4c), _ptr(ka),
-                       _ptr(ka4), _ptr(entry), _ptr(kinfo), _ptr(count), _ptr(fmt), _ptr(slot), _ptr(v8), _ptr(v4),
-                       _ptr(vstat), _ptr(kstat), _ptr(ktail), _ptr(vtail), ktail.stride(0), ktail.stride(1),
-                       ktail.stride(2), max_tail, _ptr(kc), _ptr(vcur), kc.stride(0), kc.stride(1), _ptr(step),
-                       _ptr(out), 0 if out.dtype == torch.float32 else 1, out.stride(0), out.stride(1), _ptr(pm),
-                       _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, k8c.size(0),
-                       0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), _ptr(xslot), _ptr(kxc),
-                       _ptr(vxc), 0 if kxc is None else kxc.numel() * kxc.element_size() // KX_BYTES, float(scale),
-                       self._stream(q.device))
-        return out
+        args = [0, q.stride(0), q.stride(1), _ptr(k8c), _ptr(k4c), _ptr(ka),
+                _ptr(ka4), _ptr(entry), _ptr(kinfo), _ptr(count), _ptr(fmt), _ptr(slot), _ptr(v8), _ptr(v4),
+                _ptr(vstat), _ptr(kstat), _ptr(ktail), _ptr(vtail), ktail.stride(0), ktail.stride(1),
+                ktail.stride(2), max_tail, 0, 0, kc.stride(0), kc.stride(1), _ptr(step),
+                0, 0 if out.dtype == torch.float32 else 1, out.stride(0), out.stride(1), _ptr(pm),
+                _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, k8c.size(0),
+                0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), _ptr(xslot), _ptr(kxc),
+                _ptr(vxc), 0 if kxc is None else kxc.numel() * kxc.element_size() // KX_BYTES, float(scale), 0]
+        keep = (k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, step, pm, pl,
+                po, prompt_t, xslot, kxc, vxc)
+        return DecodePlan(self, args, q, kcur, out, keep)
 
     def decode_occupancy(self) -> int:
         """Resident decode workgroups per compute unit."""
@@ -260,6 +269,37 @@ class Module:
         n = ctypes.c_int(0)
         self._call(self.lib.tri_device_cus, ctypes.byref(n))
         return int(n.value)
+
+
+def _geometry(t):
+    return tuple(t.shape), t.stride(), t.dtype, t.device
+
+
+class DecodePlan:
+    """A validated, marshalled ``decode`` call; ``run`` swaps in the per-step tensors."""
+
+    Q, QSB, QSH, KC, VC, KSB, KSH, OUT, STREAM = 0, 1, 2, 22, 23, 24, 25, 27, 50
+
+    def __init__(self, module, args, q, kcur, out, keep):
+        self.module, self.args, self.keep = module, args, keep
+        self.qgeom, self.cgeom, self.ogeom = _geometry(q), _geometry(kcur), _geometry(out)
+        self.device = q.device
+        self.fns = {3: module.lib.tri_decode, 1: module.lib.tri_decode_partials, 2: module.lib.tri_decode_merge}
+
+    def run(self, q, kcur, vcur, out, phase=3):
+        if _geometry(q) != self.qgeom or _geometry(kcur) != self.cgeom or _geometry(vcur) != self.cgeom or \
+                _geometry(out) != self.ogeom:
+            raise RuntimeError("decode plan: q / k / v / out differ in shape, strides, dtype or device from the plan")
+        a = self.args
+        a[self.Q], a[self.KC], a[self.VC], a[self.OUT] = q.data_ptr(), kcur.data_ptr(), vcur.data_ptr(), out.data_ptr()
+        index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        a[self.STREAM] = torch.cuda.current_stream(index).cuda_stream
+        if torch.cuda.current_device() != index:
+            with torch.cuda.device(index):
+                self.module._call(self.fns[phase], *a)
+        else:
+            self.module._call(self.fns[phase], *a)
+        return out
 
 
 def _only_f16(bands, tiles: int) -> bool:

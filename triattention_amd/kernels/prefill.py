@@ -156,6 +156,19 @@ class Prefill:
         return ops
 
     def __call__(self, layer, q, k, v, scale):
+        return self._run(layer, q, k, v, scale, attend=True)
+
+    def store_only(self, layer, k, v, heads):
+        """Extension: quantize, pack and store K/V of a ``heads``-q-head layer into the decode
+        cache without computing the prompt's attention (the cache is all a caller needs when
+        the prompt outputs are not used).  Q's codes are computed from a zero Q and discarded."""
+        if self.decode_cache is None:
+            raise ValueError("store_only needs a decode cache")
+        batch, _, t, d = k.shape
+        q = torch.zeros((1, 1, 1, d), dtype=k.dtype, device=k.device).expand(batch, heads, t, d)
+        self._run(layer, q, k, v, None, attend=False)
+
+    def _run(self, layer, q, k, v, scale, attend):
         batch, hq, t, _ = q.shape
         hk, rows, device = k.shape[1], (t + 63) // 64, q.device
         table = self.table(layer, hq, hk, rows, device)
@@ -170,19 +183,22 @@ class Prefill:
         self.module.prepare_qk(q, k, ops["q8"], ops["qa"], ops["kp"], ka, ops["partial"], kstat,
                                ops["q4"], ops["qa4"], ops["k4"], ka4)
         self.module.pack_v(v, ops["partial"], vstat, packed[F16], packed[I8], packed[I4])
-        dtype = self.out_dtype or q.dtype
-        out = torch.empty((batch, t, hq, 128), dtype=dtype, device=device).transpose(1, 2)
         exact, nx = self.exact(layer, hq, hk, device)
-        if exact is None:
-            self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
-                                  ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
-                                  scale)
-        else:
+        if exact is not None:
             kx, vx = self.exact_records(batch * nx * rows * KX_BYTES, device)
             self.module.pack_exact(k, v, exact, nx, kx, vx)
-            self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4], vstat,
-                                  ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"], ka4, out,
-                                  scale, exact=exact, q=q, kx=kx, vx=vx, nx=nx)
+        out = None
+        if attend:
+            dtype = self.out_dtype or q.dtype
+            out = torch.empty((batch, t, hq, 128), dtype=dtype, device=device).transpose(1, 2)
+            if exact is None:
+                self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4],
+                                      vstat, ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"],
+                                      ka4, out, scale)
+            else:
+                self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4],
+                                      vstat, ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"],
+                                      ka4, out, scale, exact=exact, q=q, kx=kx, vx=vx, nx=nx)
         if decode is not None:
             exact_kv = sorted(set(int(h) for h in self.bands_fn.bf16(layer))) if exact is not None else []
             self.decode_cache.store(layer, t, ops["kp"], ka, kstat, vstat, packed, decode[0], table.host,

@@ -10,7 +10,8 @@ device, so CPU and GPU runs see identical bits.
   C2  prefill B4, Hq28/Hk4, T8192: per (tensor, head, channel) scale exp(U(0, ln 30));
       one seeded KV head bf16, the others INT8 or INT4 with p = 0.5.
   C3  ragged decode B64, Hq32/Hk8: prompt lengths round(exp(U(ln 512, ln 32768))),
-      per-KV-head Bernoulli(0.5) INT8 / INT4.
+      per-KV-head Bernoulli(0.5) INT8 / INT4.  At full size its prompt K/V are drawn on
+      the device (``outlier_tensor_device``); the parity tests use host draws.
 """
 from __future__ import annotations
 
@@ -100,6 +101,23 @@ def config3_lengths(seed: int = 1003, batch: int = 64, lo: int = 512, hi: int = 
     g = gen(seed)
     u = torch.rand(batch, generator=g, dtype=torch.float64)
     return [int(round(math.exp(math.log(lo) + float(x) * (math.log(hi) - math.log(lo))))) for x in u]
+
+
+def outlier_tensor_device(g: torch.Generator, batch: int, heads: int, t: int, d: int = 128,
+                          factor: float = 20.0, channels: int = 4) -> torch.Tensor:
+    """``outlier_tensor``'s distribution drawn on the generator's device (for full-size
+    configurations whose host generation would take minutes; bits differ from the host draw)."""
+    x = torch.randn(batch, heads, t, d, generator=g, device=g.device)
+    idx = torch.rand(batch, heads, d, generator=g, device=g.device).argsort(-1)[..., :channels]
+    mult = torch.ones(batch, heads, d, device=g.device).scatter_(-1, idx, factor)
+    return (x * mult[:, :, None, :]).to(torch.bfloat16)
+
+
+def config3_map(seed: int = 1003, hq: int = 32, hk: int = 8):
+    """Per-KV-head INT8 / INT4 kinds of config 3 and the q-head bands they give."""
+    g = gen(seed + 7)
+    kinds = ["i8" if float(torch.rand(1, generator=g)) < 0.5 else "i4" for _ in range(hk)]
+    return kinds, kv_head_bands(kinds, hq // hk)
 
 
 def config3(seed: int = 1003, batch: int = 64, hq: int = 32, hk: int = 8, lengths=None):

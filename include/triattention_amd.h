@@ -89,7 +89,7 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * [batch][hk][1][128] (strides c_sb, c_sh); step int64 [1] on the device;
  * out [batch][hq][1][128] (strides o_sb, o_sh), out_dtype 0 = fp32, 1 = bf16;
  * pm/pl f32 [batch][hq][splits], po f32 [batch][hq][splits][128] with
- * splits = max(1, ceil(maxn / per)); n_k8/n_k4/n_v8/n_v4 are the record
+ * splits = max(1, ceil(maxn / per)) with 1 <= per <= 64; n_k8/n_k4/n_v8/n_v4 are the record
  * counts of the compacted arrays (each array below 2 GiB).
  * Exact (bf16) KV heads (extension): xslot NULL, or int32 [batch][hk] with -1
  * for a quantized head and otherwise the index of the head's first KX/VX

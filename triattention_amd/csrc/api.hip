@@ -202,6 +202,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
       !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
     return fail("decode: null buffer");
   if (batch < 1 || hq < 1 || hk < 1 || maxn < 1 || per < 1 || tiles_max < 1) return fail("decode: empty shape");
+  if (per > tri::MAX_PER) return fail("decode: per (tiles per split) must be at most 64");
   if (hq % hk != 0 || hq / hk > tri::MAX_GROUP) return fail("decode: GQA group must divide and be <= 8");
   if (max_tail < 1 || max_tail > tri::MAX_TAIL) return fail("decode: max_tail must be in [1, 1024]");
   if ((k4c == nullptr) != (ka4 == nullptr)) return fail("decode: INT4 K records and scales (all or none)");
@@ -283,20 +284,23 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (phase & 1) {
     const dim3 grid(splits, hk, batch);
-    const int rows = std::min(hq / hk, 4);
+    // groups of up to 4 q-heads use the DUP lane layout (both wave halves on rows 0..3)
+    const int g = hq / hk;
     if (xslot == nullptr) {
-      switch (rows) {
-        case 1: tri::decode_kernel<1><<<grid, 64, 0, s>>>(d); break;
-        case 2: tri::decode_kernel<2><<<grid, 64, 0, s>>>(d); break;
-        case 3: tri::decode_kernel<3><<<grid, 64, 0, s>>>(d); break;
-        default: tri::decode_kernel<4><<<grid, 64, 0, s>>>(d); break;
+      switch (g) {
+        case 1: tri::decode_kernel<1, false, true><<<grid, 64, 0, s>>>(d); break;
+        case 2: tri::decode_kernel<2, false, true><<<grid, 64, 0, s>>>(d); break;
+        case 3: tri::decode_kernel<3, false, true><<<grid, 64, 0, s>>>(d); break;
+        case 4: tri::decode_kernel<4, false, true><<<grid, 64, 0, s>>>(d); break;
+        default: tri::decode_kernel<4, false, false><<<grid, 64, 0, s>>>(d); break;
       }
     } else {
-      switch (rows) {
-        case 1: tri::decode_kernel<1, true><<<grid, 64, 0, s>>>(d); break;
-        case 2: tri::decode_kernel<2, true><<<grid, 64, 0, s>>>(d); break;
-        case 3: tri::decode_kernel<3, true><<<grid, 64, 0, s>>>(d); break;
-        default: tri::decode_kernel<4, true><<<grid, 64, 0, s>>>(d); break;
+      switch (g) {
+        case 1: tri::decode_kernel<1, true, true><<<grid, 64, 0, s>>>(d); break;
+        case 2: tri::decode_kernel<2, true, true><<<grid, 64, 0, s>>>(d); break;
+        case 3: tri::decode_kernel<3, true, true><<<grid, 64, 0, s>>>(d); break;
+        case 4: tri::decode_kernel<4, true, true><<<grid, 64, 0, s>>>(d); break;
+        default: tri::decode_kernel<4, true, false><<<grid, 64, 0, s>>>(d); break;
       }
     }
   }
@@ -326,7 +330,7 @@ int tri_decode_occupancy(int* blocks) {
   g_error.clear();
   if (!blocks) return fail("decode_occupancy: null output");
   int n = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, tri::decode_kernel<4>, 64, 0);
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, tri::decode_kernel<4, false, false>, 64, 0);
   if (e != hipSuccess) return fail("decode_occupancy: %s", hipGetErrorString(e));
   *blocks = n;
   return 0;

@@ -3,19 +3,22 @@
 // Record layouts (one record = one 64-key tile of one KV head).  Sizes match the
 // reference's record word counts (triattention/kernels/decode.py:7-8,
 // cuda/prefill_sm80.cu:17-22); the byte order inside a record is chosen so that
-// each 1 KiB (512 B for 4-bit records) "fragment" is exactly one operand of a
-// 32x32 MFMA, loaded with one 16-byte (8-byte) access per lane:
+// each 1 KiB "fragment" is exactly one operand of a 32x32 MFMA, loaded with one
+// 16-byte access per lane (4-bit records pair two fragments per 16 bytes):
 //
 //   K8  8192 B  fragment F = kb*4 + ks (kb: 32-key block, ks: 32-feature step)
 //               lane L byte j  <->  key kb*32 + L%32, feature ks*32 + 16*(L/32) + j
-//   K4  4096 B  fragment F (512 B), lane L holds words w0,w1; K8-layout byte j is
+//   K4  4096 B  the 4-bit codes of the K8 layout; fragment F's lane L word pair
+//               (w0, w1) sits at byte (F/2)*1024 + 16*L + 8*(F%2), so one 16-byte
+//               access per lane fetches fragments 2P and 2P+1.  K8-layout byte j is
 //               the low nibble of w0 byte j (j<4), high nibble of w0 byte j-4 (j<8),
 //               low nibble of w1 byte j-8 (j<12), high nibble of w1 byte j-12.
 //   V8  8192 B  fragment F = cb*2 + kb (cb: 32-channel block, kb: 32-key block)
 //               lane L byte p  <->  key kb*32 + 8*(p/4) + 4*(L/32) + p%4, channel cb*32 + L%32
 //   V16 16384 B fragment F = (cb*2 + kb)*2 + kh, lane L fp16 element e (0..7)
 //               <->  key kb*32 + 8*(2*kh + e/4) + 4*(L/32) + e%4, channel cb*32 + L%32
-//   V4  4096 B  fragment F = cb*2 + kb (512 B), nibbles of the V8 layout packed as K4.
+//   V4  4096 B  nibbles of the V8 layout placed as in K4 (fragment F = cb*2 + kb, so
+//               16 bytes of lane L hold both 32-key blocks of channel block cb).
 //
 // The V orders equal the accumulator order of the QK^T MFMA (key = row of the
 // 32x32 result), so a lane's probabilities feed the PV MFMA without shuffles.
@@ -97,11 +100,12 @@ __device__ __forceinline__ float texp2_p(float x) {
   return __builtin_amdgcn_ldexpf(p, (int)n);
 }
 
-// Sign pattern of the 128-channel rotation (prefill_sm80.cu:95).
-__device__ __forceinline__ bool rot_sign(int c) {
-  const uint32_t s = c < 32 ? 0x9a3b5e71u : c < 64 ? 0x2c6d8f13u : c < 96 ? 0xe41b7a95u : 0x5f02c3d8u;
-  return (s >> (c & 31)) & 1u;
+// Sign pattern of the 128-channel rotation (prefill_sm80.cu:95): bit c & 31 of
+// word c >> 5 flips channel c.
+__device__ __forceinline__ uint32_t rot_word(int w) {
+  return w == 0 ? 0x9a3b5e71u : w == 1 ? 0x2c6d8f13u : w == 2 ? 0xe41b7a95u : 0x5f02c3d8u;
 }
+__device__ __forceinline__ bool rot_sign(int c) { return (rot_word(c >> 5) >> (c & 31)) & 1u; }
 
 // Rotation of one 128-vector held by 32 consecutive lanes, 4 channels each
 // (channel 4*l + i in lane l of the 32-lane group).  Butterfly stages run over
@@ -125,10 +129,86 @@ __device__ __forceinline__ void rotate128_x4(float (&x)[4], int l32) {
   for (int i = 0; i < 4; ++i) x[i] *= 0.08838834764831845f;
 }
 
+// DPP lane moves within 16-lane rows: quad_perm [1,0,3,2] (lane ^ 1), quad_perm
+// [2,3,0,1] (lane ^ 2), quad_perm [3,2,1,0] (lane ^ 3), row_half_mirror (lane
+// 7 - i of each 8), row_mirror (lane 15 - i of each 16).  VALU operations,
+// unlike __shfl_xor's LDS permute.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// the value of lane ^ BIT, BIT in {1, 2, 4}: lane ^ 4 is the half-row mirror
+// (lane ^ 7) of the quad reversal (lane ^ 3)
+template <int BIT>
+__device__ __forceinline__ float lane_xor8(float v) {
+  if constexpr (BIT == 1) return dpp_move<0xB1>(v);
+  else if constexpr (BIT == 2) return dpp_move<0x4E>(v);
+  else return dpp_move<0x141>(dpp_move<0x1B>(v));
+}
+
+// one cross-lane butterfly stage over lane bit BIT of an 8-lane group
+template <int BIT>
+__device__ __forceinline__ void rot_stage8(float (&x)[16], int t) {
+  const bool upper = t & BIT;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float y = lane_xor8<BIT>(x[i]);
+    x[i] = upper ? y - x[i] : x[i] + y;
+  }
+}
+
+// Rotation of one 128-vector held by 8 consecutive lanes, 16 channels each
+// (channel 16*t + i in lane t of the 8-lane group): the same butterfly stages,
+// in the same order and with the same operands, as rotate128_x4, so the
+// results are identical.  Cross-lane stages are DPP moves.
+__device__ __forceinline__ void rotate128_x16(float (&x)[16], int t) {
+  const uint32_t sg = rot_word(t >> 1) >> (16 * (t & 1));
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if ((sg >> i) & 1u) x[i] = -x[i];
+#pragma unroll
+  for (int bit = 1; bit < 16; bit <<= 1)
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (!(i & bit)) {
+        const float lo = x[i], hi = x[i | bit];
+        x[i] = lo + hi;
+        x[i | bit] = lo - hi;
+      }
+  rot_stage8<1>(x, t);
+  rot_stage8<2>(x, t);
+  rot_stage8<4>(x, t);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] *= 0.08838834764831845f;
+}
+
+// maximum over each group of 8 consecutive lanes
+__device__ __forceinline__ float lanes8_max(float m) {
+  m = fmaxf(m, lane_xor8<1>(m));
+  m = fmaxf(m, lane_xor8<2>(m));
+  return fmaxf(m, lane_xor8<4>(m));
+}
+
 __device__ __forceinline__ float warp32_max(float m) {
 #pragma unroll
   for (int o = 16; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
   return m;
+}
+
+
+// Maximum over each 32-lane half of the wave (LANES = 32) or over the whole wave
+// (LANES = 64), in every lane: four DPP steps reduce each 16-lane row (after the
+// quad steps every lane holds its quad's maximum, the half mirror pairs quads,
+// the mirror pairs 8-lane halves), then one or two lane-xor exchanges.
+template <int LANES>
+__device__ __forceinline__ float lanes_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  v = fmaxf(v, dpp_move<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if constexpr (LANES == 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
 }
 
 // byte 1 of each of four words, packed (P levels out of the 49152.5 magic).

@@ -47,6 +47,7 @@ struct DecodeArgs {
 };
 
 constexpr int MAX_TAIL = 1024;
+constexpr int MAX_PER = 64;  // kept tiles per split: one per lane of the wave's metadata
 
 __device__ __forceinline__ v4i unpack16(v4i w) {
   return v4i{(int)nib_lo16((uint32_t)w[0]), (int)nib_hi16((uint32_t)w[0]), (int)nib_lo16((uint32_t)w[1]),
@@ -172,15 +173,34 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
 
 // R: q-head rows per lane half (min(group, 4)); EXACT: the launch holds exact
 // (bf16) KV heads, whose path is compiled in only then (it needs 2 waves/SIMD).
-template <int R, bool EXACT = false, int W = (R == 1 && !EXACT ? 3 : 2)>
+// DUP (groups of at most 4 q-heads): the score rows 4..7 of the QK MFMA do not
+// exist, so the upper half of the wave takes the tile's second 32-key block
+// for rows 0..3 instead, and every lane carries R scores rather than 2R.
+template <int R, bool EXACT = false, bool DUP = false, int W = (EXACT || R >= 3 ? 2 : 3)>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
   __shared__ __align__(16) int8_t q8s[MAX_GROUP][D];
   __shared__ __align__(16) int8_t q4s[MAX_GROUP][D];
   __shared__ float qsc[MAX_GROUP], qsc4[MAX_GROUP];
   __shared__ __align__(16) uint8_t pls[MAX_GROUP][BN];
   __shared__ __align__(16) float rsc[4][MAX_GROUP];  // alpha, base, bq, restore per row
+  __shared__ __align__(16) int4 meta[MAX_PER + 1];     // per-tile record offsets and flags
+  __shared__ __align__(16) float4 metk[MAX_PER + 1];   // per-tile K group scales
 
-  const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id; XCD x takes
+  // the x-th contiguous eighth of the (sequence, KV head, split) space, so each
+  // XCD gets every split position (the last splits hold the INT8-V tiles, and
+  // split = id % 8 would load one XCD with all of them).
+  int split, kh, b;
+  {
+    const int nsplit = gridDim.x, nkh = gridDim.y;
+    const int total = nsplit * nkh * gridDim.z;
+    const int lin = blockIdx.x + nsplit * (blockIdx.y + nkh * blockIdx.z);
+    const int q8 = total >> 3, r8 = total & 7, x = lin & 7;
+    const int w = x * q8 + min(x, r8) + (lin >> 3);
+    split = w % nsplit;
+    kh = (w / nsplit) % nkh;
+    b = w / (nsplit * nkh);
+  }
   if constexpr (EXACT) {
     if (a.xslot[(int64_t)b * a.hk + kh] >= 0) {
       decode_exact(a, b, kh, split);
@@ -193,42 +213,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   const int64_t hb = (int64_t)b * a.hk + kh;
   const int cnt = a.count[hb], first = split * a.per, last = min(cnt, first + a.per);
 
-  // ---- in-kernel Q quantization of the g rows (common_device.cuh:291-315)
+  // The g query rows are loaded first, one row per 8 lanes, 16 channels per
+  // lane (the padding rows load row g - 1, so every lane issues the same
+  // loads); quantization waits for them only after the first tile's record
+  // loads are in flight.
+  const int qrw = L >> 3, qt = L & 7;
+  uint2 qraw[4];
+  {
+    const uint16_t* qp = a.q + b * a.qsb + (int64_t)(kh * g + min(qrw, g - 1)) * a.qsh + qt * 16;
 #pragma unroll
-  for (int it = 0; it < MAX_GROUP / 2; ++it) {
-    const int r = it * 2 + half;
-    float xv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (r < g) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(a.q + b * a.qsb + (int64_t)(kh * g + r) * a.qsh + lq * 4);
-      xv[0] = bf16f(raw.x & 0xffffu); xv[1] = bf16f(raw.x >> 16);
-      xv[2] = bf16f(raw.y & 0xffffu); xv[3] = bf16f(raw.y >> 16);
-    }
-    rotate128_x4(xv, lq);
-    float mx = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(xv[i]));
-    mx = warp32_max(mx);
-    const float inv = mx > 0.f ? 127.f / mx : 0.f, inv4 = mx > 0.f ? 7.f / mx : 0.f;
-    uint32_t w8 = 0, w4 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      w8 |= ((uint32_t)(int)__builtin_rintf(xv[i] * inv) & 0xffu) << (8 * i);
-      const int c4 = (((int)__builtin_rintf(xv[i] * inv4) & 0xf) ^ 8) - 8;
-      w4 |= ((uint32_t)c4 & 0xffu) << (8 * i);
-    }
-    *reinterpret_cast<uint32_t*>(&q8s[r][lq * 4]) = r < g ? w8 : 0u;
-    *reinterpret_cast<uint32_t*>(&q4s[r][lq * 4]) = r < g ? w4 : 0u;
-    if (lq == 0) {
-      qsc[r] = (r < g && mx > 0.f) ? mx / 127.f * a.sm_log2 : 1.17549435e-38f;
-      qsc4[r] = (r < g && mx > 0.f) ? mx / 7.f * a.sm_log2 : 1.17549435e-38f;
-    }
+    for (int i = 0; i < 4; ++i) qraw[i] = *reinterpret_cast<const uint2*>(qp + 4 * i);
   }
-  for (int i = L; i < MAX_GROUP * BN / 4; i += 64) reinterpret_cast<uint32_t*>(&pls[0][0])[i] = 0u;
-  __syncthreads();
-
-  // rows of this lane: 4*half + r (r < R); the owner row of this lane's scalar work: 4*half + (L & 3)
-  const int orow = 4 * half + (L & 3);
-  const bool owner = (L & 3) < R;
+  // rows of this lane: 4*half + r (r < R), or r with DUP; the owner row of this
+  // lane's scalar work: 4*half + (L & 3), or L & 3 with DUP (lower half writes it)
+  constexpr int NK = DUP ? 1 : 2;  // 32-key blocks per lane
+  const int orow = DUP ? (L & 3) : 4 * half + (L & 3);
+  const bool owner = (L & 3) < R && (!DUP || half == 0);
+  auto qrow = [&](int r) { return DUP ? r : 4 * half + r; };
   float m_o = -3.402823466e38f;
   float den[R], acc[4][R];
 #pragma unroll
@@ -246,56 +247,129 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   const __amdgpu_buffer_rsrc_t rv4 = __builtin_amdgcn_make_buffer_rsrc((void*)a.v4c, (short)0, a.v4_bytes, 0x00020000);
   v4i kf[8], vf8[8];
   float kav[2], kmax = 0.f;
-  // Scalar metadata of an entry; fetched two entries ahead of use so that the
-  // record loads never wait on it.
+  // Per-tile metadata of this split in LDS: lane L loads entry first + L with
+  // vector loads in the prologue (at most 64 entries per split; entries past
+  // the end hold record offsets beyond every record array, whose loads return
+  // zeros without touching memory).  Scalar loads return out of order, so any
+  // use of one waits for every outstanding scalar and LDS access; per-tile
+  // scalar loads would stall every tile on the metadata of the tiles after it.
+  constexpr int OUT_OF_RANGE = (int)0x80000000u;  // >= any record array size (< 2 GiB)
+  // Entry first + L of the split (clamped into the entry table, so every lane
+  // loads; the tile index is clamped too, as entries past the count are not
+  // tiles); lanes past the split's end get the out-of-range offsets.
+  int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);  // koff, voff, info | v8 << 9 | j << 10
+  float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
+  {
+    const bool valid = L < last - first;
+    // (independent of the split's entry count, so these loads need not wait for it)
+    const int64_t li = mbase + min(first + min(L, a.per - 1), a.maxn - 1);
+    const int info = a.kinfo[li], j = min(max(a.entry[li], 0), a.tiles_max - 1), vs = a.slot[li];
+    const int is4 = valid ? (info >> 8) & 1 : 0;
+    const int vf = a.fmt[(int64_t)b * a.tiles_max + j];
+    const float4 kl = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
+    if (valid) {
+      ka = kl;
+      w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
+      w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
+      w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
+    }
+    meta[L] = w;
+    metk[L] = ka;
+    if (L == 0) {
+      meta[MAX_PER] = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);
+      metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+  }
   struct Meta {
-    int info, j, vs, vf;
+    int info, j, vf, koff, voff;
   };
-  auto fetch = [&](int e) {
+  auto unpack = [](const int4& v) {
     Meta m;
-    m.info = a.kinfo[mbase + e];
-    m.j = a.entry[mbase + e];
-    m.vs = a.slot[mbase + e];
-    m.vf = a.fmt[(int64_t)b * a.tiles_max + m.j];
+    m.koff = __builtin_amdgcn_readfirstlane(v.x);
+    m.voff = __builtin_amdgcn_readfirstlane(v.y);
+    const int z = __builtin_amdgcn_readfirstlane(v.z);
+    m.info = z & 0x1ff;
+    m.vf = ((z >> 9) & 1) ? 1 : 2;
+    m.j = (int)((unsigned)z >> 10);
     return m;
   };
+  auto fetch = [&](int e) { return unpack(meta[min(e - first, MAX_PER)]); };
+  auto k_scales = [&](int e) {
+    const float4 s4 = metk[min(e - first, MAX_PER)];
+    kmax = fmaxf(fmaxf(s4.x, s4.y), fmaxf(s4.z, s4.w));
+    kav[0] = (lq >> 4) ? s4.y : s4.x;
+    kav[1] = (lq >> 4) ? s4.w : s4.z;
+  };
   auto load_k = [&](const Meta& m) {
-    const int is4 = (m.info >> 8) & 1, kslot = (int)((unsigned)m.info >> 9);
-    const float4 k4s = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + m.j) * 4);
-    kmax = fmaxf(fmaxf(k4s.x, k4s.y), fmaxf(k4s.z, k4s.w));
-    kav[0] = (lq >> 4) ? k4s.y : k4s.x;
-    kav[1] = (lq >> 4) ? k4s.w : k4s.z;
-    if (is4) {
+    const int is4 = (m.info >> 8) & 1;
+    // The same eight 16-byte loads for either width (a per-format load sequence
+    // would make the compiler wait for every outstanding load at each tile): a
+    // K8 record is fragments 0..7; a K4 record is four fragment pairs, and the
+    // upper four loads are past the end of the range (zeros, no memory access).
+    const __amdgpu_buffer_rsrc_t rk = is4 ? rk4 : rk8;
+    const int hi = is4 ? OUT_OF_RANGE : m.koff;
 #pragma unroll
-      for (int F = 0; F < 8; ++F) {
-        const v2i w = __builtin_amdgcn_raw_buffer_load_b64(rk4, L * 8 + F * 512, kslot * K4_BYTES, 0);
-        kf[F] = v4i{w[0], w[1], 0, 0};
-      }
-    } else {
-#pragma unroll
-      for (int F = 0; F < 8; ++F) kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk8, L * 16 + F * 1024, kslot * K8_BYTES, 0);
-    }
+    for (int F = 0; F < 8; ++F) kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, L * 16 + F * 1024, F < 4 ? m.koff : hi, 0);
   };
   auto load_v = [&](const Meta& m) {
-    if (m.vf == 1) {
+    const bool v4 = m.vf != 1;
+    const __amdgpu_buffer_rsrc_t rv = v4 ? rv4 : rv8;
+    const int hi = v4 ? OUT_OF_RANGE : m.voff;
 #pragma unroll
-      for (int F = 0; F < 8; ++F) vf8[F] = __builtin_amdgcn_raw_buffer_load_b128(rv8, L * 16 + F * 1024, m.vs * V8_BYTES, 0);
-    } else {
-#pragma unroll
-      for (int F = 0; F < 8; ++F) {
-        const v2i w = __builtin_amdgcn_raw_buffer_load_b64(rv4, L * 8 + F * 512, m.vs * V4_BYTES, 0);
-        vf8[F] = v4i{w[0], w[1], 0, 0};
-      }
-    }
+    for (int F = 0; F < 8; ++F) vf8[F] = __builtin_amdgcn_raw_buffer_load_b128(rv, L * 16 + F * 1024, F < 4 ? m.voff : hi, 0);
+  };
+  // fragment f of a 4-bit record: half (f & 1) of load f >> 1, expanded to 16*code bytes
+  auto frag4 = [](const v4i (&w)[8], int f) {
+    const v4i p = w[f >> 1];
+    return (f & 1) ? unpack16(v4i{p[2], p[3], 0, 0}) : unpack16(p);
   };
 
-  Meta mc = {0, 0, 0, 1}, mn = mc;
-  if (first < last) {
-    mc = fetch(first);
-    load_k(mc);
-    load_v(mc);
-    mn = first + 1 < last ? fetch(first + 1) : mc;
+  // the first tile's records stream while Q is quantized (lane 0 holds its entry)
+  Meta mc = unpack(w);
+  load_k(mc);
+  load_v(mc);
+
+  // ---- in-kernel Q quantization of the g rows (common_device.cuh:291-315)
+  {
+    float xv[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint2 raw = qraw[i];
+      xv[4 * i] = bf16f(raw.x & 0xffffu); xv[4 * i + 1] = bf16f(raw.x >> 16);
+      xv[4 * i + 2] = bf16f(raw.y & 0xffffu); xv[4 * i + 3] = bf16f(raw.y >> 16);
+    }
+    rotate128_x16(xv, qt);
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(xv[i]));
+    mx = lanes8_max(mx);
+    const bool live = qrw < g;
+    const float inv = mx > 0.f ? 127.f / mx : 0.f, inv4 = mx > 0.f ? 7.f / mx : 0.f;
+    uint32_t w8[4], w4[4];
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd) {
+      w8[wd] = 0u;
+      w4[wd] = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = xv[4 * wd + i];
+        w8[wd] |= ((uint32_t)(int)__builtin_rintf(x * inv) & 0xffu) << (8 * i);
+        const int c4 = (((int)__builtin_rintf(x * inv4) & 0xf) ^ 8) - 8;
+        w4[wd] |= ((uint32_t)c4 & 0xffu) << (8 * i);
+      }
+      if (!live) w8[wd] = w4[wd] = 0u;
+    }
+    *reinterpret_cast<uint4*>(&q8s[qrw][qt * 16]) = make_uint4(w8[0], w8[1], w8[2], w8[3]);
+    *reinterpret_cast<uint4*>(&q4s[qrw][qt * 16]) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    if (qt == 0) {
+      qsc[qrw] = (live && mx > 0.f) ? mx / 127.f * a.sm_log2 : 1.17549435e-38f;
+      qsc4[qrw] = (live && mx > 0.f) ? mx / 7.f * a.sm_log2 : 1.17549435e-38f;
+    }
   }
+  for (int i = L; i < MAX_GROUP * BN / 4; i += 64) reinterpret_cast<uint32_t*>(&pls[0][0])[i] = 0u;
+  __syncthreads();
+  k_scales(first);
+  Meta mn = fetch(first + 1);
   for (int e = first; e < last; ++e) {
     const int info = mc.info;
     const int is4 = (info >> 8) & 1;
@@ -309,7 +383,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       v4i z = {0, 0, 0, 0};
-      qa[ks] = lq < MAX_GROUP ? *reinterpret_cast<const v4i*>(qsrc + lq * D + ks * 32 + 16 * half) : z;
+      // A-operand row lq is q-head lq; with DUP rows 4..7 repeat q-heads 0..3, so the upper
+      // half of the result holds rows 0..3 against the second key block
+      const int qr = DUP ? (lq & 3) : lq;
+      qa[ks] = lq < MAX_GROUP ? *reinterpret_cast<const v4i*>(qsrc + qr * D + ks * 32 + 16 * half) : z;
     }
     v16i s[2];
 #pragma unroll
@@ -317,32 +394,38 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s[kb] = mfma_i8(qa[ks], is4 ? unpack16(kf[kb * 4 + ks]) : kf[kb * 4 + ks], s[kb]);
+      for (int ks = 0; ks < 4; ++ks) s[kb] = mfma_i8(qa[ks], is4 ? frag4(kf, kb * 4 + ks) : kf[kb * 4 + ks], s[kb]);
     }
-    int dot[R][2];
+    int dot[R][NK];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) dot[r][kb] = is4 ? (s[kb][r] >> 4) : s[kb][r];
+      for (int t = 0; t < NK; ++t) {
+        const int v = DUP ? (half ? s[1][r] : s[0][r]) : s[t][r];
+        dot[r][t] = is4 ? (v >> 4) : v;
+      }
     const float kv0 = kav[0], kv1 = kav[1];
-    if (e + 1 < last) load_k(mn);  // K registers are free again
-    const float kavc[2] = {kv0, kv1};
-    bool ok[R][2];
-    float slope[R][2], trow[R];
+    load_k(mn);  // K registers are free again (past the end: no memory access)
+    k_scales(e + 1);
+    float kavc[NK];
+    if constexpr (DUP) kavc[0] = half ? kv1 : kv0;
+    else { kavc[0] = kv0; kavc[NK - 1] = kv1; }
+    bool ok[R][NK];
+    float slope[R][NK], trow[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int q = 4 * half + r;
+      const int q = qrow(r);
       const bool on = q < g && ((rowmask >> q) & 1u);
       const float qs = is4 ? qsc4[q] : qsc[q];
       trow[r] = -__builtin_inff();
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        ok[r][kb] = on && (j * BN + kb * 32 + lq < prompt);
-        slope[r][kb] = qs * kavc[kb];
-        if (ok[r][kb]) trow[r] = fmaxf(trow[r], slope[r][kb] * (float)dot[r][kb]);
+      for (int t = 0; t < NK; ++t) {
+        const int kb = DUP ? half : t;
+        ok[r][t] = on && (j * BN + kb * 32 + lq < prompt);
+        slope[r][t] = qs * kavc[t];
+        if (ok[r][t]) trow[r] = fmaxf(trow[r], slope[r][t] * (float)dot[r][t]);
       }
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) trow[r] = fmaxf(trow[r], __shfl_xor(trow[r], o, 64));
+      trow[r] = lanes_max<DUP ? 64 : 32>(trow[r]);
     }
     // ---- per-row scalars on the owner lane (common_device.cuh:222-238)
     const float levels = vf == 1 ? 255.f : 15.f;
@@ -369,10 +452,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
     float alpha[R], base[R], bq[R], restore[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      alpha[r] = rsc[0][4 * half + r];
-      base[r] = rsc[1][4 * half + r];
-      bq[r] = rsc[2][4 * half + r];
-      restore[r] = rsc[3][4 * half + r];
+      alpha[r] = rsc[0][qrow(r)];
+      base[r] = rsc[1][qrow(r)];
+      bq[r] = rsc[2][qrow(r)];
+      restore[r] = rsc[3][qrow(r)];
     }
     bool rescale = false;
 #pragma unroll
@@ -390,20 +473,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
     for (int r = 0; r < R; ++r) {
       uint32_t psum = 0;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int d = dot[r][kb];
+      for (int t = 0; t < NK; ++t) {
+        const int kb = DUP ? half : t;
+        const int d = dot[r][t];
         float arg = -__builtin_inff();
         uint32_t dith = 0x47400000u;
-        if (ok[r][kb]) {
-          const float c = is4 ? -base[r] : (-slope[r][kb] * MAGIC) - base[r];
-          arg = is4 ? __builtin_fmaf(slope[r][kb], (float)d, c)
-                    : __builtin_fmaf(slope[r][kb], __uint_as_float(MAGIC_BITS + (uint32_t)d), c);
+        if (ok[r][t]) {
+          const float c = is4 ? -base[r] : (-slope[r][t] * MAGIC) - base[r];
+          arg = is4 ? __builtin_fmaf(slope[r][t], (float)d, c)
+                    : __builtin_fmaf(slope[r][t], __uint_as_float(MAGIC_BITS + (uint32_t)d), c);
           dith |= (uint32_t)d & 0xffu;
         }
         const uint32_t y = __float_as_uint(__builtin_fmaf(texp2(arg), levels, __uint_as_float(dith)));
         const uint32_t p = (y >> 8) & 0xffu;
         psum += p;
-        pls[4 * half + r][kb * 32 + lq] = (uint8_t)p;
+        pls[qrow(r)][kb * 32 + lq] = (uint8_t)p;
       }
       den[r] = __builtin_fmaf((float)psum, bq[r], den[r]);
     }
@@ -419,7 +503,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       }
       pa[kb] = w;
     }
-    const Meta mnn = e + 2 < last ? fetch(e + 2) : mn;
+    const Meta mnn = fetch(e + 2);
     if (vf == 1) {
       const v4i neg127 = {(int)0x81818181u, (int)0x81818181u, (int)0x81818181u, (int)0x81818181u};
       const v4i p0 = pa[0] ^ 0x7f7f7f7f, p1 = pa[1] ^ 0x7f7f7f7f;  // 127 - P as s8
@@ -437,13 +521,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
         v16i d = {};
-        d = mfma_i8(pa[0], unpack16(vf8[cb * 2]), d);
-        d = mfma_i8(pa[1], unpack16(vf8[cb * 2 + 1]), d);  // = 16 * sum_k P v
+        d = mfma_i8(pa[0], frag4(vf8, cb * 2), d);
+        d = mfma_i8(pa[1], frag4(vf8, cb * 2 + 1), d);  // = 16 * sum_k P v
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[cb][r] = __builtin_fmaf((float)(d[r] >> 4), restore[r], acc[cb][r]);
       }
     }
-    if (e + 1 < last) load_v(mn);  // V registers are free again
+    load_v(mn);  // V registers are free again
     mc = mn;
     mn = mnn;
   }
@@ -453,7 +537,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int o = 1; o < 32; o <<= 1) den[r] += __shfl_xor(den[r], o, 64);
+    for (int o = 1; o < (DUP ? 64 : 32); o <<= 1) den[r] += __shfl_xor(den[r], o, 64);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int q = 4 * half + r;

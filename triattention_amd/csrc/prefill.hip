@@ -56,8 +56,9 @@ __device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, __shfl_xor
 template <int KIND>
 __device__ __forceinline__ v4i k_frag(const uint8_t* __restrict__ k_lds, int F, int L) {
   if constexpr (KIND == KQ4) {
-    // packed 4-bit record in LDS: unpack this lane's 8 bytes to 16 bytes of 16*code
-    const uint2 w = *reinterpret_cast<const uint2*>(k_lds + F * 512 + L * 8);
+    // packed 4-bit record in LDS (fragments 2P and 2P+1 share lane L's 16 bytes at
+    // P*1024 + 16L): unpack this lane's 8 bytes to 16 bytes of 16*code
+    const uint2 w = *reinterpret_cast<const uint2*>(k_lds + (F >> 1) * 1024 + L * 16 + (F & 1) * 8);
     return v4i{(int)nib_lo16(w.x), (int)nib_hi16(w.x), (int)nib_lo16(w.y), (int)nib_hi16(w.y)};
   } else {
     return *reinterpret_cast<const v4i*>(k_lds + F * 1024 + L * 16);

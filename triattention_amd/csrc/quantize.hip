@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restr
     const int key = kb * 32 + (L & 31), f0 = ks * 32 + 16 * (L >> 5);
     const uint4 n = *reinterpret_cast<const uint4*>(&c4[key][f0]);  // one nibble value per byte
     const uint32_t w0 = n.x | (n.y << 4), w1 = n.z | (n.w << 4);
-    *reinterpret_cast<uint2*>(rec4 + F * 512 + L * 8) = make_uint2(w0, w1);
+    *reinterpret_cast<uint2*>(rec4 + (F >> 1) * 1024 + L * 16 + (F & 1) * 8) = make_uint2(w0, w1);
   }
 }
 
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict_
     }
     if (v8 != nullptr) *reinterpret_cast<uint4*>(v8 + rec * V8_BYTES + F * 1024 + L * 16) = make_uint4(b8[0], b8[1], b8[2], b8[3]);
     if (v4 != nullptr)
-      *reinterpret_cast<uint2*>(v4 + rec * V4_BYTES + F * 512 + L * 8) =
+      *reinterpret_cast<uint2*>(v4 + rec * V4_BYTES + (F >> 1) * 1024 + L * 16 + (F & 1) * 8) =
           make_uint2(b4[0] | (b4[1] << 4), b4[2] | (b4[3] << 4));
   }
 }

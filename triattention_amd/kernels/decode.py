@@ -183,7 +183,8 @@ class DecodeCache:
         cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
             torch.cuda.get_device_properties(device).multi_processor_count
         wave = cus * max(1, self.module.decode_occupancy())
-        per = max(1, -(-int(count.sum()) // wave))
+        # split size (decode.py:54-55); the kernel takes at most 64 tiles per split
+        per = min(64, max(1, -(-int(count.sum()) // wave)))
         to = lambda x: x.to(torch.int32).to(device)
         tail_k = torch.zeros((total, hk, self.max_tail, 128), dtype=torch.bfloat16, device=device)
         return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, fmt=to(fmt), slot=to(slot), entry=to(entry),

@@ -37,10 +37,14 @@ def _v16_index():
 
 
 def _nibble_index():
-    """For each byte of a 4-bit record: the 8-bit-layout byte of its low and high nibble."""
+    """For each byte of a 4-bit record: the 8-bit-layout byte of its low and high nibble.
+
+    Fragment F's 8-byte word pair of lane L sits at byte (F // 2) * 1024 + 16 L + 8 (F % 2),
+    so one 16-byte access per lane fetches two fragments."""
     o = np.arange(4096)
-    slot, bb = o // 8, o % 8
-    base = slot * 16
+    F = 2 * (o // 1024) + (o % 16) // 8
+    L, bb = (o // 16) % 64, o % 8
+    base = F * 1024 + L * 16
     lo = np.where(bb < 4, bb, 8 + (bb - 4))
     return base + lo, base + lo + 4
 

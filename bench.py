@@ -13,6 +13,7 @@ on a bounded sample, prefill attention TOPS on configs[0] and configs[2] (C0, C2
 and the ragged decode of configs[3] (C3).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-c3]
+       python bench.py --c4   (configs[4]: end-to-end greedy generation, one JSON line of its own)
        python bench.py --copy-probe   (a plain 256 MiB device copy, five times: the
        known-size kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)
 
@@ -145,6 +146,85 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
             "tokens_per_s": round(batch / (ms * 1e-3), 1)}
 
 
+def c4_config():
+    """C4 model, prompt and map: random-init Qwen2-7B shape, 4096 random
+    prompt ids, a seeded per-(layer, KV head) draw over INT8 / INT4 / bf16."""
+    import torch
+    import transformers
+
+    from triattention_amd.maps import INF, from_bands
+
+    cfg = transformers.Qwen2Config(vocab_size=152064, hidden_size=3584, intermediate_size=18944,
+                                   num_hidden_layers=28, num_attention_heads=28, num_key_value_heads=4,
+                                   max_position_embeddings=32768, rope_theta=1e6, initializer_range=0.02,
+                                   tie_word_embeddings=False)
+    g = torch.Generator().manual_seed(1004)
+    ids = torch.randint(152064, (1, 4096), generator=g)
+    kinds = torch.randint(3, (28, 4), generator=g)  # 0 INT8, 1 INT4, 2 bf16
+    band = {0: [INF, INF], 1: [1, INF], 2: [INF, INF]}
+    bands = {str(l): [band[int(kinds[l, h // 7])] for h in range(28)] for l in range(28)}
+    bf16 = {str(l): [h for h in range(4) if int(kinds[l, h]) == 2] for l in range(28)}
+    mixed = from_bands(bands, bf16=bf16)
+    exact = from_bands(bands, bf16={str(l): [0, 1, 2, 3] for l in range(28)})
+    share = {name: float((kinds == i).float().mean()) for i, name in enumerate(("int8", "int4", "bf16"))}
+    return cfg, ids, mixed, exact, share
+
+
+def c4_e2e(args):
+    """C4: greedy generation of 256 tokens after a 4096-token prompt through TriAttention, on the mixed
+    map and, for comparison, with every KV head exact (bf16) on the same kernels."""
+    import torch
+    import transformers
+
+    from triattention_amd.models import TriAttention
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg, ids, mixed, exact, share = c4_config()
+    log("C4: random-init Qwen2-7B (bf16, N(0, 0.02)) on the GPU")
+    torch.manual_seed(1004)
+    with torch.device(dev):
+        model = transformers.Qwen2ForCausalLM(cfg).to(torch.bfloat16).eval()
+    ids = ids.to(dev)
+    new = 256
+    runs = {}
+    for name, fn in (("mixed", mixed), ("all_bf16", exact)):
+        tri = TriAttention(model, fn, max_new_tokens=new)
+        for rep in range(2):  # the first run also builds the per-layer plans and buffers
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with torch.inference_mode():
+                out = model(input_ids=ids, use_cache=False, logits_to_keep=1)
+                first = int(out.logits[0, -1].argmax())
+            t1 = time.perf_counter()
+            tokens = [first]
+            with torch.inference_mode():
+                for i in range(new - 1):
+                    position = torch.tensor([[ids.shape[1] + i]], device=dev)
+                    out = model(input_ids=torch.tensor([[tokens[-1]]], device=dev), position_ids=position,
+                                use_cache=False)
+                    tri.decode_cache.advance()
+                    tokens.append(int(out.logits[0, -1].argmax()))
+            t2 = time.perf_counter()
+        runs[name] = {"prefill_ms": round((t1 - t0) * 1e3, 2), "decode_s": round(t2 - t1, 4),
+                      "decode_tokens_per_s": round((new - 1) / (t2 - t1), 2),
+                      "generate_tokens_per_s": round(new / (t2 - t0), 2), "tokens_head": tokens[:8]}
+        log(f"C4 {name}: prefill {runs[name]['prefill_ms']} ms, decode {runs[name]['decode_tokens_per_s']} tokens/s")
+    result = {
+        "metric": "C4 end-to-end greedy decode tokens/s (prefill time reported separately)",
+        "value": runs["mixed"]["decode_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": new,
+        "warmup": 1, "ms_per_step": round(runs["mixed"]["decode_s"] / (new - 1) * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 model; int8/int4/bf16 attention per map",
+        "data": "synthetic (random-init weights N(0, 0.02), 4096 random prompt ids, seed 1004)",
+        "config": {"workload": "C4 e2e: Qwen2-7B architecture (28 layers, hidden 3584, Hq 28 / Hk 4, FFN 18944, "
+                               "vocab 152064, rope 1e6), prompt 4096 + 256 greedy steps, batch 1, HF eager "
+                               "modules without the HF KV cache (the decode cache holds K/V)",
+                   "map_share": share, "global_batch": 1, "seq_len": 4096, "parallelism": "single GPU"},
+        "runs": runs,
+    }
+    print(json.dumps(result))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,9 +235,13 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=8)
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--no-c3", action="store_true")
+    ap.add_argument("--c4", action="store_true", help="run the C4 end-to-end generation instead")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
+        return
+    if args.c4 and args.gpus == 1:
+        c4_e2e(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",

@@ -94,6 +94,20 @@ def oracle_prefill(q, k, v, bands, scale, decode_cache=False):
     return np.stack(outs), codes
 
 
+def assert_close_bf16(gpu, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, what=""):
+    """assert_close for a bf16 output: each element may also be off by the half ulp of bf16 rounding,
+    at most |ref| * 2**-8 (8 significand bits)."""
+    gpu = np.asarray(gpu, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(gpu - ref)
+    allowed = max_abs + np.abs(ref) * 2.0 ** -8
+    assert np.isfinite(gpu).all(), f"{what}: non-finite output"
+    worst = float((err - allowed).max())
+    assert worst <= 0 and err.mean() <= mean_abs + float(np.abs(ref).mean()) * 2.0 ** -9, \
+        f"{what}: max abs {err.max():.3e}, worst excess over the bf16 bar {worst:.3e}, mean abs {err.mean():.3e}"
+    return float(err.max()), float(err.mean())
+
+
 def assert_close(gpu, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, what=""):
     err = np.abs(np.asarray(gpu, np.float64) - np.asarray(ref, np.float64))
     assert np.isfinite(np.asarray(gpu)).all(), f"{what}: non-finite output"

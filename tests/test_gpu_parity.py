@@ -212,7 +212,7 @@ def _attend64(q, keys, values, scale):
     return outs
 
 
-@pytest.mark.parametrize("prompt,bf16_kv,batch", [(300, [1], 2), (64, [0, 2], 1), (1500, [2], 2)])
+@pytest.mark.parametrize("prompt,bf16_kv,batch", [(300, [1], 2), (64, [0, 2], 1), (1500, [2], 2), (200, [0, 1, 2], 2)])
 def test_decode_with_exact_heads(module, prompt, bf16_kv, batch):
     """Maps with bf16 KV heads through Prefill + DecodeCache: quantized heads match the oracle, exact heads
     match float64 attention over the raw bf16 prompt and tail."""

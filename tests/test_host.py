@@ -214,3 +214,24 @@ def test_record_codec_round_trip_and_layout():
     p = 4 * (w // 8) + w % 4
     L = (ch % 32) + 32 * ((w % 8) // 4)
     assert rec[((ch // 32) * 2 + kb) * 1024 + L * 16 + p] == codes[0, 13, 70].view(np.uint8)
+
+
+def test_every_head_exact_keeps_one_placeholder_record_per_kind():
+    """A layer whose KV heads are all bf16 selects no quantized record; each record array the kernel
+    takes is then a single zero record (the kernel needs non-empty arrays and never reads it)."""
+    cache = DecodeCache(FakeModule(), max_tail=4)
+    hk, prompt, batch = 2, 130, 1
+    tiles = (prompt + 63) // 64
+    bands = torch.tensor([[INF, INF]] * 4, dtype=torch.int32)
+    kp = torch.zeros(batch * hk * tiles * 2048, dtype=torch.uint32)
+    packed = {F16: None, I8: torch.zeros(batch * hk * tiles * 2048, dtype=torch.uint32), I4: None}
+    ka = torch.ones(batch * hk * tiles * 4)
+    stat = torch.zeros(batch, hk, 3, 128)
+    kx = torch.zeros(batch * hk * tiles * 16384, dtype=torch.uint8)
+    codes, _ = cache.codes(tiles)
+    cache.store(0, prompt, kp, ka, stat, stat.clone(), packed, codes, bands, None, None, [0, 1], kx, kx.clone())
+    e = cache.layers[0]
+    assert e["k8"].shape == (1, 2048) and not e["k8"].to(torch.int64).any()
+    assert e["v"][I8].shape == (1, 2048) and e["v"][I4].shape == (1, 1024)
+    assert e["xslot"].tolist() == [[0, tiles]]
+    assert e["count"].tolist() == [[tiles, tiles]]

@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import torch
 
+from .extension import _geometry
 from .prefill import I4, I8
 
 WORDS = {I8: 2048, I4: 1024}
@@ -178,7 +179,9 @@ class DecodeCache:
             ov8 += b * g["nv"][I8]
             ov4 += b * g["nv"][I4]
             row += b
-        cat = lambda parts, words: (torch.cat(parts) if parts else
+        # a record kind no tile uses (e.g. every KV head exact) gets one zero record: the kernel takes
+        # non-empty record arrays and never reads it
+        cat = lambda parts, words: (torch.cat(parts) if sum(p.shape[0] for p in parts) else
                                     torch.zeros((1, words), dtype=torch.uint32, device=device))
         cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
             torch.cuda.get_device_properties(device).multi_processor_count
@@ -209,9 +212,9 @@ class DecodeCache:
         return out
 
     def plan(self, layer, q, k, out, scale):
-        """The layer's validated decode call for q / k / out of these shapes (built once, then reused)."""
+        """The layer's validated decode call for q / k (and v) / out of these shapes (built once, then reused)."""
         e = self.layers[layer]
-        key = ("plan", tuple(q.shape), q.stride(), tuple(k.shape), k.stride(), out.dtype, out.stride(), float(scale))
+        key = ("plan", _geometry(q), _geometry(k), _geometry(out), float(scale))
         if key not in e:
             hq = q.shape[1]
             e[key] = self.module.plan_decode(

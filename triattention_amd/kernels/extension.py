@@ -235,6 +235,7 @@ class Module:
             _check(xslot.dtype == torch.int32 and xslot.is_cuda and xslot.numel() == b * hk and kxc is not None and
                    vxc is not None and kxc.numel() * kxc.element_size() % KX_BYTES == 0 and
                    kxc.numel() * kxc.element_size() == vxc.numel() * vxc.element_size(), "exact heads: xslot / KX / VX")
+        _check(_geometry(vcur) == _geometry(kcur), "decode: k and v of the new token must have the same shape and strides")
         _check(step.dtype == torch.int64 and step.is_cuda and kcur.stride(3) == 1 and
                entry.dtype == torch.int32 and kinfo.dtype == torch.int32 and count.dtype == torch.int32 and
                slot.dtype == torch.int32 and fmt.dtype == torch.int32 and prompt_t.dtype == torch.int32 and
@@ -272,7 +273,9 @@ class Module:
 
 
 def _geometry(t):
-    return tuple(t.shape), t.stride(), t.dtype, t.device
+    """What a launch depends on: shape, dtype, device and the strides of the dimensions of extent > 1
+    (a stride over a dimension of extent 1 is never applied)."""
+    return tuple(t.shape), tuple(s if n > 1 else None for n, s in zip(t.shape, t.stride())), t.dtype, t.device
 
 
 class DecodePlan:

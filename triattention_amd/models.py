@@ -1,0 +1,146 @@
+"""Hugging Face integration: the attention hook, prefill/decode dispatch and
+greedy generation on the gfx950 kernels.
+
+Mirrors triattention/models.py (load_tokenizer :15-18, load_model :21-32,
+render_prompt :35-37, eos_ids :40-42, exact_attention :45-47, use_attention
+:50-55, TriAttention :58-85) with the same names, arguments and behaviour:
+
+* a model's attention calls go to ``Prefill`` for a prompt and to
+  ``DecodeCache`` for a one-token query of a layer whose prompt is stored;
+* ``generate`` runs the model without the HF KV cache (the decode cache holds
+  the quantized prompt and the bf16 tail of generated tokens) and returns the
+  greedy tokens, stopping at an end-of-sequence id.
+
+``exact_attention`` (the reference's bf16 baseline, SDPA flash there) runs the
+exact-head path of this library's prefill kernel: every KV head listed as
+bf16, so each q-head attends causally over the unquantized bf16 operands with
+fp32 accumulation.
+
+Extensions: ``TriAttention`` accepts a map path or a ``bands_fn`` (as built by
+``triattention_amd.maps``), and an optional ``module`` (the loaded extension).
+Model loaders read local paths only.
+"""
+from __future__ import annotations
+
+import torch
+
+from .kernels.decode import DecodeCache
+from .kernels.extension import load_extension
+from .kernels.prefill import Prefill
+from .maps import INF, load_map, preset
+
+
+def load_tokenizer(path):
+    """Tokenizer of a local model directory (models.py:15-18)."""
+    from transformers import AutoConfig, AutoTokenizer
+
+    mistral = AutoConfig.from_pretrained(path).model_type == "mistral3"
+    return AutoTokenizer.from_pretrained(path, **({"fix_mistral_regex": True} if mistral else {}))
+
+
+def load_model(path):
+    """bf16 causal LM from a local model directory, on the GPU, in eval mode (models.py:21-32).
+
+    Qwen2 models get the reference's YaRN extension (factor 4 over 32768 positions)."""
+    import transformers
+    from transformers import AutoConfig
+
+    config = AutoConfig.from_pretrained(path)
+    if config.model_type == "qwen2":
+        theta = config.rope_parameters["rope_theta"]
+        config.rope_parameters = dict(rope_type="yarn", factor=4.0, original_max_position_embeddings=32768,
+                                      rope_theta=theta)
+        config.max_position_embeddings = 4 * 32768
+    loader = transformers.AutoModelForImageTextToText if hasattr(config, "vision_config") else \
+        transformers.AutoModelForCausalLM
+    return loader.from_pretrained(path, config=config, dtype=torch.bfloat16).cuda().eval()
+
+
+def render_prompt(tokenizer, prompt):
+    """Chat-template rendering of one user turn (models.py:35-37)."""
+    return tokenizer.apply_chat_template([{"role": "user", "content": prompt}], tokenize=False,
+                                         add_generation_prompt=True, date_string="30 Jul 2026")
+
+
+def eos_ids(tokenizer, model):
+    """Union of the tokenizer's and the generation config's end-of-sequence ids (models.py:40-42)."""
+    as_set = lambda ids: set(ids if isinstance(ids, list) else [ids])
+    return as_set(tokenizer.eos_token_id) | as_set(model.generation_config.eos_token_id)
+
+
+class _AllExact:
+    """bands_fn that keeps every KV head bf16 (the bands themselves are then unused)."""
+
+    layer_independent = True
+
+    def __init__(self, kv_heads):
+        self.kv_heads = kv_heads
+
+    def __call__(self, layer, heads):
+        return torch.tensor([[INF, INF]] * heads, dtype=torch.int32)
+
+    def bf16(self, layer):
+        return list(range(self.kv_heads))
+
+
+_exact = {}
+
+
+def exact_attention(query, key, value, scaling):
+    """Exact causal GQA attention, [B, Hq, T, 128] bf16 -> [B, Hq, T, 128] (models.py:45-47).
+
+    Runs the prefill kernel with every KV head exact: bf16 operands, fp32 scores,
+    softmax and accumulation."""
+    kv_heads = key.shape[1]
+    runner = _exact.get(kv_heads)
+    if runner is None:
+        runner = _exact[kv_heads] = Prefill(load_extension(), _AllExact(kv_heads))
+    return runner(0, query, key, value, scaling)
+
+
+def use_attention(model, name, fn):
+    """Register ``fn(module, q, k, v, scaling) -> [B, H, T, D]`` as attention implementation ``name``
+    and switch ``model`` to it (models.py:50-55)."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    def attention(module, query, key, value, attention_mask, scaling, dropout=0.0, **kwargs):
+        return fn(module, query, key, value, scaling).transpose(1, 2).contiguous(), None
+
+    ALL_ATTENTION_FUNCTIONS[name] = attention
+    model.set_attn_implementation(name)
+
+
+class TriAttention:
+    """Quantized attention for a HF model: prompt through ``Prefill``, generated tokens through
+    ``DecodeCache`` (models.py:58-85)."""
+
+    def __init__(self, model, qk_map=None, max_new_tokens=256, module=None):
+        self.model = model
+        module = module if module is not None else load_extension()
+        self.decode_cache = DecodeCache(module, max_tail=max_new_tokens)
+        bands_fn = qk_map if callable(qk_map) else load_map(qk_map or preset(model), model)
+        self.prefill = Prefill(module, bands_fn, self.decode_cache)
+
+        def attention(mod, query, key, value, scaling):
+            if query.shape[2] == 1 and self.decode_cache.stored(mod.layer_idx):
+                return self.decode_cache(mod.layer_idx, query, key, value, scaling)
+            return self.prefill(mod.layer_idx, query, key, value, scaling)
+
+        use_attention(model, "triattention", attention)
+
+    @torch.inference_mode()
+    def generate(self, ids, max_new_tokens, eos):
+        """Greedy tokens after the prompt ``ids`` [1, T], at most ``max_new_tokens``, stopping before an id
+        in ``eos`` (models.py:72-85)."""
+        out = self.model(input_ids=ids, use_cache=False, logits_to_keep=1)
+        tokens = []
+        for i in range(max_new_tokens):
+            token = int(out.logits[0, -1].argmax())
+            if token in eos:
+                break
+            tokens.append(token)
+            position = torch.tensor([[ids.shape[1] + i]], device=ids.device)
+            out = self.model(input_ids=torch.tensor([[token]], device=ids.device), position_ids=position,
+                             use_cache=False)
+            self.decode_cache.advance()
+        return tokens

@@ -86,7 +86,8 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * [batch][hk]; fmt int32 [batch][tiles_max] (1 = INT8 V, 2 = INT4 V); prompt
  * int32 [batch] lengths; vstat/kstat f32 [batch][hk][3][128]; ktail/vtail bf16
  * [batch][hk][max_tail][128] (strides t_sb, t_sh, t_st); kcur/vcur bf16
- * [batch][hk][1][128] (strides c_sb, c_sh); step int64 [1] on the device;
+ * [batch][hk][1][128] (strides c_sb, c_sh); tail and new-token rows 16-byte
+ * aligned (strides multiples of 8 elements); step int64 [1] on the device;
  * out [batch][hq][1][128] (strides o_sb, o_sh), out_dtype 0 = fp32, 1 = bf16;
  * pm/pl f32 [batch][hq][splits], po f32 [batch][hq][splits][128] with
  * splits = max(1, ceil(maxn / per)) with 1 <= per <= 64; n_k8/n_k4/n_v8/n_v4 are the record

@@ -208,6 +208,10 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   if ((k4c == nullptr) != (ka4 == nullptr)) return fail("decode: INT4 K records and scales (all or none)");
   if (out_dtype != 0 && out_dtype != 1) return fail("decode: out dtype must be fp32 or bf16");
   if (!aligned(q, 8) || (q_sh % 4) || (q_sb % 4)) return fail("decode: q rows must be 8-byte aligned");
+  if (!aligned(kcur, 16) || !aligned(vcur, 16) || (c_sb % 8) || (c_sh % 8))
+    return fail("decode: k/v of the new token must be 16-byte aligned rows");
+  if (!aligned(ktail, 16) || !aligned(vtail, 16) || (t_sb % 8) || (t_sh % 8) || (t_st % 8))
+    return fail("decode: tail buffers must be 16-byte aligned rows");
   if (!aligned(po, 16)) return fail("decode: po must be 16-byte aligned");
   const int splits = std::max(1, (maxn + per - 1) / per);
   const int64_t lim = (int64_t)1 << 31;

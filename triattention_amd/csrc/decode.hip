@@ -572,67 +572,94 @@ struct MergeArgs {
 
 // LSE merge of the split partials with the exact bf16 tail
 // (common_device.cuh:373-469).  One 256-thread workgroup per (sequence, q-head).
+// Tail scores: 8 lanes per token (16 channels each), 32 tokens per pass; tail
+// values: 16 lanes per token (8 channels each), 16 tokens per pass, so a long
+// tail keeps many rows in flight instead of one row per thread and step.
 __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
-  __shared__ float ts[MAX_TAIL];
-  __shared__ float wmax[8], wl[4];
-  __shared__ float wo[4][D];
-  const int hq = blockIdx.x, b = blockIdx.y, g = a.hq / a.hk, kh = hq / g;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, sub = lane >> 5;
+  __shared__ float ts[MAX_TAIL];  // tail scores, then their weights texp2(score - m)
+  __shared__ float vo[16][D];     // tail value sums of the 16 token groups
+  __shared__ float wo[4][D];      // split sums of the four waves
+  __shared__ float wred[4][3];  // per wave: max, split weight sum, tail weight sum
+  // XCD x (workgroups are dealt round-robin by linear id) takes the x-th contiguous eighth of the
+  // (sequence, q-head) space, so the q-heads of one KV head share an L2 for their tail reads
+  int hq, b;
+  {
+    const int total = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int q8 = total >> 3, r8 = total & 7, x = lin & 7;
+    const int w = x * q8 + min(x, r8) + (lin >> 3);
+    hq = w % gridDim.x;
+    b = w / gridDim.x;
+  }
+  const int g = a.hq / a.hk, kh = hq / g;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int prior = (int)min((int64_t)a.max_tail - 1, *a.step), tail = prior + 1;
   const int64_t hb = (int64_t)b * a.hk + kh;
   const float* vmean = a.vstat + hb * 3 * D;
   const float* vscale = vmean + D;
   const uint16_t* kc = a.kcur + b * a.csb + kh * a.csh;
   const uint16_t* vc = a.vcur + b * a.csb + kh * a.csh;
+  const uint16_t* kt = a.ktail + b * a.tsb + kh * a.tsh;
+  const uint16_t* vt = a.vtail + b * a.tsb + kh * a.tsh;
+  const int64_t pbase = ((int64_t)b * a.hq + hq) * a.splits;
   if (hq % g == 0 && tid < D) {
     a.ktail[b * a.tsb + kh * a.tsh + prior * a.tst + tid] = kc[tid];
     a.vtail[b * a.tsb + kh * a.tsh + prior * a.tst + tid] = vc[tid];
   }
-  // tail scores: 32-lane fma chains over 4 channels each, then a xor butterfly
-  float qv[4], kmu[4];
+  // ---- tail scores q . (k - kmean) * sm_log2: token group tid >> 3, channels 16 * (tid & 7) ..
+  {
+    const int grp = tid >> 3, c0 = (tid & 7) * 16;
+    float qv[16], mu[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    qv[i] = bf16f(a.q[b * a.qsb + hq * a.qsh + l32 * 4 + i]);
-    kmu[i] = a.kstat[hb * 3 * D + l32 * 4 + i];
-  }
-  // 8 half-waves x 8 tokens in flight per round
-  for (int t0 = (wave * 2 + sub) * 8; t0 < tail; t0 += 64) {
-    uint2 raw[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int t = min(t0 + u, tail - 1);
-      const uint16_t* kv = t < prior ? a.ktail + b * a.tsb + kh * a.tsh + (int64_t)t * a.tst : kc;
-      raw[u] = *reinterpret_cast<const uint2*>(kv + l32 * 4);
+    for (int i = 0; i < 16; ++i) {
+      qv[i] = bf16f(a.q[b * a.qsb + hq * a.qsh + c0 + i]);
+      mu[i] = a.kstat[hb * 3 * D + c0 + i];
     }
-    float part[8];
+    for (int t0 = grp; t0 < tail; t0 += 4 * 32) {
+      uint4 raw[4][2];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float kx[4] = {bf16f(raw[u].x & 0xffffu), bf16f(raw[u].x >> 16), bf16f(raw[u].y & 0xffffu),
-                           bf16f(raw[u].y >> 16)};
-      part[u] = 0.f;
+      for (int u = 0; u < 4; ++u) {
+        const int t = min(t0 + u * 32, tail - 1);
+        const uint16_t* row = (t < prior ? kt + (int64_t)t * a.tst : kc) + c0;
+        raw[u][0] = *reinterpret_cast<const uint4*>(row);
+        raw[u][1] = *reinterpret_cast<const uint4*>(row + 8);
+      }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) part[u] = __builtin_fmaf(qv[i], kx[i] - kmu[i], part[u]);
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t w[8] = {raw[u][0].x, raw[u][0].y, raw[u][0].z, raw[u][0].w,
+                               raw[u][1].x, raw[u][1].y, raw[u][1].z, raw[u][1].w};
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float kx = bf16f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
+          part = __builtin_fmaf(qv[i], kx - mu[i], part);
+        }
+        part += lane_xor8<1>(part);
+        part += lane_xor8<2>(part);
+        part += lane_xor8<4>(part);
+        const int t = t0 + u * 32;
+        if ((tid & 7) == 0 && t < tail) ts[t] = part * a.sm_log2;
+      }
     }
-#pragma unroll
-    for (int o = 16; o; o >>= 1)
-#pragma unroll
-      for (int u = 0; u < 8; ++u) part[u] += __shfl_xor(part[u], o, 32);
-    if (l32 == 0)
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (t0 + u < tail) ts[t0 + u] = part[u] * a.sm_log2;
   }
+  // the split partials of this q-head, loaded while the scores are in flight
+  float pm_own = -3.402823466e38f;
+  for (int s = tid; s < a.splits; s += 256) pm_own = fmaxf(pm_own, a.pm[pbase + s]);
   __syncthreads();
-  const int64_t pbase = ((int64_t)b * a.hq + hq) * a.splits;
-  float m = -3.402823466e38f;
-  for (int s = tid; s < a.splits; s += 256) m = fmaxf(m, a.pm[pbase + s]);
+  float m = pm_own;
   for (int t = tid; t < tail; t += 256) m = fmaxf(m, ts[t]);
 #pragma unroll
   for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  if (lane == 0) wmax[wave] = m;
+  if (lane == 0) wred[wave][0] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  // four interleaved split accumulators, summed in order
+  m = fmaxf(fmaxf(wred[0][0], wred[1][0]), fmaxf(wred[2][0], wred[3][0]));
+  // tail weights, in place
+  float lt = 0.f;
+  for (int t = tid; t < tail; t += 256) {
+    const float e = texp2(ts[t] - m);
+    ts[t] = e;
+    lt += e;
+  }
+  // split sums: four interleaved accumulators, one per wave
   float l = 0.f, o0 = 0.f, o1 = 0.f;
   for (int s = wave; s < a.splits; s += 4) {
     const float w = texp2(a.pm[pbase + s] - m);
@@ -641,40 +668,51 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
     o0 = __builtin_fmaf(p.x, w, o0);
     o1 = __builtin_fmaf(p.y, w, o1);
   }
-  if (lane == 0) wl[wave] = l;
+#pragma unroll
+  for (int o = 32; o; o >>= 1) lt += __shfl_xor(lt, o, 64);
+  if (lane == 0) {
+    wred[wave][1] = l;
+    wred[wave][2] = lt;
+  }
   wo[wave][lane * 2] = o0;
   wo[wave][lane * 2 + 1] = o1;
   __syncthreads();
+  // ---- tail values: token group tid >> 4, channels 8 * (tid & 15) ..
+  {
+    const int grp = tid >> 4, c0 = (tid & 15) * 8;
+    float av[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int t0 = grp; t0 < tail; t0 += 4 * 16) {
+      uint4 raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = min(t0 + u * 16, tail - 1);
+        raw[u] = *reinterpret_cast<const uint4*>((t < prior ? vt + (int64_t)t * a.tst : vc) + c0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = t0 + u * 16;
+        const float e = t < tail ? ts[t] : 0.f;
+        const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) av[i] = __builtin_fmaf(e, bf16f((uint16_t)(w[i >> 1] >> (16 * (i & 1)))), av[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vo[grp][c0 + i] = av[i];
+  }
+  __syncthreads();
   if (tid >= D) return;
-  float total = 0.f, acc = 0.f;
+  float lsum = 0.f, osum = 0.f, tsum = 0.f, vsum = 0.f;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    total += wl[w];
-    acc += wo[w][tid];
+    lsum += wred[w][1];
+    tsum += wred[w][2];
+    osum += wo[w][tid];
   }
-  acc = __builtin_fmaf(acc, vscale[tid], total * vmean[tid]);
-  const uint16_t* vt = a.vtail + b * a.tsb + kh * a.tsh + tid;
-  int t = 0;
-  for (; t + 8 <= prior; t += 8) {
-    uint16_t vv[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) vv[u] = vt[(int64_t)(t + u) * a.tst];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float e = texp2(ts[t + u] - m);
-      total += e;
-      acc = __builtin_fmaf(e, bf16f(vv[u]), acc);
-    }
-  }
-  for (; t < prior; ++t) {
-    const float e = texp2(ts[t] - m);
-    total += e;
-    acc = __builtin_fmaf(e, bf16f(vt[(int64_t)t * a.tst]), acc);
-  }
-  const float e = texp2(ts[prior] - m);
-  total += e;
-  acc = __builtin_fmaf(e, bf16f(vc[tid]), acc);
-  const float r = acc / total;
+  for (int grp = 0; grp < 16; ++grp) vsum += vo[grp][tid];
+  const float acc = __builtin_fmaf(osum, vscale[tid], lsum * vmean[tid]) + vsum;
+  const float r = acc / (lsum + tsum);
   if (a.out_dtype == 0) static_cast<float*>(a.out)[b * a.osb + hq * a.osh + tid] = r;
   else static_cast<uint16_t*>(a.out)[b * a.osb + hq * a.osh + tid] = f32_to_bf16(r);
 }

@@ -571,17 +571,18 @@ struct MergeArgs {
 };
 
 // LSE merge of the split partials with the exact bf16 tail
-// (common_device.cuh:373-469).  One 256-thread workgroup per (sequence, q-head).
-// Tail scores: 8 lanes per token (16 channels each), 32 tokens per pass; tail
-// values: 16 lanes per token (8 channels each), 16 tokens per pass, so a long
-// tail keeps many rows in flight instead of one row per thread and step.
+// (common_device.cuh:373-469).  One 256-thread workgroup per (sequence, q-head),
+// XCD-aware so the q-heads of one KV head share an L2 for their tail reads.
+// Every global load that does not depend on another is issued first (the split
+// partials of up to 16 splits, the first 32 tail tokens' K rows and first 64
+// tail tokens' V rows), so a short tail costs one memory round trip; longer
+// tails and more splits continue in loops.  Tail scores: 8 lanes per token (16
+// channels each); tail values: 16 lanes per token (8 channels each).
 __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   __shared__ float ts[MAX_TAIL];  // tail scores, then their weights texp2(score - m)
   __shared__ float vo[16][D];     // tail value sums of the 16 token groups
   __shared__ float wo[4][D];      // split sums of the four waves
-  __shared__ float wred[4][3];  // per wave: max, split weight sum, tail weight sum
-  // XCD x (workgroups are dealt round-robin by linear id) takes the x-th contiguous eighth of the
-  // (sequence, q-head) space, so the q-heads of one KV head share an L2 for their tail reads
+  __shared__ float wred[4][3];    // per wave: max, split weight sum, tail weight sum
   int hq, b;
   {
     const int total = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
@@ -601,54 +602,72 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   const uint16_t* kt = a.ktail + b * a.tsb + kh * a.tsh;
   const uint16_t* vt = a.vtail + b * a.tsb + kh * a.tsh;
   const int64_t pbase = ((int64_t)b * a.hq + hq) * a.splits;
+  const int sgrp = tid >> 3, sc0 = (tid & 7) * 16;  // score layout: token group, first channel
+  const int vgrp = tid >> 4, vc0 = (tid & 15) * 8;  // value layout
+  // ---- loads issued up front
+  float qv[16], mu[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    qv[i] = bf16f(a.q[b * a.qsb + hq * a.qsh + sc0 + i]);
+    mu[i] = a.kstat[hb * 3 * D + sc0 + i];
+  }
+  uint4 kraw[2];
+  {
+    const int t = min(sgrp, tail - 1);
+    const uint16_t* row = (t < prior ? kt + (int64_t)t * a.tst : kc) + sc0;
+    kraw[0] = *reinterpret_cast<const uint4*>(row);
+    kraw[1] = *reinterpret_cast<const uint4*>(row + 8);
+  }
+  uint4 vraw[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = min(vgrp + u * 16, tail - 1);
+    vraw[u] = *reinterpret_cast<const uint4*>((t < prior ? vt + (int64_t)t * a.tst : vc) + vc0);
+  }
+  float pmv[4], plv[4];
+  float2 pov[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int s = min(wave + 4 * u, a.splits - 1);
+    pmv[u] = a.pm[pbase + s];
+    plv[u] = a.pl[pbase + s];
+    pov[u] = *reinterpret_cast<const float2*>(a.po + (pbase + s) * D + lane * 2);
+  }
+  const float vmv = tid < D ? vmean[tid] : 0.f, vsv = tid < D ? vscale[tid] : 0.f;
   if (hq % g == 0 && tid < D) {
     a.ktail[b * a.tsb + kh * a.tsh + prior * a.tst + tid] = kc[tid];
     a.vtail[b * a.tsb + kh * a.tsh + prior * a.tst + tid] = vc[tid];
   }
-  // ---- tail scores q . (k - kmean) * sm_log2: token group tid >> 3, channels 16 * (tid & 7) ..
-  {
-    const int grp = tid >> 3, c0 = (tid & 7) * 16;
-    float qv[16], mu[16];
+  // ---- tail scores q . (k - kmean) * sm_log2
+  auto score = [&](const uint4 (&raw)[2], int t) {
+    const uint32_t w[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
+    float part = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      qv[i] = bf16f(a.q[b * a.qsb + hq * a.qsh + c0 + i]);
-      mu[i] = a.kstat[hb * 3 * D + c0 + i];
+      const float kx = bf16f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
+      part = __builtin_fmaf(qv[i], kx - mu[i], part);
     }
-    for (int t0 = grp; t0 < tail; t0 += 4 * 32) {
-      uint4 raw[4][2];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int t = min(t0 + u * 32, tail - 1);
-        const uint16_t* row = (t < prior ? kt + (int64_t)t * a.tst : kc) + c0;
-        raw[u][0] = *reinterpret_cast<const uint4*>(row);
-        raw[u][1] = *reinterpret_cast<const uint4*>(row + 8);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t w[8] = {raw[u][0].x, raw[u][0].y, raw[u][0].z, raw[u][0].w,
-                               raw[u][1].x, raw[u][1].y, raw[u][1].z, raw[u][1].w};
-        float part = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float kx = bf16f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
-          part = __builtin_fmaf(qv[i], kx - mu[i], part);
-        }
-        part += lane_xor8<1>(part);
-        part += lane_xor8<2>(part);
-        part += lane_xor8<4>(part);
-        const int t = t0 + u * 32;
-        if ((tid & 7) == 0 && t < tail) ts[t] = part * a.sm_log2;
-      }
-    }
+    part += lane_xor8<1>(part);
+    part += lane_xor8<2>(part);
+    part += lane_xor8<4>(part);
+    if ((tid & 7) == 0 && t < tail) ts[t] = part * a.sm_log2;
+  };
+  score(kraw, sgrp);
+  for (int t0 = sgrp + 32; t0 < tail; t0 += 32) {
+    const int t = min(t0, tail - 1);
+    const uint16_t* row = (t < prior ? kt + (int64_t)t * a.tst : kc) + sc0;
+    uint4 raw[2] = {*reinterpret_cast<const uint4*>(row), *reinterpret_cast<const uint4*>(row + 8)};
+    score(raw, t0);
   }
-  // the split partials of this q-head, loaded while the scores are in flight
   float pm_own = -3.402823466e38f;
-  for (int s = tid; s < a.splits; s += 256) pm_own = fmaxf(pm_own, a.pm[pbase + s]);
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (wave + 4 * u < a.splits) pm_own = fmaxf(pm_own, pmv[u]);
+  for (int s = wave + 16; s < a.splits; s += 4) pm_own = fmaxf(pm_own, a.pm[pbase + s]);
   __syncthreads();
   float m = pm_own;
   for (int t = tid; t < tail; t += 256) m = fmaxf(m, ts[t]);
-#pragma unroll
-  for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  m = lanes_max<64>(m);
   if (lane == 0) wred[wave][0] = m;
   __syncthreads();
   m = fmaxf(fmaxf(wred[0][0], wred[1][0]), fmaxf(wred[2][0], wred[3][0]));
@@ -659,9 +678,18 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
     ts[t] = e;
     lt += e;
   }
-  // split sums: four interleaved accumulators, one per wave
+  // split sums: wave w takes splits w, w + 4, ... in order
   float l = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int s = wave; s < a.splits; s += 4) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (wave + 4 * u < a.splits) {
+      const float w = texp2(pmv[u] - m);
+      l = __builtin_fmaf(plv[u], w, l);
+      o0 = __builtin_fmaf(pov[u].x, w, o0);
+      o1 = __builtin_fmaf(pov[u].y, w, o1);
+    }
+  }
+  for (int s = wave + 16; s < a.splits; s += 4) {
     const float w = texp2(a.pm[pbase + s] - m);
     l = __builtin_fmaf(a.pl[pbase + s], w, l);
     const float2 p = *reinterpret_cast<const float2*>(a.po + (pbase + s) * D + lane * 2);
@@ -677,28 +705,29 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   wo[wave][lane * 2] = o0;
   wo[wave][lane * 2 + 1] = o1;
   __syncthreads();
-  // ---- tail values: token group tid >> 4, channels 8 * (tid & 15) ..
+  // ---- tail values
   {
-    const int grp = tid >> 4, c0 = (tid & 15) * 8;
     float av[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int t0 = grp; t0 < tail; t0 += 4 * 16) {
+    auto accum = [&](const uint4& raw, int t) {
+      const float e = t < tail ? ts[t] : 0.f;
+      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) av[i] = __builtin_fmaf(e, bf16f((uint16_t)(w[i >> 1] >> (16 * (i & 1)))), av[i]);
+    };
+#pragma unroll
+    for (int u = 0; u < 4; ++u) accum(vraw[u], vgrp + u * 16);
+    for (int t0 = vgrp + 64; t0 < tail; t0 += 4 * 16) {
       uint4 raw[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int t = min(t0 + u * 16, tail - 1);
-        raw[u] = *reinterpret_cast<const uint4*>((t < prior ? vt + (int64_t)t * a.tst : vc) + c0);
+        raw[u] = *reinterpret_cast<const uint4*>((t < prior ? vt + (int64_t)t * a.tst : vc) + vc0);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int t = t0 + u * 16;
-        const float e = t < tail ? ts[t] : 0.f;
-        const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) av[i] = __builtin_fmaf(e, bf16f((uint16_t)(w[i >> 1] >> (16 * (i & 1)))), av[i]);
-      }
+      for (int u = 0; u < 4; ++u) accum(raw[u], t0 + u * 16);
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vo[grp][c0 + i] = av[i];
+    for (int i = 0; i < 8; ++i) vo[vgrp][vc0 + i] = av[i];
   }
   __syncthreads();
   if (tid >= D) return;
@@ -711,7 +740,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   }
 #pragma unroll
   for (int grp = 0; grp < 16; ++grp) vsum += vo[grp][tid];
-  const float acc = __builtin_fmaf(osum, vscale[tid], lsum * vmean[tid]) + vsum;
+  const float acc = __builtin_fmaf(osum, vsv, lsum * vmv) + vsum;
   const float r = acc / (lsum + tsum);
   if (a.out_dtype == 0) static_cast<float*>(a.out)[b * a.osb + hq * a.osh + tid] = r;
   else static_cast<uint16_t*>(a.out)[b * a.osb + hq * a.osh + tid] = f32_to_bf16(r);

@@ -196,6 +196,41 @@ __device__ __forceinline__ float warp32_max(float m) {
 }
 
 
+// DPP move restricted to the 16-lane rows in ROWS; other rows keep v.  Row
+// broadcasts: 0x142 (row_bcast:15) gives rows 1 and 3 lane 15 of the row before
+// (with ROWS = 0xA), 0x143 (row_bcast:31) gives rows 2 and 3 lane 31 (ROWS = 0xC).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(x, x, CTRL, ROWS, 0xf, false));
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+// maximum of each 16-lane row, in every lane of the row
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  return fmaxf(v, dpp_move<0x140>(v));
+}
+// maximum over the wave as a uniform value: rows, then row_bcast:15 and
+// row_bcast:31 fold the rows into lane 63 (VALU only, no LDS permute)
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, dpp_rows<0x142, 0xA>(v));
+  v = fmaxf(v, dpp_rows<0x143, 0xC>(v));
+  return readlane_f(v, 63);
+}
+// maximum over the lane's 32-lane half: row_bcast:15 folds rows 0-1 into lane 31
+// and rows 2-3 into lane 63
+__device__ __forceinline__ float half_max(float v, bool upper) {
+  v = row16_max(v);
+  v = fmaxf(v, dpp_rows<0x142, 0xA>(v));
+  const float lo = readlane_f(v, 31), hi = readlane_f(v, 63);
+  return upper ? hi : lo;
+}
+
 // Maximum over each 32-lane half of the wave (LANES = 32) or over the whole wave
 // (LANES = 64), in every lane: four DPP steps reduce each 16-lane row (after the
 // quad steps every lane holds its quad's maximum, the half mirror pairs quads,

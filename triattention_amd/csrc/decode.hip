@@ -176,13 +176,12 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
 // DUP (groups of at most 4 q-heads): the score rows 4..7 of the QK MFMA do not
 // exist, so the upper half of the wave takes the tile's second 32-key block
 // for rows 0..3 instead, and every lane carries R scores rather than 2R.
-template <int R, bool EXACT = false, bool DUP = false, int W = (EXACT || R >= 3 ? 2 : 3)>
+template <int R, bool EXACT = false, bool DUP = false, int W = (EXACT || R >= 4 ? 2 : 3)>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
   __shared__ __align__(16) int8_t q8s[MAX_GROUP][D];
   __shared__ __align__(16) int8_t q4s[MAX_GROUP][D];
   __shared__ float qsc[MAX_GROUP], qsc4[MAX_GROUP];
   __shared__ __align__(16) uint8_t pls[MAX_GROUP][BN];
-  __shared__ __align__(16) float rsc[4][MAX_GROUP];  // alpha, base, bq, restore per row
   __shared__ __align__(16) int4 meta[MAX_PER + 1];     // per-tile record offsets and flags
   __shared__ __align__(16) float4 metk[MAX_PER + 1];   // per-tile K group scales
 
@@ -425,10 +424,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
         slope[r][t] = qs * kavc[t];
         if (ok[r][t]) trow[r] = fmaxf(trow[r], slope[r][t] * (float)dot[r][t]);
       }
-      trow[r] = lanes_max<DUP ? 64 : 32>(trow[r]);
+      trow[r] = DUP ? wave_max(trow[r]) : half_max(trow[r], half);
     }
     // ---- per-row scalars on the owner lane (common_device.cuh:222-238)
     const float levels = vf == 1 ? 255.f : 15.f;
+    float alpha_r[R], base_r[R], bq_r[R], restore_r[R];
     {
       float tile_o = -__builtin_inff();
 #pragma unroll
@@ -441,22 +441,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       base += __builtin_fmaf(qs_o * cur_kmax, 0.75f, fabsf(base) * 2.4e-7f);
       const float bq = any ? texp2(base - n) / levels : 0.f;
       const float restore = vf == 1 ? bq : bq * (127.f / 7.f);
-      if (lq < 4 && owner) {
-        rsc[0][orow] = alpha;
-        rsc[1][orow] = base;
-        rsc[2][orow] = bq;
-        rsc[3][orow] = restore;
+      // row q's scalars are in lane q (q < 4) or 32 + q - 4; every lane reads its rows' by readlane
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if constexpr (DUP) {
+          alpha_r[r] = readlane_f(alpha, r);
+          base_r[r] = readlane_f(base, r);
+          bq_r[r] = readlane_f(bq, r);
+          restore_r[r] = readlane_f(restore, r);
+        } else {
+          alpha_r[r] = half ? readlane_f(alpha, 32 + r) : readlane_f(alpha, r);
+          base_r[r] = half ? readlane_f(base, 32 + r) : readlane_f(base, r);
+          bq_r[r] = half ? readlane_f(bq, 32 + r) : readlane_f(bq, r);
+          restore_r[r] = half ? readlane_f(restore, 32 + r) : readlane_f(restore, r);
+        }
       }
     }
-    __syncthreads();
-    float alpha[R], base[R], bq[R], restore[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      alpha[r] = rsc[0][qrow(r)];
-      base[r] = rsc[1][qrow(r)];
-      bq[r] = rsc[2][qrow(r)];
-      restore[r] = rsc[3][qrow(r)];
-    }
+    const float (&alpha)[R] = alpha_r, (&base)[R] = base_r, (&bq)[R] = bq_r, (&restore)[R] = restore_r;
     bool rescale = false;
 #pragma unroll
     for (int r = 0; r < R; ++r) rescale |= alpha[r] != 1.f;

@@ -176,7 +176,7 @@ def c4_e2e(args):
     import torch
     import transformers
 
-    from triattention_amd.models import TriAttention
+    from triattention_amd.models import TriAttention, _GraphStep
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -188,28 +188,40 @@ def c4_e2e(args):
     ids = ids.to(dev)
     new = 256
     runs = {}
-    for name, fn in (("mixed", mixed), ("all_bf16", exact)):
+    for name, fn, graph in (("mixed", mixed, True), ("mixed_eager", mixed, False), ("all_bf16", exact, True)):
         tri = TriAttention(model, fn, max_new_tokens=new)
         for rep in range(2):  # the first run also builds the per-layer plans and buffers
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             with torch.inference_mode():
                 out = model(input_ids=ids, use_cache=False, logits_to_keep=1)
-                first = int(out.logits[0, -1].argmax())
+                torch.cuda.synchronize()
             t1 = time.perf_counter()
-            tokens = [first]
+            # TriAttention.generate's loop after the prompt (the prompt forward is timed above)
             with torch.inference_mode():
-                for i in range(new - 1):
+                tokens, step = [], None
+                for i in range(new):
+                    tokens.append(int(out.logits[0, -1].argmax()))
+                    if i == new - 1:
+                        break
+                    if step is not None:
+                        step.ids.fill_(tokens[-1])
+                        step.position.fill_(ids.shape[1] + i)
+                        out = step.replay()
+                        continue
                     position = torch.tensor([[ids.shape[1] + i]], device=dev)
                     out = model(input_ids=torch.tensor([[tokens[-1]]], device=dev), position_ids=position,
                                 use_cache=False)
                     tri.decode_cache.advance()
-                    tokens.append(int(out.logits[0, -1].argmax()))
+                    if graph:
+                        step = _GraphStep(model, tri.decode_cache, dev)
             t2 = time.perf_counter()
         runs[name] = {"prefill_ms": round((t1 - t0) * 1e3, 2), "decode_s": round(t2 - t1, 4),
                       "decode_tokens_per_s": round((new - 1) / (t2 - t1), 2),
-                      "generate_tokens_per_s": round(new / (t2 - t0), 2), "tokens_head": tokens[:8]}
+                      "generate_tokens_per_s": round(new / (t2 - t0), 2), "hip_graph": graph,
+                      "tokens_head": tokens[:8]}
         log(f"C4 {name}: prefill {runs[name]['prefill_ms']} ms, decode {runs[name]['decode_tokens_per_s']} tokens/s")
+    assert runs["mixed"]["tokens_head"] == runs["mixed_eager"]["tokens_head"], "graph replay changed the tokens"
     result = {
         "metric": "C4 end-to-end greedy decode tokens/s (prefill time reported separately)",
         "value": runs["mixed"]["decode_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": new,
@@ -217,8 +229,9 @@ def c4_e2e(args):
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 model; int8/int4/bf16 attention per map",
         "data": "synthetic (random-init weights N(0, 0.02), 4096 random prompt ids, seed 1004)",
         "config": {"workload": "C4 e2e: Qwen2-7B architecture (28 layers, hidden 3584, Hq 28 / Hk 4, FFN 18944, "
-                               "vocab 152064, rope 1e6), prompt 4096 + 256 greedy steps, batch 1, HF eager "
-                               "modules without the HF KV cache (the decode cache holds K/V)",
+                               "vocab 152064, rope 1e6), prompt 4096 + 256 greedy steps, batch 1, HF modules "
+                               "without the HF KV cache (the decode cache holds K/V); value: the one-token "
+                               "forward replayed as a HIP graph (mixed_eager: the same without it)",
                    "map_share": share, "global_batch": 1, "seq_len": 4096, "parallelism": "single GPU"},
         "runs": runs,
     }

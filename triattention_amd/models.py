@@ -129,18 +129,55 @@ class TriAttention:
         use_attention(model, "triattention", attention)
 
     @torch.inference_mode()
-    def generate(self, ids, max_new_tokens, eos):
+    def generate(self, ids, max_new_tokens, eos, graph=False):
         """Greedy tokens after the prompt ``ids`` [1, T], at most ``max_new_tokens``, stopping before an id
-        in ``eos`` (models.py:72-85)."""
+        in ``eos`` (models.py:72-85).
+
+        Extension: ``graph=True`` runs the first generated token's forward eagerly, captures the
+        one-token forward (every layer's projections, decode kernels and the step advance) in a
+        HIP graph, and replays it for the following tokens with the token id and position written
+        into the graph's input buffers.  Same kernels and arguments, so the same tokens."""
         out = self.model(input_ids=ids, use_cache=False, logits_to_keep=1)
         tokens = []
+        step = None
         for i in range(max_new_tokens):
             token = int(out.logits[0, -1].argmax())
             if token in eos:
                 break
             tokens.append(token)
+            if step is not None:
+                step.ids.fill_(token)
+                step.position.fill_(ids.shape[1] + i)
+                out = step.replay()
+                continue
             position = torch.tensor([[ids.shape[1] + i]], device=ids.device)
             out = self.model(input_ids=torch.tensor([[token]], device=ids.device), position_ids=position,
                              use_cache=False)
             self.decode_cache.advance()
+            if graph:
+                step = _GraphStep(self.model, self.decode_cache, ids.device)
         return tokens
+
+
+class _GraphStep:
+    """The one-token forward plus the decode step advance, captured once and replayed."""
+
+    def __init__(self, model, cache, device):
+        self.ids = torch.zeros((1, 1), dtype=torch.long, device=device)
+        self.position = torch.zeros((1, 1), dtype=torch.long, device=device)
+        # one untimed forward on a side stream first, as graph capture requires of libraries that
+        # set up state lazily; it writes the tail slot of the coming step, which the first replay
+        # rewrites, and does not advance the step
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            model(input_ids=self.ids, position_ids=self.position, use_cache=False)
+        torch.cuda.current_stream(device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = model(input_ids=self.ids, position_ids=self.position, use_cache=False)
+            cache.advance()
+
+    def replay(self):
+        self.graph.replay()
+        return self.out

@@ -81,6 +81,8 @@ class DecodeCache:
         self.layers, self.formats, self.step = {}, {}, None
         self.ragged = False
         self.out_dtype = None
+        self.meta_cache = {}
+        self.wave = None
 
     def codes(self, rows):
         if rows not in self.formats:
@@ -98,19 +100,18 @@ class DecodeCache:
         batch = vstat.shape[0]
         hk, device = vstat.shape[1], ka.device
         exact_kv = sorted(set(int(h) for h in exact_kv))
-        meta = sequence_metadata(bands, tiles, hk, codes, exact_kv)
+        meta, dev = self._metadata(bands, tiles, hk, codes, exact_kv, device)
         nbytes = batch * len(exact_kv) * tiles * KX_BYTES
-        # record indices of every sequence of the batch, sequence-major
-        seq = torch.arange(batch)[:, None] * (hk * tiles)
-        pick = lambda select: (seq + meta["rows"][select][None, :]).flatten().to(device)
-        group = dict(prompt=prompt, batch=batch, hk=hk, tiles=tiles, meta=meta,
+        # record indices of every sequence of the batch, sequence-major, built on the device
+        seq = torch.arange(batch, dtype=torch.int64, device=device)[:, None] * (hk * tiles)
+        pick = lambda kind: (seq + dev["pick"][kind][None, :]).flatten()
+        group = dict(prompt=prompt, batch=batch, hk=hk, tiles=tiles, meta=meta, dev=dev,
                      n8=int(meta["is8"].sum()), n4=int(meta["is4"].sum()),
                      nv={code: int(meta["vsel"][code].sum()) for code in (I8, I4)},
-                     fmt=codes.to(torch.int64),
-                     k8=kp.view(batch * hk * tiles, K8_WORDS).index_select(0, pick(meta["is8"])),
-                     k4=(k4.view(batch * hk * tiles, K4_WORDS).index_select(0, pick(meta["is4"]))
+                     k8=kp.view(batch * hk * tiles, K8_WORDS).index_select(0, pick("k8")),
+                     k4=(k4.view(batch * hk * tiles, K4_WORDS).index_select(0, pick("k4"))
                          if bool(meta["is4"].any()) else None),
-                     v={code: (packed[code].view(batch * hk * tiles, WORDS[code]).index_select(0, pick(meta["vsel"][code]))
+                     v={code: (packed[code].view(batch * hk * tiles, WORDS[code]).index_select(0, pick(code))
                                if bool(meta["vsel"][code].any()) else None) for code in (I8, I4)},
                      ka=ka.view(batch, hk, tiles, 4), ka4=ka4.view(batch, hk, tiles, 4) if ka4 is not None else None,
                      kstat=kstat.view(batch, hk, 3, 128), vstat=vstat.view(batch, hk, 3, 128), exact=exact_kv,
@@ -123,46 +124,67 @@ class DecodeCache:
         groups = entry["groups"] + [group] if (self.ragged and entry is not None) else [group]
         self.layers[layer] = self._assemble(groups, device)
 
+    def _metadata(self, bands, tiles, hk, codes, exact_kv, device):
+        """One sequence's metadata (host, closed-form integer code) and its device copy, cached per
+        (bands, tiles, KV heads, exact heads, device): every sequence of the same length shares it."""
+        b = torch.as_tensor(bands, dtype=torch.int32).cpu()
+        key = (b.numpy().tobytes(), tiles, hk, tuple(exact_kv), str(device))
+        hit = self.meta_cache.get(key)
+        if hit is None:
+            meta = sequence_metadata(b, tiles, hk, codes, exact_kv)
+            to = lambda x: x.to(device)
+            dev = dict(valid=to(meta["valid"]), order=to(meta["order"]), is4=to(meta["is4"]),
+                       kslot=to(meta["kslot"]), kbase=to(meta["kbase"]), vcode=to(meta["vcode"]),
+                       vslot=to(meta["vslot"]), count=to(meta["count"]), fmt=to(codes.to(torch.int64) - 1),
+                       pick={kind: to(meta["rows"][select]) for kind, select in
+                             (("k8", meta["is8"]), ("k4", meta["is4"]), (I8, meta["vsel"][I8]),
+                              (I4, meta["vsel"][I4]))})
+            hit = self.meta_cache[key] = (meta, dev)
+        return hit
+
     def _assemble(self, groups, device):
-        """Batched metadata and concatenated records over every stored sequence."""
+        """Batched metadata and concatenated records over every stored sequence: a few device
+        operations per group (a store's sequences share one length), none per sequence."""
         hk = groups[0]["hk"]
         total = sum(g["batch"] for g in groups)
         tiles_max = max(g["tiles"] for g in groups)
         maxn = max(g["meta"]["maxn"] for g in groups)
-        entry = torch.zeros((total, hk, maxn), dtype=torch.int64)
+        i64 = dict(dtype=torch.int64, device=device)
+        entry = torch.zeros((total, hk, maxn), **i64)
         kinfo = torch.zeros_like(entry)
         slot = torch.zeros_like(entry)
-        count = torch.zeros((total, hk), dtype=torch.int64)
-        fmt = torch.ones((total, tiles_max), dtype=torch.int64)
-        prompt = torch.zeros(total, dtype=torch.int64)
+        count = torch.zeros((total, hk), **i64)
+        fmt = torch.ones((total, tiles_max), **i64)
+        prompt = torch.zeros(total, **i64)
         has4 = any(g["k4"] is not None for g in groups)
         ka = torch.ones((total, hk, tiles_max, 4), dtype=torch.float32, device=device)
         ka4 = torch.ones_like(ka) if has4 else None
         kstat = torch.empty((total, hk, 3, 128), dtype=torch.float32, device=device)
         vstat = torch.empty_like(kstat)
         k8s, k4s, v8s, v4s, kxs, vxs = [], [], [], [], [], []
-        xslot = torch.full((total, hk), -1, dtype=torch.int64)
+        xslot = torch.full((total, hk), -1, **i64)
         o8 = o4 = ov8 = ov4 = ox = 0
         row = 0
         for g in groups:
-            m, n, b = g["meta"], g["meta"]["maxn"], g["batch"]
-            for s in range(b):
-                r = row + s
-                entry[r, :, :n] = torch.where(m["valid"], m["order"], 0)
-                ks = torch.where(m["is4"], m["kslot"] + o4 + s * g["n4"], m["kslot"] + o8 + s * g["n8"])
-                kinfo[r, :, :n] = torch.where(m["valid"], m["kbase"] | (ks << 9), 0)
-                vs = torch.where(m["vcode"] == I4, m["vslot"] + ov4 + s * g["nv"][I4], m["vslot"] + ov8 + s * g["nv"][I8])
-                slot[r, :, :n] = torch.where(m["valid"], vs, 0)
-                count[r] = m["count"]
-                fmt[r, :g["tiles"]] = g["fmt"] - 1
-                prompt[r] = g["prompt"]
-                for xs, h in enumerate(g["exact"]):
-                    xslot[r, h] = ox + (s * len(g["exact"]) + xs) * g["tiles"]
-            ka[row:row + b, :, :g["tiles"]] = g["ka"]
+            d, n, b, tiles = g["dev"], g["meta"]["maxn"], g["batch"], g["tiles"]
+            rows = slice(row, row + b)
+            sq = torch.arange(b, **i64)
+            s3 = sq[:, None, None]
+            entry[rows, :, :n] = torch.where(d["valid"], d["order"], 0)
+            ks = torch.where(d["is4"], d["kslot"] + o4 + s3 * g["n4"], d["kslot"] + o8 + s3 * g["n8"])
+            kinfo[rows, :, :n] = torch.where(d["valid"], d["kbase"] | (ks << 9), 0)
+            vs = torch.where(d["vcode"] == I4, d["vslot"] + ov4 + s3 * g["nv"][I4], d["vslot"] + ov8 + s3 * g["nv"][I8])
+            slot[rows, :, :n] = torch.where(d["valid"], vs, 0)
+            count[rows] = d["count"]
+            fmt[rows, :tiles] = d["fmt"]
+            prompt[rows] = g["prompt"]
+            for xs, h in enumerate(g["exact"]):
+                xslot[rows, h] = ox + (sq * len(g["exact"]) + xs) * tiles
+            ka[rows, :, :tiles] = g["ka"]
             if g["ka4"] is not None and ka4 is not None:
-                ka4[row:row + b, :, :g["tiles"]] = g["ka4"]
-            kstat[row:row + b] = g["kstat"]
-            vstat[row:row + b] = g["vstat"]
+                ka4[rows, :, :tiles] = g["ka4"]
+            kstat[rows] = g["kstat"]
+            vstat[rows] = g["vstat"]
             k8s.append(g["k8"])
             if g["k4"] is not None:
                 k4s.append(g["k4"])
@@ -173,21 +195,22 @@ class DecodeCache:
             if g["exact"]:
                 kxs.append(g["kx"])
                 vxs.append(g["vx"])
-                ox += b * len(g["exact"]) * g["tiles"]
+                ox += b * len(g["exact"]) * tiles
             o8 += b * g["n8"]
             o4 += b * g["n4"]
             ov8 += b * g["nv"][I8]
             ov4 += b * g["nv"][I4]
             row += b
-        # a record kind no tile uses (e.g. every KV head exact) gets one zero record: the kernel takes
-        # non-empty record arrays and never reads it
         cat = lambda parts, words: (torch.cat(parts) if sum(p.shape[0] for p in parts) else
                                     torch.zeros((1, words), dtype=torch.uint32, device=device))
-        cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
-            torch.cuda.get_device_properties(device).multi_processor_count
-        wave = cus * max(1, self.module.decode_occupancy())
-        # split size (decode.py:54-55); the kernel takes at most 64 tiles per split
-        per = min(64, max(1, -(-int(count.sum()) // wave)))
+        if self.wave is None:
+            cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
+                torch.cuda.get_device_properties(device).multi_processor_count
+            self.wave = cus * max(1, self.module.decode_occupancy())
+        # split size (decode.py:54-55), from the host copy of the counts (no device sync); the
+        # kernel takes at most 64 tiles per split
+        kept = sum(g["batch"] * int(g["meta"]["count"].sum()) for g in groups)
+        per = min(64, max(1, -(-kept // self.wave)))
         to = lambda x: x.to(torch.int32).to(device)
         tail_k = torch.zeros((total, hk, self.max_tail, 128), dtype=torch.bfloat16, device=device)
         return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, fmt=to(fmt), slot=to(slot), entry=to(entry),

@@ -252,6 +252,17 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   d.per = per;
   d.tiles_max = tiles_max;
   d.splits = splits;
+  {
+    // a prime that does not divide the grid size, so lin -> lin * scatter mod grid is a permutation
+    const int64_t grid_size = (int64_t)splits * hk * batch;
+    const int primes[3] = {1000003, 1000033, 1000037};
+    d.scatter = primes[0];
+    for (int p : primes)
+      if (grid_size % p != 0) {
+        d.scatter = p;
+        break;
+      }
+  }
   d.sm_log2 = (float)(scale * 1.4426950408889634);
   d.k8_bytes = (int)(n_k8 * tri::K8_BYTES);
   d.k4_bytes = k4c ? (int)(n_k4 * tri::K4_BYTES) : 0;

@@ -44,6 +44,7 @@ struct DecodeArgs {
   const float* kstat;   // [B][Hk][3][128]: K mean (the frame of the merge's tail scores)
   const float* vstat;   // [B][Hk][3][128]: V mean, scale, 1/scale
   int kx_bytes;
+  int scatter;          // prime coprime to the grid size: workgroup lin takes work item lin * scatter mod grid
 };
 
 constexpr int MAX_TAIL = 1024;
@@ -185,20 +186,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   __shared__ __align__(16) int4 meta[MAX_PER + 1];     // per-tile record offsets and flags
   __shared__ __align__(16) float4 metk[MAX_PER + 1];   // per-tile K group scales
 
-  // Workgroups are dealt to the 8 XCDs round-robin by linear id; XCD x takes
-  // the x-th contiguous eighth of the (sequence, KV head, split) space, so each
-  // XCD gets every split position (the last splits hold the INT8-V tiles, and
-  // split = id % 8 would load one XCD with all of them).
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id.  Work item w = lin * scatter mod
+  // grid scatters each head's splits over the XCDs and CUs: the last splits of a head hold its
+  // INT8-V tiles, and in a ragged batch the long sequences' splits would otherwise crowd the
+  // XCDs that receive them.  (Splits share no data but Q, so nothing is lost in L2.)
   int split, kh, b;
   {
     const int nsplit = gridDim.x, nkh = gridDim.y;
     const int total = nsplit * nkh * gridDim.z;
     const int lin = blockIdx.x + nsplit * (blockIdx.y + nkh * blockIdx.z);
-    const int q8 = total >> 3, r8 = total & 7, x = lin & 7;
-    const int w = x * q8 + min(x, r8) + (lin >> 3);
+    const int w = (int)(((int64_t)lin * a.scatter) % total);
     split = w % nsplit;
     kh = (w / nsplit) % nkh;
     b = w / (nsplit * nkh);
+  }
+  // A split past its head's kept tiles (ragged batches: most splits of the short sequences)
+  // writes the empty partial (m = -FLT_MAX, l = 0, o = 0) and leaves.
+  if (split * a.per >= a.count[(int64_t)b * a.hk + kh]) {
+    const int L = threadIdx.x, g = a.hq / a.hk;
+    for (int r = 0; r < g; ++r) {
+      const int64_t idx = ((int64_t)b * a.hq + kh * g + r) * a.splits + split;
+      *reinterpret_cast<float2*>(a.po + idx * D + 2 * L) = make_float2(0.f, 0.f);
+      if (L == 0) {
+        a.pm[idx] = -3.402823466e38f;
+        a.pl[idx] = 0.f;
+      }
+    }
+    return;
   }
   if constexpr (EXACT) {
     if (a.xslot[(int64_t)b * a.hk + kh] >= 0) {

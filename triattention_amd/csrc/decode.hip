@@ -6,10 +6,11 @@
 //
 // One 64-lane wave per (sequence, KV head, split).  The kept tiles of a split
 // stream straight from HBM into MFMA operand registers (one 16-byte load per
-// lane per 1 KiB fragment, next tile prefetched while the current one is
-// processed); no LDS staging is needed because every fragment is consumed by
-// exactly one wave.  The g <= 8 query heads of the KV group occupy columns
-// 0..g-1 of the 32-wide MFMA B operand.
+// lane per 1 KiB fragment, the next tile's K and V issued while the current one
+// is processed); no LDS staging is needed because every fragment is consumed by
+// exactly one wave.  Quantized heads: the g <= 8 query heads of the KV group
+// are the rows of the MFMA A operand (S = Q K^T, one key per lane and row
+// block); exact heads: they are the columns of the B operand (S^T = K Q^T).
 #include "common.h"
 
 namespace tri {

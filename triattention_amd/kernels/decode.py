@@ -19,6 +19,8 @@ op then serves the whole ragged batch in one launch.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from .extension import _geometry
@@ -28,6 +30,7 @@ WORDS = {I8: 2048, I4: 1024}
 K8_WORDS, K4_WORDS = 2048, 1024
 KX_BYTES = 16384
 NEAR_V8 = 16
+SPLITS_PER_CU = 4  # decode workgroups per CU that the split size targets
 
 
 def tile_states(bands: torch.Tensor, tiles: int) -> torch.Tensor:
@@ -206,11 +209,17 @@ class DecodeCache:
         if self.wave is None:
             cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
                 torch.cuda.get_device_properties(device).multi_processor_count
-            self.wave = cus * max(1, self.module.decode_occupancy())
-        # split size (decode.py:54-55), from the host copy of the counts (no device sync); the
-        # kernel takes at most 64 tiles per split
+            self.wave = cus * max(1, min(self.module.decode_occupancy(), SPLITS_PER_CU))
+        # Split size, from the host copy of the counts (no device sync).  The reference spreads
+        # the kept tiles over one full wave of resident workgroups (decode.py:54-55); here over
+        # SPLITS_PER_CU workgroups per CU, and every average head gets at least 4 splits.  One
+        # wave per SIMD streams as many tiles per second as two (each wave is bound by its own
+        # per-tile instruction stream), so fewer, longer splits save prologues and partials
+        # (C1: 37 vs 41 us), while ragged batches need the splits to spread their long heads
+        # (C3: 133 us at 24 tiles per split, 157 us at 48).  At most 64 tiles per split.
         kept = sum(g["batch"] * int(g["meta"]["count"].sum()) for g in groups)
-        per = min(64, max(1, -(-kept // self.wave)))
+        mean = kept / max(1, total * hk)
+        per = min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 4))))
         to = lambda x: x.to(torch.int32).to(device)
         tail_k = torch.zeros((total, hk, self.max_tail, 128), dtype=torch.bfloat16, device=device)
         return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, fmt=to(fmt), slot=to(slot), entry=to(entry),

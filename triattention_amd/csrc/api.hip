@@ -57,7 +57,7 @@ int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, cons
     return fail("prepare_qk: output buffers must be 16-byte aligned");
   const int tiles = (t + tri::BN - 1) / tri::BN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  tri::quantize_q_kernel<<<dim3((t + 7) / 8, hq, batch), 256, 0, s>>>(
+  tri::quantize_q_kernel<<<dim3((t + 31) / 32, hq, batch), 256, 0, s>>>(
       static_cast<const uint16_t*>(q), q_sb, q_sh, q_st, hq, t, static_cast<int8_t*>(q8), qa,
       static_cast<uint8_t*>(q4), qa4);
   tri::partial_kernel<<<dim3(tri::STAT_BLOCKS, hk, batch), tri::D, 0, s>>>(static_cast<const uint16_t*>(k), k_sb,

@@ -8,35 +8,50 @@
 
 namespace tri {
 
-// One 128-feature row per 32 lanes, 8 rows per 256-thread block.
+// One 128-feature row per 8 lanes (16 features per lane, rotated with DPP lane
+// moves by rotate128_x16), 32 rows per 256-thread block.
 // common_device.cuh:1-28 (quantize_q_kernel).
 __global__ __launch_bounds__(256) void quantize_q_kernel(const uint16_t* __restrict__ q, int64_t sb, int64_t sh,
                                                          int64_t st, int hq, int t, int8_t* __restrict__ q8,
                                                          float* __restrict__ qa, uint8_t* __restrict__ q4,
                                                          float* __restrict__ qa4) {
-  const int l32 = threadIdx.x & 31, row = blockIdx.x * 8 + (threadIdx.x >> 5), h = blockIdx.y, b = blockIdx.z;
-  if (row >= t) return;  // whole 32-lane groups leave together
-  const uint2 raw = *reinterpret_cast<const uint2*>(q + b * sb + h * sh + (int64_t)row * st + l32 * 4);
-  float x[4] = {bf16f(raw.x & 0xffffu), bf16f(raw.x >> 16), bf16f(raw.y & 0xffffu), bf16f(raw.y >> 16)};
-  rotate128_x4(x, l32);
+  const int sub = threadIdx.x & 7, row = blockIdx.x * 32 + (threadIdx.x >> 3), h = blockIdx.y, b = blockIdx.z;
+  if (row >= t) return;  // whole 8-lane groups leave together
+  const uint16_t* src = q + b * sb + h * sh + (int64_t)row * st + sub * 16;
+  float x[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(src + 4 * i);
+    x[4 * i] = bf16f(raw.x & 0xffffu);
+    x[4 * i + 1] = bf16f(raw.x >> 16);
+    x[4 * i + 2] = bf16f(raw.y & 0xffffu);
+    x[4 * i + 3] = bf16f(raw.y >> 16);
+  }
+  rotate128_x16(x, sub);
   float m = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(x[i]));
-  m = warp32_max(m);
+  for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(x[i]));
+  m = lanes8_max(m);
   const int64_t r = ((int64_t)b * hq + h) * t + row;
   const float inv = m > 0.f ? 127.f / m : 0.f;
-  uint32_t word = 0;
+  uint32_t w[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) word |= ((uint32_t)(int)__builtin_rintf(x[i] * inv) & 0xffu) << (8 * i);
-  reinterpret_cast<uint32_t*>(q8 + r * D)[l32] = word;
-  if (l32 == 0) qa[r] = m / 127.f;
+  for (int k = 0; k < 4; ++k) {
+    w[k] = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[k] |= ((uint32_t)(int)__builtin_rintf(x[4 * k + i] * inv) & 0xffu) << (8 * i);
+  }
+  *reinterpret_cast<uint4*>(q8 + r * D + sub * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  if (sub == 0) qa[r] = m / 127.f;
   if (q4 != nullptr) {
     const float inv4 = m > 0.f ? 7.f / m : 0.f;
-    uint32_t nib = 0;
+    uint32_t nib[2] = {0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) nib |= ((uint32_t)(int)__builtin_rintf(x[i] * inv4) & 0xfu) << (4 * i);
-    reinterpret_cast<uint16_t*>(q4 + r * (D / 2))[l32] = (uint16_t)nib;
-    if (l32 == 0) qa4[r] = m / 7.f;
+    for (int i = 0; i < 16; ++i) nib[i >> 3] |= ((uint32_t)(int)__builtin_rintf(x[i] * inv4) & 0xfu) << (4 * (i & 7));
+    uint32_t* dst = reinterpret_cast<uint32_t*>(q4 + r * (D / 2) + sub * 8);
+    dst[0] = nib[0];
+    dst[1] = nib[1];
+    if (sub == 0) qa4[r] = m / 7.f;
   }
 }
 

@@ -106,7 +106,8 @@ __global__ __launch_bounds__(128) void finalize_kernel(const float* __restrict__
   stat[hb * 3 * D + 2 * D + c] = 1.f / scale;
 }
 
-// y = R(k - mean) for one 64-key tile; wave w owns the 16-key group w.
+// y = R(k - mean) for one 64-key tile; wave w owns the 16-key group w, one key
+// per 8 lanes (16 features per lane, DPP rotation), two passes of 8 keys.
 // INT8 record + group scale ka, optional INT4 record + ka4.
 // common_device.cuh:58-131 (quantize_k_kernel).
 __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restrict__ k, int64_t sb, int64_t sh,
@@ -116,34 +117,39 @@ __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restr
   __shared__ __align__(16) uint8_t c8[BN][D];
   __shared__ __align__(16) uint8_t c4[BN][D];
   const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, sub = lane & 7;
   const int64_t hb = (int64_t)b * hk + hd;
-  const float* mean = kstat + hb * 3 * D;
-  float mc[4];
+  const float* mean = kstat + hb * 3 * D + sub * 16;
+  float mc[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) mc[i] = mean[l32 * 4 + i];
-  float y[8][4];
+  for (int i = 0; i < 16; ++i) mc[i] = mean[i];
+  float y[2][16];
   float cm = 0.f;
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int r = wave * 16 + it * 2 + half, tk = tile * BN + r;
-    float x[4] = {0.f, 0.f, 0.f, 0.f};
-    if (tk < t) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(k + b * sb + hd * sh + (int64_t)tk * st + l32 * 4);
-      x[0] = bf16f(raw.x & 0xffffu) - mc[0];
-      x[1] = bf16f(raw.x >> 16) - mc[1];
-      x[2] = bf16f(raw.y & 0xffffu) - mc[2];
-      x[3] = bf16f(raw.y >> 16) - mc[3];
-    }
-    rotate128_x4(x, l32);  // every lane of the wave takes part (padded rows rotate zeros)
+  for (int it = 0; it < 2; ++it) {
+    const int r = wave * 16 + it * 8 + (lane >> 3), tk = tile * BN + r;
+    float x[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 16; ++i) x[i] = 0.f;
+    if (tk < t) {
+      const uint16_t* src = k + b * sb + hd * sh + (int64_t)tk * st + sub * 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint2 raw = *reinterpret_cast<const uint2*>(src + 4 * i);
+        x[4 * i] = bf16f(raw.x & 0xffffu) - mc[4 * i];
+        x[4 * i + 1] = bf16f(raw.x >> 16) - mc[4 * i + 1];
+        x[4 * i + 2] = bf16f(raw.y & 0xffffu) - mc[4 * i + 2];
+        x[4 * i + 3] = bf16f(raw.y >> 16) - mc[4 * i + 3];
+      }
+    }
+    rotate128_x16(x, sub);  // every lane of the wave takes part (padded rows rotate zeros)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
       y[it][i] = x[i];
       cm = fmaxf(cm, fabsf(x[i]));
     }
   }
-#pragma unroll
-  for (int o = 32; o; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 64));
+  cm = wave_max(cm);
   const float inv = cm > 0.f ? 127.f / cm : 0.f, inv4 = cm > 0.f ? 7.f / cm : 0.f;
   const int64_t si = (hb * tiles + tile) * 4 + wave;
   if (lane == 0) {
@@ -151,16 +157,21 @@ __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restr
     if (k4 != nullptr) ka4[si] = cm > 0.f ? cm / 7.f : 1.f;
   }
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int r = wave * 16 + it * 2 + half;
-    uint32_t w8 = 0, w4 = 0;
+  for (int it = 0; it < 2; ++it) {
+    const int r = wave * 16 + it * 8 + (lane >> 3);
+    uint32_t w8[4], w4[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      w8 |= ((uint32_t)(int)__builtin_rintf(y[it][i] * inv) & 0xffu) << (8 * i);
-      w4 |= ((uint32_t)(int)__builtin_rintf(y[it][i] * inv4) & 0xfu) << (8 * i);
+    for (int q = 0; q < 4; ++q) {
+      w8[q] = 0u;
+      w4[q] = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w8[q] |= ((uint32_t)(int)__builtin_rintf(y[it][4 * q + i] * inv) & 0xffu) << (8 * i);
+        w4[q] |= ((uint32_t)(int)__builtin_rintf(y[it][4 * q + i] * inv4) & 0xfu) << (8 * i);
+      }
     }
-    *reinterpret_cast<uint32_t*>(&c8[r][l32 * 4]) = w8;
-    *reinterpret_cast<uint32_t*>(&c4[r][l32 * 4]) = w4;
+    *reinterpret_cast<uint4*>(&c8[r][sub * 16]) = make_uint4(w8[0], w8[1], w8[2], w8[3]);
+    *reinterpret_cast<uint4*>(&c4[r][sub * 16]) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
   }
   __syncthreads();
   uint8_t* rec8 = k8 + (hb * tiles + tile) * K8_BYTES;

@@ -14,6 +14,7 @@ and the ragged decode of configs[3] (C3).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-c3]
        python bench.py --c4   (configs[4]: end-to-end greedy generation, one JSON line of its own)
+       python bench.py --calibrate   (the calibration sweep's Prefill executors sharing scratch)
        python bench.py --copy-probe   (a plain 256 MiB device copy, five times: the
        known-size kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)
 
@@ -238,6 +239,54 @@ def c4_e2e(args):
     print(json.dumps(result))
 
 
+def calibration_sweep(args):
+    """configs-adjacent consumer measurement (calibrate.py:44-64): every distance-band configuration of
+    the calibration grid as its own Prefill executor, all sharing one scratch dict, over one
+    Qwen2-7B-shape attention layer (B 1, Hq 28 / Hk 4, T 4096).  Reports the sweep's time."""
+    import torch
+
+    from triattention_amd import synthetic as S
+    from triattention_amd.kernels.extension import load_extension
+    from triattention_amd.kernels.prefill import Prefill
+    from triattention_amd.maps import INF, uniform
+
+    w8s = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, INF)
+    w4s = (2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, INF)
+    grid = [(w8, w4) for w8 in w8s for w4 in sorted({w8, *w4s}) if w4 >= w8 and not (w8 == INF and w4 != INF)]
+    dev = torch.device("cuda:0")
+    module = load_extension()
+    g = torch.Generator(device=dev).manual_seed(1005)
+    t = 4096
+    q, k, v = (S.outlier_tensor_device(g, 1, 28, t), S.outlier_tensor_device(g, 1, 4, t),
+               S.outlier_tensor_device(g, 1, 4, t))
+    shared = {}
+    executors = []
+    for w8, w4 in grid:
+        executors.append(Prefill(module, uniform(w8, w4)))
+        executors[-1].buffers = shared
+    for pre in executors:  # builds every band table and view
+        pre(0, q, k, v, 128 ** -0.5)
+    torch.cuda.synchronize()
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for pre in executors:
+            pre(0, q, k, v, 128 ** -0.5)
+    torch.cuda.synchronize()
+    sweep_ms = (time.perf_counter() - t0) / reps * 1e3
+    scratch = sum(b.numel() * b.element_size() for b in shared.values())
+    log(f"calibration sweep: {len(grid)} executors, {sweep_ms:.1f} ms per sweep, shared scratch {scratch / 2**20:.1f} MiB")
+    print(json.dumps({
+        "metric": "calibration sweep time (all band configurations of one layer, shared scratch)",
+        "value": round(sweep_ms, 3), "unit": "ms", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": round(sweep_ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8/int4 codes, fp32 softmax", "data": "synthetic (device-drawn N(0,1) with outlier channels)",
+        "config": {"workload": f"calibrate.py pattern: {len(grid)} Prefill executors with uniform bands sharing one "
+                               "scratch dict, one Qwen2-7B-shape layer (B 1, Hq 28 / Hk 4, T 4096)",
+                   "executors": len(grid), "per_executor_ms": round(sweep_ms / len(grid), 4),
+                   "shared_scratch_bytes": scratch, "parallelism": "single GPU"}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,12 +298,16 @@ def main():
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--c4", action="store_true", help="run the C4 end-to-end generation instead")
+    ap.add_argument("--calibrate", action="store_true", help="time the calibration sweep's Prefill executors instead")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
         return
     if args.c4 and args.gpus == 1:
         c4_e2e(args)
+        return
+    if args.calibrate and args.gpus == 1:
+        calibration_sweep(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",

@@ -284,3 +284,24 @@ def test_config2_shape_slice(module):
     bar = exact_max_abs_bar(c["q"], c["k"], c["v"], c["scale"], exact_q, ex)
     mx, _ = assert_close(out.numpy()[:, exact_q], ex[:, exact_q], max_abs=bar, what="config 2 exact heads")
     print(f"config2 exact heads: max abs {mx:.3e}, bar {bar:.3e} (fp32 SDPA vs float64)")
+
+
+def test_shared_scratch_executors(module):
+    """Calibration's pattern (calibrate.py:44-48): many Prefill executors with different uniform bands
+    share one scratch dict; each must return what an executor with its own scratch returns."""
+    print("\n[parity] shared-scratch Prefill executors", flush=True)
+    from triattention_amd.maps import uniform
+    q, k, v = small(6100, 1, 6, 2, 300)
+    dev = torch.device("cuda")
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    configs = [(1, 2), (2, 8), (INF, INF), (1, INF), (4, 4), (16, INF)]
+    shared = {}
+    outs = []
+    for w8, w4 in configs:
+        pre = Prefill(module, uniform(w8, w4), out_dtype=torch.float32)
+        pre.buffers = shared
+        outs.append(pre(0, q, k, v, 128 ** -0.5).clone())
+    # a second pass over the same executors, then fresh executors with their own scratch
+    for (w8, w4), first in zip(configs, outs):
+        alone = Prefill(module, uniform(w8, w4), out_dtype=torch.float32)(0, q, k, v, 128 ** -0.5)
+        assert torch.equal(first, alone), (w8, w4)

@@ -105,30 +105,6 @@ __device__ __forceinline__ float texp2_p(float x) {
 __device__ __forceinline__ uint32_t rot_word(int w) {
   return w == 0 ? 0x9a3b5e71u : w == 1 ? 0x2c6d8f13u : w == 2 ? 0xe41b7a95u : 0x5f02c3d8u;
 }
-__device__ __forceinline__ bool rot_sign(int c) { return (rot_word(c >> 5) >> (c & 31)) & 1u; }
-
-// Rotation of one 128-vector held by 32 consecutive lanes, 4 channels each
-// (channel 4*l + i in lane l of the 32-lane group).  Butterfly stages run over
-// index bits 0..6 in order, (lo, hi) -> (lo + hi, lo - hi).
-__device__ __forceinline__ void rotate128_x4(float (&x)[4], int l32) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (rot_sign(l32 * 4 + i)) x[i] = -x[i];
-  const float a = x[0] + x[1], b = x[0] - x[1], c = x[2] + x[3], d = x[2] - x[3];
-  x[0] = a + c; x[1] = b + d; x[2] = a - c; x[3] = b - d;
-#pragma unroll
-  for (int bit = 1; bit < 32; bit <<= 1) {
-    const bool upper = l32 & bit;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float y = __shfl_xor(x[i], bit, 32);
-      x[i] = upper ? y - x[i] : x[i] + y;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] *= 0.08838834764831845f;
-}
-
 // DPP lane moves within 16-lane rows: quad_perm [1,0,3,2] (lane ^ 1), quad_perm
 // [2,3,0,1] (lane ^ 2), quad_perm [3,2,1,0] (lane ^ 3), row_half_mirror (lane
 // 7 - i of each 8), row_mirror (lane 15 - i of each 16).  VALU operations,
@@ -158,9 +134,10 @@ __device__ __forceinline__ void rot_stage8(float (&x)[16], int t) {
 }
 
 // Rotation of one 128-vector held by 8 consecutive lanes, 16 channels each
-// (channel 16*t + i in lane t of the 8-lane group): the same butterfly stages,
-// in the same order and with the same operands, as rotate128_x4, so the
-// results are identical.  Cross-lane stages are DPP moves.
+// (channel 16*t + i in lane t of the 8-lane group), prefill_sm80.cu:95-115: sign
+// flips, then butterfly stages over index bits 0..6 in order, (lo, hi) ->
+// (lo + hi, lo - hi), then the 1/sqrt(128) scale.  Bits 0-3 are in-register
+// stages, bits 4-6 cross-lane stages through DPP moves.
 __device__ __forceinline__ void rotate128_x16(float (&x)[16], int t) {
   const uint32_t sg = rot_word(t >> 1) >> (16 * (t & 1));
 #pragma unroll
@@ -189,11 +166,6 @@ __device__ __forceinline__ float lanes8_max(float m) {
   return fmaxf(m, lane_xor8<4>(m));
 }
 
-__device__ __forceinline__ float warp32_max(float m) {
-#pragma unroll
-  for (int o = 16; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
-  return m;
-}
 
 
 // DPP move restricted to the 16-lane rows in ROWS; other rows keep v.  Row
@@ -231,20 +203,6 @@ __device__ __forceinline__ float half_max(float v, bool upper) {
   return upper ? hi : lo;
 }
 
-// Maximum over each 32-lane half of the wave (LANES = 32) or over the whole wave
-// (LANES = 64), in every lane: four DPP steps reduce each 16-lane row (after the
-// quad steps every lane holds its quad's maximum, the half mirror pairs quads,
-// the mirror pairs 8-lane halves), then one or two lane-xor exchanges.
-template <int LANES>
-__device__ __forceinline__ float lanes_max(float v) {
-  v = fmaxf(v, dpp_move<0xB1>(v));
-  v = fmaxf(v, dpp_move<0x4E>(v));
-  v = fmaxf(v, dpp_move<0x141>(v));
-  v = fmaxf(v, dpp_move<0x140>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  if constexpr (LANES == 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
-}
 
 // byte 1 of each of four words, packed (P levels out of the 49152.5 magic).
 __device__ __forceinline__ uint32_t pack_byte1(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {

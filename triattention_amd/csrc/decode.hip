@@ -683,7 +683,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   __syncthreads();
   float m = pm_own;
   for (int t = tid; t < tail; t += 256) m = fmaxf(m, ts[t]);
-  m = lanes_max<64>(m);
+  m = wave_max(m);
   if (lane == 0) wred[wave][0] = m;
   __syncthreads();
   m = fmaxf(fmaxf(wred[0][0], wred[1][0]), fmaxf(wred[2][0], wred[3][0]));

@@ -20,13 +20,17 @@
  *  - IEEE-754 binary32 with round-to-nearest-even and denormals kept.  The
  *    reference was built with --use_fast_math; its approximate division,
  *    reciprocal and exp2 are replaced by IEEE division and by ora_texp2 below.
- *  - ora_texp2 is the one exp2 of the path: x clamped to >= -125, n = rint(x),
- *    f = x - n, a degree-6 polynomial for 2^f evaluated by fmaf in Horner
- *    order, scaled by 2^n.  Max error 0.93 ulp over [-125, 0].  The GPU
- *    kernels compute the same function, so quantized P levels (discrete
- *    functions of exp2) agree bit for bit; they obtain n from the 1.5*2^23
- *    shifter and add it to the exponent field instead of calling rint/ldexp.
- *    ora_texp2_shifter restates that form so tests can pin the equality.
+ *  - ora_texp2 is the one exp2 of the oracle: x clamped to >= -125,
+ *    n = rint(x), f = x - n, a degree-6 polynomial for 2^f evaluated by fmaf
+ *    in Horner order, scaled by 2^n.  Max error 0.93 ulp over [-125, 0].
+ *    The GPU kernels compute the same function for the per-tile factors and
+ *    the merge weights (n from the 1.5*2^23 shifter, added to the exponent
+ *    field; ora_texp2_shifter restates that form so tests can pin the
+ *    equality).  For the per-score probabilities (P levels, fp16 P) they use
+ *    the hardware exp2 (v_exp_f32, ~1 ulp), as the reference uses the
+ *    hardware ex2.approx: a P level then differs from this oracle's only
+ *    where e * levels falls within a few ulp of a rounding boundary, and
+ *    the outputs stay far inside the parity tolerance.
  *  - Per-element expressions that decide discrete values (codes, P levels,
  *    fp16 probabilities) follow the reference's operation sequence literally,
  *    including the 1.5*2^23 "magic" offset in the 8-bit score argument

@@ -41,6 +41,21 @@ def test_codes_and_output_small(module, t):
     assert_close(out.numpy(), ref, what=f"prefill t={t}")
 
 
+def test_zero_query_and_key_rows(module):
+    """All-zero query rows (scale 0, so every score of the row is 0 and masked keys give 0 * -inf) and
+    all-zero key rows: outputs finite and within the parity bar, codes bit-exact."""
+    print("\n[parity] prefill t=150 with zero query / key rows", flush=True)
+    q, k, v = small(2500, 1, 6, 2, 150)
+    q[0, :, [0, 5, 64, 149]] = 0
+    q[0, 2, 70:90] = 0
+    k[0, 1, [3, 64, 100]] = 0
+    bands = torch.tensor(MIXED, dtype=torch.int32)
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5)
+    ref, codes = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    compare_codes(ops, codes[0], 0, 1, 6, 2, 150)
+    assert_close(out.numpy(), ref, what="prefill with zero rows")
+
+
 def test_batch_and_band_variety(module):
     print("\n[parity] batch=2 t=333 assorted bands", flush=True)
     q, k, v = small(3000, 2, 8, 2, 333)

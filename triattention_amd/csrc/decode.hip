@@ -500,7 +500,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
                     : __builtin_fmaf(slope[r][t], __uint_as_float(MAGIC_BITS + (uint32_t)d), c);
           dith |= (uint32_t)d & 0xffu;
         }
-        const uint32_t y = __float_as_uint(__builtin_fmaf(texp2(arg), levels, __uint_as_float(dith)));
+        const uint32_t y = __float_as_uint(__builtin_fmaf(pexp2(arg), levels, __uint_as_float(dith)));
         const uint32_t p = (y >> 8) & 0xffu;
         psum += p;
         pls[qrow(r)][kb * 32 + lq] = (uint8_t)p;

@@ -146,7 +146,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int gi = kb * 2 + (r >> 3);
-        const _Float16 h = (_Float16)texp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
+        // (a zero query row has slope 0, and 0 * -inf of a masked key is NaN: the clamp turns it
+        // into 2^-125, which rounds to fp16 0 as the masked key's probability must)
+        const _Float16 h = (_Float16)pexp2(fmaxf(__builtin_fmaf(slope[gi], score(kb, r), c[gi]), -125.f));
         p[kb][r >> 3][r & 7] = h;
         psum += (float)h;
       }
@@ -183,7 +185,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = qd * 4 + i, gi = kb * 2 + (r >> 3);
-          const float e = texp2_p(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
+          const float e = pexp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
           y[i] = __float_as_uint(__builtin_fmaf(e, 255.f, PMAGIC_HALF));
         }
         const uint32_t w = pack_byte1(y[0], y[1], y[2], y[3]);

@@ -463,7 +463,7 @@ def main():
         times, errs = [], []
         for rep in range(3):
             t0 = time.perf_counter()
-            outs = [O.decode(sample[b], bands.numpy(), S.bits(qb[b, :, 0]), prompt, e["per"], scale, zeros, zeros,
+            outs = [O.decode(sample[b], bands.numpy(), S.bits(qb[b, :, 0]), prompt, cache.split_of(0, b), scale, zeros, zeros,
                              S.bits(kb[b, :, 0]), S.bits(vb[b, :, 0]), 0) for b in range(ns)]
             times.append(time.perf_counter() - t0)
         for b in range(ns):

@@ -96,7 +96,12 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * for a quantized head and otherwise the index of the head's first KX/VX
  * record in kxc/vxc (tri_pack_exact layout, n_kx records of 16 KiB each); such
  * a head keeps every prompt tile (count = tiles, entry[e] = e) and attends
- * exactly over its bf16 prompt and tail. */
+ * exactly over its bf16 prompt and tail.
+ * Split partition (extension): bounds NULL splits every head's kept tiles into
+ * runs of `per` (the reference's split); otherwise bounds is int32
+ * [batch][hk][nsplit + 1] and split s of a head covers entries
+ * [bounds[s], bounds[s + 1]) (nondecreasing, bounds[0] = 0, bounds[nsplit] =
+ * count, at most 64 entries per split), pm/pl/po then hold splits = nsplit. */
 int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -105,7 +110,8 @@ int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const
                void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
                const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
-               const void* vxc, int64_t n_kx, double scale, void* stream);
+               const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
+               void* stream);
 
 /* The two launches of tri_decode separately, same arguments: the split-KV
  * kernel (writes pm/pl/po) and the merge with the bf16 tail (writes out and
@@ -120,7 +126,7 @@ int tri_decode_partials(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                         int64_t o_sh, float* pm, float* pl, float* po, const int32_t* prompt, int batch, int hq,
                         int hk, int maxn, int per, int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8,
                         int64_t n_v4, const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
-                        double scale, void* stream);
+                        const int32_t* bounds, int nsplit, double scale, void* stream);
 int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                      const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                      const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -129,7 +135,8 @@ int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c,
                      const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                      float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                      int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
-                     const void* vxc, int64_t n_kx, double scale, void* stream);
+                     const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
+                     void* stream);
 
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */

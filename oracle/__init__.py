@@ -64,7 +64,7 @@ def lib():
         L.ora_decode_state.argtypes = [I, I, I, I]
         L.ora_decode_vfmt.restype = I
         L.ora_decode_vfmt.argtypes = [I, I]
-        L.ora_decode.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P]
+        L.ora_decode.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I, P]
         L.ora_num_threads.restype = I
         _lib = L
     return _lib
@@ -244,12 +244,19 @@ def decode_state(w8, w4, tiles, j):
     return lib().ora_decode_state(int(w8), int(w4), int(tiles), int(j))
 
 
-def decode(codes, bands, q_bits, prompt: int, per: int, scale: float, ktail, vtail, kcur, vcur, step: int):
+def decode(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vtail, kcur, vcur, step: int):
     """fp32 output [Hq, 128] of one decode step of one sequence.
 
     ``codes`` holds the prompt's prefill operands (k8/ka/k4/ka4/v8/v4/kstat/vstat);
     q_bits [Hq,128], ktail/vtail [Hk,max_tail,128], kcur/vcur [Hk,128] are uint16 bf16 bits.
+    ``per`` is the uniform split size (common_host.cuh:55), or an int [Hk, splits+1] array of
+    per-head split bounds (the product's balanced partition, an extension).
     """
+    if np.ndim(per) == 0:
+        bounds, nsplit, per = None, 0, int(per)
+    else:
+        bounds = _c(per, np.int32)
+        nsplit, per = bounds.shape[1] - 1, 1
     hq = q_bits.shape[0]
     hk = codes["kstat"].shape[0]
     b = _c(bands, np.int32).reshape(hq, 2)
@@ -262,7 +269,8 @@ def decode(codes, bands, q_bits, prompt: int, per: int, scale: float, ktail, vta
     lib().ora_decode(hq, hk, int(prompt), _p(b), int(per), sm_log2(scale), _p(_c(q_bits, np.uint16)),
                      _p(codes["k8"]), _p(codes["ka"]), _p(codes["k4"]), _p(codes["ka4"]), _p(v8), _p(v4),
                      _p(codes["vstat"]), _p(codes["kstat"]), _p(ktail), _p(vtail), int(ktail.shape[1]),
-                     _p(_c(kcur, np.uint16)), _p(_c(vcur, np.uint16)), int(step), _p(out))
+                     _p(_c(kcur, np.uint16)), _p(_c(vcur, np.uint16)), int(step),
+                     None if bounds is None else _p(bounds), int(nsplit), _p(out))
     return out
 
 

@@ -494,6 +494,8 @@ static float tail_score(const uint16_t* qv, const uint16_t* kv, const float* kme
 
 typedef struct {
   int hq, hk, prompt, per, max_tail;
+  const int32_t* bounds; /* NULL: uniform split of `per`; else [hk][nsplit + 1] entry bounds */
+  int nsplit;
   const int32_t* bands;
   float sm_log2;
   const uint16_t* q;
@@ -538,7 +540,7 @@ static void decode_head(const decode_args* a, int qh, float* out_row) {
     }
     if (c2 > maxn) maxn = c2;
   }
-  const int splits = (maxn + a->per - 1) / a->per > 1 ? (maxn + a->per - 1) / a->per : 1;
+  const int splits = a->bounds ? a->nsplit : (maxn + a->per - 1) / a->per > 1 ? (maxn + a->per - 1) / a->per : 1;
 
   /* in-kernel Q quantization (common_device.cuh:291-315) */
   float y[D];
@@ -560,7 +562,15 @@ static void decode_head(const decode_args* a, int qh, float* out_row) {
   float* pl = (float*)malloc(sizeof(float) * splits);
   float* po = (float*)malloc(sizeof(float) * splits * D);
   for (int s = 0; s < splits; ++s) {
-    const int first = s * a->per, last = count < first + a->per ? count : first + a->per;
+    int first = s * a->per, last = count < first + a->per ? count : first + a->per;
+    if (a->bounds) {
+      /* the caller's partition, clamped as the kernel clamps it: into [0, count), at most 64 per split */
+      const int32_t* bd = a->bounds + (int64_t)kh * (a->nsplit + 1) + s;
+      first = bd[0] < 0 ? 0 : bd[0] > count ? count : bd[0];
+      last = bd[1] < first ? first : bd[1];
+      if (last > count) last = count;
+      if (last > first + 64) last = first + 64;
+    }
     float m = -FLT_MAX, dw[4] = {0.f, 0.f, 0.f, 0.f}, out[D];
     for (int c = 0; c < D; ++c) out[c] = 0.f;
     for (int e = first; e < last; ++e) {
@@ -679,9 +689,9 @@ void ora_decode(int hq, int hk, int prompt, const int32_t* bands, int per, float
                 const int8_t* k8, const float* ka, const int8_t* k4, const float* ka4, const int8_t* v8,
                 const int8_t* v4, const float* vstat, const float* kstat, const uint16_t* ktail,
                 const uint16_t* vtail, int max_tail, const uint16_t* kcur, const uint16_t* vcur, int64_t step,
-                float* out) {
-  decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, bands, sm_log2, q, k8, k4, v8, v4,
-                   ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
+                const int32_t* bounds, int nsplit, float* out) {
+  decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, bounds, nsplit < 1 ? 1 : nsplit, bands, sm_log2,
+                   q, k8, k4, v8, v4, ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
   for (int qh = 0; qh < hq; ++qh) decode_head(&a, qh, out + (int64_t)qh * D);
 }
 

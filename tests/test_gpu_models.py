@@ -77,7 +77,7 @@ def test_generate_through_the_kernels_matches_the_oracle(module):
         _, q0, k0, v0, _, scale = pre[layer]
         b = np.asarray(bands[str(layer)], np.int32)
         codes = O.prefill_codes(bits(q0[0]), bits(k0[0]), bits(v0[0]), b, decode_cache=True)
-        per = tri.decode_cache.inner.layers[layer]["per"]
+        split = tri.decode_cache.inner.split_of(layer, 0)
         exact_kv = bf16.get(str(layer), [])
         exact_q = [h for h in range(4) if h // 2 in exact_kv]
         quant_q = [h for h in range(4) if h // 2 not in exact_kv]
@@ -85,7 +85,7 @@ def test_generate_through_the_kernels_matches_the_oracle(module):
         vtail = np.zeros_like(ktail)
         keys, values = k0[0].float(), v0[0].float()
         for step, (_, q, k, v, out, _) in enumerate(c for c in dec if c[0] == layer):
-            ref = O.decode(codes, b, bits(q[0, :, 0]), prompt, per, scale, ktail, vtail, bits(k[0, :, 0]),
+            ref = O.decode(codes, b, bits(q[0, :, 0]), prompt, split, scale, ktail, vtail, bits(k[0, :, 0]),
                            bits(v[0, :, 0]), step)
             assert_close_bf16(out[0, quant_q, 0].numpy(), ref[quant_q], what=f"decode layer {layer} step {step}")
             keys, values = torch.cat([keys, k[0].float()], 1), torch.cat([values, v[0].float()], 1)

@@ -88,19 +88,19 @@ def test_bf16_output_within_one_ulp(module):
     assert bool((torch.abs(out16 - r) <= ulp + 1e-30).all())
 
 
-def _decode_case(module, prompt, bands, batch=1, steps=3, max_tail=8, seed=5000, hq=6, hk=2):
-    print(f"\n[parity] decode prompt={prompt} batch={batch} steps={steps}", flush=True)
+def _decode_case(module, prompt, bands, batch=1, steps=3, max_tail=8, seed=5000, hq=6, hk=2, per=None):
+    print(f"\n[parity] decode prompt={prompt} batch={batch} steps={steps} per={per}", flush=True)
     q, k, v = small(seed, batch, hq, hk, prompt)
     scale = 128 ** -0.5
     cache = DecodeCache(module, max_tail=max_tail)
     cache.out_dtype = torch.float32
+    cache.per = per
     _, ops, pre = run_prefill(module, q, k, v, bands, scale, decode_cache=cache)
     ref_codes = [O.prefill_codes(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), decode_cache=True)
                  for b in range(batch)]
     kept = next(iter(pre.layer_buffers.values()))
     for b in range(batch):
         compare_codes(ops, ref_codes[b], b, batch, hq, hk, prompt, kept=kept)
-    per = cache.layers[0]["per"]
     g = S.gen(seed + 1)
     ktail = np.zeros((batch, hk, max_tail, 128), np.uint16)
     vtail = np.zeros_like(ktail)
@@ -109,8 +109,8 @@ def _decode_case(module, prompt, bands, batch=1, steps=3, max_tail=8, seed=5000,
         qd, kd, vd = S.outlier_tensor(g, batch, hq, 1), S.outlier_tensor(g, batch, hk, 1), S.outlier_tensor(g, batch, hk, 1)
         out = cache(0, qd.to(dev), kd.to(dev), vd.to(dev), scale).float().cpu().numpy()
         for b in range(batch):
-            ref = O.decode(ref_codes[b], bands.numpy(), bits(qd[b, :, 0]), prompt, per, scale, ktail[b], vtail[b],
-                           bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
+            ref = O.decode(ref_codes[b], bands.numpy(), bits(qd[b, :, 0]), prompt, cache.split_of(0, b), scale,
+                           ktail[b], vtail[b], bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
             assert_close(out[b, :, 0], ref, what=f"decode step {step} seq {b}")
             prior = min(step, max_tail - 1)
             ktail[b, :, prior] = bits(kd[b, :, 0])
@@ -126,6 +126,13 @@ def test_decode_mixed(module):
 def test_decode_bands_and_tail_overflow(module):
     bands = torch.tensor([[2, 4], [1, INF], [INF, INF], [3, 6], [1, 1], [2, 2]], dtype=torch.int32)
     _decode_case(module, 1500, bands, batch=2, steps=5, max_tail=3, seed=5100)
+
+
+@pytest.mark.parametrize("per", [1, 3, 64])
+def test_decode_uniform_split(module, per):
+    """The reference's split (runs of `per` tiles, no partition) through the same kernel."""
+    bands = torch.tensor([[2, 4], [1, INF], [INF, INF], [3, 6], [1, 1], [2, 2]], dtype=torch.int32)
+    _decode_case(module, 1500, bands, batch=2, steps=2, max_tail=3, seed=5150, per=per)
 
 
 def test_decode_short_prompt(module):
@@ -166,7 +173,6 @@ def test_ragged_decode_batch(module):
         codes.append(O.prefill_codes(bits(q[0]), bits(k[0]), bits(v[0]), bands.numpy(), decode_cache=True))
     e = cache.layers[0]
     assert e["batch"] == len(prompts)
-    per = e["per"]
     g = S.gen(8100)
     ktail = np.zeros((len(prompts), hk, max_tail, 128), np.uint16)
     vtail = np.zeros_like(ktail)
@@ -176,8 +182,8 @@ def test_ragged_decode_batch(module):
                       S.outlier_tensor(g, len(prompts), hk, 1))
         out = cache(0, qd.to(dev), kd.to(dev), vd.to(dev), scale).float().cpu().numpy()
         for b, n in enumerate(prompts):
-            ref = O.decode(codes[b], bands.numpy(), bits(qd[b, :, 0]), n, per, scale, ktail[b], vtail[b],
-                           bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
+            ref = O.decode(codes[b], bands.numpy(), bits(qd[b, :, 0]), n, cache.split_of(0, b), scale, ktail[b],
+                           vtail[b], bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
             assert_close(out[b, :, 0], ref, what=f"ragged step {step} seq {b} (prompt {n})")
             ktail[b, :, step] = bits(kd[b, :, 0])
             vtail[b, :, step] = bits(vd[b, :, 0])
@@ -241,7 +247,6 @@ def test_decode_with_exact_heads(module, prompt, bf16_kv, batch):
     run_prefill(module, q, k, v, bands, scale, decode_cache=cache, bf16_kv=bf16_kv)
     ref_codes = [O.prefill_codes(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), decode_cache=True)
                  for b in range(batch)]
-    per = cache.layers[0]["per"]
     g = S.gen(7100 + prompt)
     ktail = np.zeros((batch, hk, max_tail, 128), np.uint16)
     vtail = np.zeros_like(ktail)
@@ -255,8 +260,8 @@ def test_decode_with_exact_heads(module, prompt, bf16_kv, batch):
         keys, values = torch.cat([keys, kd], 2), torch.cat([values, vd], 2)
         for b in range(batch):
             if quant_q:
-                ref = O.decode(ref_codes[b], bands.numpy(), bits(qd[b, :, 0]), prompt, per, scale, ktail[b],
-                               vtail[b], bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
+                ref = O.decode(ref_codes[b], bands.numpy(), bits(qd[b, :, 0]), prompt, cache.split_of(0, b), scale,
+                               ktail[b], vtail[b], bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
                 assert_close(out[b, quant_q, 0], ref[quant_q], what=f"quantized heads step {step} seq {b}")
             r64, r32 = _attend64(qd[b, :, 0], keys[b], values[b], scale)
             bar = max(2e-3, float(np.abs(r32[exact_q] - r64[exact_q]).max()))

@@ -90,6 +90,38 @@ class FakeModule:
         return 2
 
 
+def test_balanced_partition_is_a_valid_cost_balanced_split():
+    """Bounds start at 0, end at the count, never decrease, hold at most 64 entries per split, fit the
+    slot budget, and cut C1-like heads (INT8 or INT4 K, INT8 V on the sink and last 16 tiles) into
+    splits within 10% of the mean cost at two workgroups per SIMD."""
+    from triattention_amd.kernels.decode import balanced_partition, entry_costs
+    rng = np.random.default_rng(3)
+    cache = DecodeCache(None)
+    hk = 8
+    for tiles, slots, batch in ((64, 2048, 32), (64, 1024, 32), (7, 64, 3), (512, 300, 2), (1, 16, 1)):
+        w8 = rng.choice([1, 2, INF], size=3 * hk)
+        bands = torch.tensor([[int(a), INF] for a in w8], dtype=torch.int32)
+        meta = sequence_metadata(bands, tiles, hk, cache.codes(tiles)[0])
+        (b,), splits = balanced_partition([meta], [batch], slots)
+        assert b.shape == (hk, splits + 1) and b.dtype == torch.int32
+        assert (b[:, 0] == 0).all() and (b[:, -1] == meta["count"]).all()
+        sizes = b.diff(dim=1)
+        assert (sizes >= 0).all() and (sizes <= 64).all()
+        n = (sizes > 0).sum(1)
+        floor = int(torch.clamp((meta["count"] + 63) // 64, min=1).sum())
+        assert batch * int(n.sum()) <= max(slots, batch * floor)
+        if tiles == 64 and slots == 2048:
+            c = entry_costs(meta)
+            cum = torch.cat([torch.zeros(hk, 1, dtype=torch.float64), c.cumsum(1)], 1)
+            part = (cum.gather(1, b[:, 1:].long()) - cum.gather(1, b[:, :-1].long()))[sizes > 0]
+            assert float(part.max()) <= 1.1 * float(part.mean())
+    # a head far costlier than the rest still gets runs of at most 64 entries
+    meta = sequence_metadata(torch.tensor([[INF, INF]] * 4, dtype=torch.int32), 300, 2,
+                             cache.codes(300)[0], exact_kv=[1])
+    (b,), _ = balanced_partition([meta], [1], 4)
+    assert (b.diff(dim=1) <= 64).all() and (b[:, -1] == meta["count"]).all()
+
+
 def test_ragged_cache_assembly_slots_are_consistent():
     cache = DecodeCache(FakeModule(), max_tail=8)
     cache.ragged = True
@@ -124,6 +156,36 @@ def test_ragged_cache_assembly_slots_are_consistent():
                     vsrc, vdst = (v8, e["v"][I8]) if int(e["fmt"][row, j]) == 1 else (v4, e["v"][I4])
                     assert torch.equal(vdst[int(e["slot"][row, kh, n])], vsrc[s, kh, j])
             row += 1
+
+
+def test_split_rule_balances_one_wave_and_runs_uniform_above():
+    """Up to BALANCE_TILES kept tiles per slot the cache holds a balanced partition (bounds cover every
+    kept entry); above it, uniform runs of `per` tiles and no bounds; cache.per forces the uniform
+    split."""
+    from triattention_amd.kernels.decode import BALANCE_TILES
+    hk, bands = 2, torch.tensor([[INF, INF], [1, INF], [2, 4], [1, 1]], dtype=torch.int32)
+    prompt, batch = 3000, 2
+    tiles = (prompt + 63) // 64
+    z32 = lambda n: torch.zeros(n, dtype=torch.int32).to(torch.uint32)
+    for wave, per, balanced in ((1024, None, True), (2, None, False), (1024, 5, False)):
+        cache = DecodeCache(FakeModule(), max_tail=8)
+        cache.wave, cache.per = wave, per
+        codes, _ = cache.codes(tiles)
+        packed = {F16: None, I8: z32(batch * hk * tiles * 2048), I4: z32(batch * hk * tiles * 1024)}
+        stat = torch.zeros(batch, hk, 3, 128)
+        cache.store(0, prompt, z32(batch * hk * tiles * 2048), torch.ones(batch * hk * tiles * 4), stat.clone(),
+                    stat.clone(), packed, codes, bands, z32(batch * hk * tiles * 1024), torch.ones(batch * hk * tiles * 4))
+        e = cache.layers[0]
+        kept = int(e["count"].sum())
+        assert (kept <= BALANCE_TILES * wave and per is None) == balanced
+        if balanced:
+            b = e["bounds_host"]
+            assert b.shape == (batch, hk, e["splits"] + 1)
+            assert (b[:, :, 0] == 0).all() and (b[:, :, -1] == e["count"].numpy()).all()
+            assert np.array_equal(cache.split_of(0, 1), b[1])
+        else:
+            assert e["bounds"] is None and e["splits"] == -(-e["maxn"] // e["per"])
+            assert cache.split_of(0, 0) == e["per"] and (per is None or e["per"] == per)
 
 
 def test_exact_heads_in_a_ragged_cache():

@@ -298,6 +298,27 @@ def test_decode_split_invariance():
     assert np.abs(outs[0] - outs[2]).max() < 1e-4 and np.abs(outs[1] - outs[2]).max() < 1e-4
 
 
+def test_decode_bounds_reproduce_the_uniform_split():
+    """Bounds [0, per, 2 per, ..., count] per head give the uniform split's bits; a different partition
+    moves the output only by the partials' rounding."""
+    bands = np.array([[INF, INF], [1, INF], [2, 5], [1, 1]], np.int32)
+    prompt = 900
+    codes, qd, kd, vd = _decode_setup(52, prompt, bands)
+    z = np.zeros((2, 4, 128), np.uint16)
+    run = lambda split: O.decode(codes, bands, bits(qd), prompt, split, 128 ** -0.5, z, z, bits(kd), bits(vd), 0)
+    tiles = (prompt + 63) // 64
+    count = [sum(max(O.decode_state(*bands[2 * h + r], tiles, j) for r in range(2)) > 0 for j in range(tiles))
+             for h in range(2)]
+    maxn = max(count)
+    for per in (1, 3, 5, 64):
+        splits = -(-maxn // per)
+        bounds = np.array([[min(c, s * per) for s in range(splits + 1)] for c in count], np.int32)
+        assert np.array_equal(run(bounds).view(np.uint32), run(per).view(np.uint32)), per
+    # uneven runs, an empty split and the tail-heavy last split
+    odd = np.array([[0, 2, 2, 9, count[0], count[0]], [0, 1, 7, 8, 10, count[1]]], np.int32)
+    assert np.abs(run(odd) - run(100)).max() < 1e-4
+
+
 def test_decode_close_to_dequantized_float64():
     """Decode keeps the tiles of each head's band, INT8/INT4 K by group maximum,
     INT8/INT4 V by recency, and the exact bf16 current token."""

@@ -196,13 +196,15 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                        float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
-                       const void* kxc, const void* vxc, int64_t n_kx, double scale, void* stream, int phase) {
+                       const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
+                       void* stream, int phase) {
   g_error.clear();
   if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
       !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
     return fail("decode: null buffer");
-  if (batch < 1 || hq < 1 || hk < 1 || maxn < 1 || per < 1 || tiles_max < 1) return fail("decode: empty shape");
-  if (per > tri::MAX_PER) return fail("decode: per (tiles per split) must be at most 64");
+  if (batch < 1 || hq < 1 || hk < 1 || maxn < 1 || tiles_max < 1) return fail("decode: empty shape");
+  if (!bounds && (per < 1 || per > tri::MAX_PER)) return fail("decode: per (tiles per split) must be in [1, 64]");
+  if (bounds && (nsplit < 1 || nsplit > 65535)) return fail("decode: nsplit must be in [1, 65535] with a partition");
   if (hq % hk != 0 || hq / hk > tri::MAX_GROUP) return fail("decode: GQA group must divide and be <= 8");
   if (max_tail < 1 || max_tail > tri::MAX_TAIL) return fail("decode: max_tail must be in [1, 1024]");
   if ((k4c == nullptr) != (ka4 == nullptr)) return fail("decode: INT4 K records and scales (all or none)");
@@ -213,7 +215,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   if (!aligned(ktail, 16) || !aligned(vtail, 16) || (t_sb % 8) || (t_sh % 8) || (t_st % 8))
     return fail("decode: tail buffers must be 16-byte aligned rows");
   if (!aligned(po, 16)) return fail("decode: po must be 16-byte aligned");
-  const int splits = std::max(1, (maxn + per - 1) / per);
+  const int splits = bounds ? nsplit : std::max(1, (maxn + per - 1) / per);
   const int64_t lim = (int64_t)1 << 31;
   if (n_k8 < 1 || n_v8 < 1 || n_v4 < 1 || n_k8 * tri::K8_BYTES >= lim || n_k4 * tri::K4_BYTES >= lim ||
       n_v8 * tri::V8_BYTES >= lim || n_v4 * tri::V4_BYTES >= lim || (k4c != nullptr && n_k4 < 1))
@@ -250,6 +252,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   d.hk = hk;
   d.maxn = maxn;
   d.per = per;
+  d.bounds = bounds;
   d.tiles_max = tiles_max;
   d.splits = splits;
   {
@@ -326,7 +329,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
 #define TRI_DECODE_ARGS                                                                                      \
   q, q_sb, q_sh, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8c, v4c, vstat, kstat, ktail, vtail, t_sb, t_sh, \
       t_st, max_tail, kcur, vcur, c_sb, c_sh, step, out, out_dtype, o_sb, o_sh, pm, pl, po, prompt, batch, hq, hk,  \
-      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, xslot, kxc, vxc, n_kx, scale, stream
+      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, xslot, kxc, vxc, n_kx, bounds, nsplit, scale, stream
 #define TRI_DECODE_PARAMS                                                                                          \
   const void *q, int64_t q_sb, int64_t q_sh, const void *k8c, const void *k4c, const float *ka, const float *ka4,  \
       const int32_t *entry, const int32_t *kinfo, const int32_t *count, const int32_t *fmt, const int32_t *slot,  \
@@ -335,7 +338,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
       int64_t c_sh, const int64_t *step, void *out, int out_dtype, int64_t o_sb, int64_t o_sh, float *pm,          \
       float *pl, float *po, const int32_t *prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,    \
       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t *xslot, const void *kxc,           \
-      const void *vxc, int64_t n_kx, double scale, void *stream
+      const void *vxc, int64_t n_kx, const int32_t *bounds, int nsplit, double scale, void *stream
 
 int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
 int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }

@@ -46,10 +46,29 @@ struct DecodeArgs {
   const float* vstat;   // [B][Hk][3][128]: V mean, scale, 1/scale
   int kx_bytes;
   int scatter;          // prime coprime to the grid size: workgroup lin takes work item lin * scatter mod grid
+  // split partition (extension): null for the reference's uniform split of `per` tiles, else
+  // [B][Hk][splits + 1] entry bounds, split s of a head covering entries [bounds[s], bounds[s + 1])
+  const int32_t* bounds;
 };
 
 constexpr int MAX_TAIL = 1024;
 constexpr int MAX_PER = 64;  // kept tiles per split: one per lane of the wave's metadata
+
+// Entries [first, last) of split `split` of head hb: the uniform split of a.per
+// tiles, or the caller's partition clamped into [0, count) and to MAX_PER
+// entries (a partition outside that contract loses tiles, never reads out of
+// bounds).
+__device__ __forceinline__ void split_range(const DecodeArgs& a, int64_t hb, int split, int& first, int& last) {
+  const int cnt = a.count[hb];
+  if (a.bounds) {
+    const int32_t* bd = a.bounds + hb * (a.splits + 1) + split;
+    first = min(max(bd[0], 0), cnt);
+    last = min(max(bd[1], first), min(cnt, first + MAX_PER));
+  } else {
+    first = split * a.per;
+    last = min(cnt, first + a.per);
+  }
+}
 
 __device__ __forceinline__ v4i unpack16(v4i w) {
   return v4i{(int)nib_lo16((uint32_t)w[0]), (int)nib_hi16((uint32_t)w[0]), (int)nib_lo16((uint32_t)w[1]),
@@ -68,7 +87,8 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
   const int L = threadIdx.x, lq = L & 31, half = L >> 5;
   const int g = a.hq / a.hk, prompt = a.prompt[b];
   const int64_t hb = (int64_t)b * a.hk + kh;
-  const int cnt = a.count[hb], first = split * a.per, last = min(cnt, first + a.per);
+  int first, last;
+  split_range(a, hb, split, first, last);
   const int x0 = a.xslot[hb];
   float cq = 0.f;
   const float* kmean = a.kstat + hb * 3 * D;
@@ -203,7 +223,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   }
   // A split past its head's kept tiles (ragged batches: most splits of the short sequences)
   // writes the empty partial (m = -FLT_MAX, l = 0, o = 0) and leaves.
-  if (split * a.per >= a.count[(int64_t)b * a.hk + kh]) {
+  int first, last;
+  split_range(a, (int64_t)b * a.hk + kh, split, first, last);
+  if (first >= last) {
     const int L = threadIdx.x, g = a.hq / a.hk;
     for (int r = 0; r < g; ++r) {
       const int64_t idx = ((int64_t)b * a.hq + kh * g + r) * a.splits + split;
@@ -225,7 +247,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   const int g = a.hq / a.hk;
   const int prompt = a.prompt[b];
   const int64_t hb = (int64_t)b * a.hk + kh;
-  const int cnt = a.count[hb], first = split * a.per, last = min(cnt, first + a.per);
 
   // The g query rows are loaded first, one row per 8 lanes, 16 channels per
   // lane (the padding rows load row g - 1, so every lane issues the same
@@ -268,32 +289,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   // use of one waits for every outstanding scalar and LDS access; per-tile
   // scalar loads would stall every tile on the metadata of the tiles after it.
   constexpr int OUT_OF_RANGE = (int)0x80000000u;  // >= any record array size (< 2 GiB)
-  // Entry first + L of the split (clamped into the entry table, so every lane
-  // loads; the tile index is clamped too, as entries past the count are not
-  // tiles); lanes past the split's end get the out-of-range offsets.
-  int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);  // koff, voff, info | v8 << 9 | j << 10
-  float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
-  {
-    const bool valid = L < last - first;
-    // (independent of the split's entry count, so these loads need not wait for it)
-    const int64_t li = mbase + min(first + min(L, a.per - 1), a.maxn - 1);
-    const int info = a.kinfo[li], j = min(max(a.entry[li], 0), a.tiles_max - 1), vs = a.slot[li];
-    const int is4 = valid ? (info >> 8) & 1 : 0;
-    const int vf = a.fmt[(int64_t)b * a.tiles_max + j];
-    const float4 kl = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
-    if (valid) {
-      ka = kl;
-      w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
-      w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
-      w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
-    }
-    meta[L] = w;
-    metk[L] = ka;
-    if (L == 0) {
-      meta[MAX_PER] = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);
-      metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
-    }
-  }
   struct Meta {
     int info, j, vf, koff, voff;
   };
@@ -338,9 +333,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
     return (f & 1) ? unpack16(v4i{p[2], p[3], 0, 0}) : unpack16(p);
   };
 
-  // the first tile's records stream while Q is quantized (lane 0 holds its entry)
+
+  // Entry first + L of the split (clamped into the entry table, so every lane
+  // loads; the tile index is clamped too, as entries past the count are not
+  // tiles); lanes past the split's end get the out-of-range offsets.
+  int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);  // koff, voff, info | v8 << 9 | j << 10
+  float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
+  {
+    const bool valid = L < last - first;
+    // (independent of the split's entry count, so these loads need not wait for it)
+    const int64_t li = mbase + min(first + min(L, last - first - 1), a.maxn - 1);
+    const int info = a.kinfo[li], jr = a.entry[li], vs = a.slot[li];
+    // (keep the entry and slot loads ahead of the K loads: the tile-index loads below wait for
+    // the entry, and waits count loads in issue order)
+    __builtin_amdgcn_sched_barrier(0);
+    const int is4 = valid ? (info >> 8) & 1 : 0;
+    if (valid) w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
+    {
+      // the first tile's K streams as soon as its kinfo is in (lane 0 holds the entry), one
+      // memory round trip before its V, whose format and slot need the tile index first
+      Meta m0;
+      m0.koff = __builtin_amdgcn_readfirstlane(w.x);
+      m0.info = __builtin_amdgcn_readfirstlane(info & 0x1ff);
+      load_k(m0);
+    }
+    const int j = min(max(jr, 0), a.tiles_max - 1);
+    const int vf = a.fmt[(int64_t)b * a.tiles_max + j];
+    const float4 kl = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
+    if (valid) {
+      ka = kl;
+      w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
+      w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
+    }
+    meta[L] = w;
+    metk[L] = ka;
+    if (L == 0) {
+      meta[MAX_PER] = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);
+      metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+  }
+  // its V streams while Q is quantized
   Meta mc = unpack(w);
-  load_k(mc);
   load_v(mc);
 
   // ---- in-kernel Q quantization of the g rows (common_device.cuh:291-315)

@@ -30,7 +30,9 @@ WORDS = {I8: 2048, I4: 1024}
 K8_WORDS, K4_WORDS = 2048, 1024
 KX_BYTES = 16384
 NEAR_V8 = 16
-SPLITS_PER_CU = 4  # decode workgroups per CU that the split size targets
+SPLITS_PER_CU = 4  # decode workgroups per CU that the split partition targets
+TILE_COST = 4096   # per-tile cost of the split kernel beyond its record bytes (instruction stream), in bytes
+BALANCE_TILES = 16  # kept tiles per slot up to which the split partition is balanced by cost
 
 
 def tile_states(bands: torch.Tensor, tiles: int) -> torch.Tensor:
@@ -78,6 +80,60 @@ def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor, exact_kv
                 kbase=kbase, vslot=vslot, vcode=vcode, vsel=vsel, exact=exact)
 
 
+def entry_costs(meta) -> torch.Tensor:
+    """Cost of each kept entry of one sequence [Hk, maxn] (float64, 0 past the count): the bytes of
+    its K and V records plus TILE_COST."""
+    exact = meta["exact"][:, None]
+    kb = torch.where(exact, KX_BYTES, torch.where(meta["is4"], 4096, 8192))
+    vb = torch.where(exact, KX_BYTES, torch.where(meta["vcode"] == I8, 8192, 4096))
+    return torch.where(meta["valid"], kb + vb + TILE_COST, 0).to(torch.float64)
+
+
+def split_bounds(costs: torch.Tensor, valid: torch.Tensor, n: torch.Tensor) -> torch.Tensor:
+    """Entry bounds [Hk, max(n) + 1] cutting head h's kept entries into n[h] runs of near-equal cost:
+    entry e joins the run that holds the midpoint of its cost interval.  Bounds past n[h] equal the
+    count, so those splits are empty."""
+    cum = costs.cumsum(1)
+    mid = cum - costs / 2
+    s = torch.arange(int(n.max()) + 1, dtype=torch.float64)[None, :]
+    nf = n.to(torch.float64)[:, None]
+    thr = cum[:, -1:] * torch.minimum(s, nf) / nf
+    return ((mid[:, None, :] < thr[:, :, None]) & valid[:, None, :]).sum(-1)
+
+
+def balanced_partition(metas, batches, slots: int):
+    """Per-sequence split bounds [Hk, splits + 1] for each metadata in ``metas`` (one per group of
+    sequences of equal length, ``batches`` sequences each), and the common split count.
+
+    Extension (the reference splits every head into runs of one tile count, decode.py:54-55): the
+    split kernel streams each split's records at about the same rate per wave, so its time is set
+    by the largest split.  Heads are cut by cost (record bytes, TILE_COST per tile) into
+    n_h = ceil(cost_h / t) runs of near-equal cost, with the smallest target t whose split count
+    fits ``slots`` resident workgroups, at most 64 entries per split."""
+    costs = [entry_costs(m) for m in metas]
+    head = [c.sum(1) for c in costs]
+    floor = [torch.clamp((m["count"] + 63) // 64, min=1) for m in metas]
+    items = lambda t: sum(b * int(torch.maximum(torch.ceil(h / t), f).sum()) for b, h, f in zip(batches, head, floor))
+    lo, hi = max(float(c.max()) for c in costs), max(float(h.max()) for h in head) + 1.0
+    if items(hi) <= slots:
+        for _ in range(60):
+            mid = (lo + hi) / 2
+            lo, hi = (lo, mid) if items(mid) <= slots else (mid, hi)
+    out = []
+    for m, c, h, f in zip(metas, costs, head, floor):
+        n = torch.maximum(torch.ceil(h / hi).to(torch.int64), f)
+        while True:
+            b = split_bounds(c, m["valid"], n)
+            over = (b.diff(dim=1) > 64).any(1)
+            if not bool(over.any()):
+                break
+            n = n + over.to(torch.int64)
+        out.append(b)
+    splits = max(b.shape[1] - 1 for b in out)
+    pad = lambda b: torch.cat([b, b[:, -1:].expand(-1, splits + 1 - b.shape[1])], 1)
+    return [pad(b).to(torch.int32) for b in out], splits
+
+
 class DecodeCache:
     def __init__(self, module, max_tail=256):
         self.module, self.max_tail = module, max_tail
@@ -86,6 +142,8 @@ class DecodeCache:
         self.out_dtype = None
         self.meta_cache = {}
         self.wave = None
+        # None: the balanced split partition; an int: the reference's uniform split of `per` tiles
+        self.per = None
 
     def codes(self, rows):
         if rows not in self.formats:
@@ -210,19 +268,32 @@ class DecodeCache:
             cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
                 torch.cuda.get_device_properties(device).multi_processor_count
             self.wave = cus * max(1, min(self.module.decode_occupancy(), SPLITS_PER_CU))
-        # Split size, from the host copy of the counts (no device sync).  The reference spreads
-        # the kept tiles over one full wave of resident workgroups (decode.py:54-55); here over
-        # SPLITS_PER_CU workgroups per CU, and every average head gets at least 4 splits.  One
-        # wave per SIMD streams as many tiles per second as two (each wave is bound by its own
-        # per-tile instruction stream), so fewer, longer splits save prologues and partials
-        # (C1: 37 vs 41 us), while ragged batches need the splits to spread their long heads
-        # (C3: 133 us at 24 tiles per split, 157 us at 48).  At most 64 tiles per split.
+        # Split partition, from the host metadata (no device sync).
+        # - Up to BALANCE_TILES kept tiles per slot (one wave of SPLITS_PER_CU workgroups per CU;
+        #   C1: 16384 tiles on 1024 slots): every SIMD runs one split, so the kernel lasts as
+        #   long as its costliest split, and balanced_partition cuts the heads by cost (C1:
+        #   36.9 us vs 39.6 us for runs of 16 tiles).
+        # - Above that (C3: 48.8k tiles), runs of `per` tiles, as the reference splits
+        #   (decode.py:54-55), over one wave of slots with every average head in at least 4
+        #   splits: the dispatcher then balances the waves itself, and no partition tried did
+        #   better (C3: 134 us at 24 tiles per split; balanced over 2560-8192 slots 134-141 us).
+        # - self.per set: always runs of that many tiles.  At most 64 tiles per split.
         kept = sum(g["batch"] * int(g["meta"]["count"].sum()) for g in groups)
-        mean = kept / max(1, total * hk)
-        per = min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 4))))
+        if self.per is None and kept <= BALANCE_TILES * self.wave:
+            parts, splits = balanced_partition([g["meta"] for g in groups], [g["batch"] for g in groups], self.wave)
+            bounds_host = torch.cat([p[None].expand(g["batch"], -1, -1) for p, g in zip(parts, groups)])
+            per = int(bounds_host.diff(dim=2).max())
+            bounds = bounds_host.to(device)
+        else:
+            mean = kept / max(1, total * hk)
+            per = self.per or min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 4))))
+            bounds_host = bounds = None
+            splits = max(1, -(-maxn // per))
         to = lambda x: x.to(torch.int32).to(device)
         tail_k = torch.zeros((total, hk, self.max_tail, 128), dtype=torch.bfloat16, device=device)
-        return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, fmt=to(fmt), slot=to(slot), entry=to(entry),
+        return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, splits=splits, bounds=bounds,
+                    bounds_host=None if bounds_host is None else bounds_host.numpy(), fmt=to(fmt), slot=to(slot),
+                    entry=to(entry),
                     kinfo=to(kinfo), count=to(count), k8=cat(k8s, K8_WORDS), k4=cat(k4s, K4_WORDS) if has4 else None,
                     ka=ka, ka4=ka4, kstat=kstat, vstat=vstat, v={I8: cat(v8s, WORDS[I8]), I4: cat(v4s, WORDS[I4])},
                     tail_k=tail_k, tail_v=torch.zeros_like(tail_k), batch=total, tiles_max=tiles_max,
@@ -232,7 +303,7 @@ class DecodeCache:
     def __call__(self, layer, q, k, v, scale):
         e = self.layers[layer]
         hq = q.shape[1]
-        splits = max(1, -(-e["maxn"] // e["per"]))
+        splits = e["splits"]
         key = ("partials", hq)
         if key not in e:
             n = e["batch"] * hq * splits
@@ -252,8 +323,14 @@ class DecodeCache:
             e[key] = self.module.plan_decode(
                 q, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"], e["slot"],
                 e["v"][I8], e["v"][I4], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], k, k, self.step, out,
-                *e[("partials", hq)], e["prompt"], e["per"], scale, e["xslot"], e["kx"], e["vx"])
+                *e[("partials", hq)], e["prompt"], e["per"], scale, e["xslot"], e["kx"], e["vx"], e["bounds"])
         return e[key]
+
+    def split_of(self, layer, b):
+        """The split argument of the oracle's decode for sequence b of the layer: its bounds
+        [Hk, splits + 1], or the uniform `per`."""
+        e = self.layers[layer]
+        return e["per"] if e["bounds_host"] is None else e["bounds_host"][b]
 
     def advance(self):
         self.step.add_(1)

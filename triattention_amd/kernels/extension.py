@@ -62,7 +62,7 @@ def load_library() -> ctypes.CDLL:
     lib.tri_pack_exact.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I, P, I, P, P, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64,
-                   P, P, P, I64, D_, P]
+                   P, P, P, I64, P, I, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
         getattr(lib, name).argtypes = decode_args
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
@@ -201,20 +201,23 @@ class Module:
 
     # ------------------------------------------------------------------ decode
     def decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, kcur,
-               vcur, step, out, pm, pl, po, prompt, per, scale, phase=3, xslot=None, kxc=None, vxc=None):
+               vcur, step, out, pm, pl, po, prompt, per, scale, phase=3, xslot=None, kxc=None, vxc=None, bounds=None):
         """Single-token decode over the quantized cache plus the bf16 tail.
 
         ``phase`` (extension): 3 runs both kernels, 1 only the split-KV kernel,
         2 only the merge (for per-kernel timing).  ``xslot`` (extension, int32
         [B,Hk], -1 = quantized head) with the KX/VX record arrays ``kxc``/``vxc``
-        makes the listed KV heads attend exactly over their bf16 prompt."""
+        makes the listed KV heads attend exactly over their bf16 prompt.  ``bounds``
+        (extension, int32 [B,Hk,splits+1]) replaces the uniform split of ``per`` tiles
+        by the given partition of each head's kept tiles."""
         plan = self.plan_decode(q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail,
-                                vtail, kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot, kxc, vxc)
+                                vtail, kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot, kxc, vxc, bounds)
         plan.run(q, kcur, vcur, out, phase)
         return out
 
     def plan_decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail,
-                    kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot=None, kxc=None, vxc=None):
+                    kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot=None, kxc=None, vxc=None,
+                    bounds=None):
         """Validate and marshal every argument of ``decode`` once (extension).  The returned
         plan's ``run(q, kcur, vcur, out, phase)`` launches with new q / k / v / out tensors of the
         planned shapes and strides and the same cache, at a few microseconds of host time."""
@@ -230,7 +233,14 @@ class Module:
         else:
             prompt_t = torch.full((b,), int(prompt), dtype=torch.int32, device=q.device)
         tiles_max = fmt.numel() // b
-        splits = max(1, -(-maxn // int(per)))
+        if bounds is not None:
+            _check(bounds.dtype == torch.int32 and bounds.is_cuda and bounds.dim() == 3 and
+                   tuple(bounds.shape[:2]) == (b, hk) and bounds.size(2) >= 2 and bounds.is_contiguous(),
+                   "decode: bounds int32 [B,Hk,splits+1]")
+            splits = bounds.size(2) - 1
+        else:
+            _check(1 <= int(per) <= 64, "decode: per (tiles per split) must be in [1, 64]")
+            splits = max(1, -(-maxn // int(per)))
         if xslot is not None:
             _check(xslot.dtype == torch.int32 and xslot.is_cuda and xslot.numel() == b * hk and kxc is not None and
                    vxc is not None and kxc.numel() * kxc.element_size() % KX_BYTES == 0 and
@@ -255,9 +265,10 @@ class Module:
                 0, 0 if out.dtype == torch.float32 else 1, out.stride(0), out.stride(1), _ptr(pm),
                 _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, k8c.size(0),
                 0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), _ptr(xslot), _ptr(kxc),
-                _ptr(vxc), 0 if kxc is None else kxc.numel() * kxc.element_size() // KX_BYTES, float(scale), 0]
+                _ptr(vxc), 0 if kxc is None else kxc.numel() * kxc.element_size() // KX_BYTES, _ptr(bounds),
+                splits if bounds is not None else 0, float(scale), 0]
         keep = (k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, step, pm, pl,
-                po, prompt_t, xslot, kxc, vxc)
+                po, prompt_t, xslot, kxc, vxc, bounds)
         return DecodePlan(self, args, q, kcur, out, keep)
 
     def decode_occupancy(self) -> int:
@@ -281,7 +292,7 @@ def _geometry(t):
 class DecodePlan:
     """A validated, marshalled ``decode`` call; ``run`` swaps in the per-step tensors."""
 
-    Q, QSB, QSH, KC, VC, KSB, KSH, OUT, STREAM = 0, 1, 2, 22, 23, 24, 25, 27, 50
+    Q, QSB, QSH, KC, VC, KSB, KSH, OUT, STREAM = 0, 1, 2, 22, 23, 24, 25, 27, 52
 
     def __init__(self, module, args, q, kcur, out, keep):
         self.module, self.args, self.keep = module, args, keep

@@ -154,6 +154,41 @@ def test_decode_long_tail(module):
     _decode_case(module, 500, bands, batch=2, steps=20, max_tail=24, seed=5400)
 
 
+def test_decode_full_1024_token_tail(module):
+    """The largest tail the merge holds (max_tail 1024): steps 1021-1025 over a tail pre-filled with
+    random bf16 rows, the last three overwriting slot 1023 as the reference does."""
+    print("\n[parity] decode with a 1024-token tail (steps 1021-1025)", flush=True)
+    hq, hk, batch, prompt, max_tail = 8, 2, 2, 300, 1024
+    bands = torch.tensor([[INF, INF], [1, INF], [2, 5], [1, 1], [3, INF], [1, 2], [INF, INF], [2, 2]],
+                         dtype=torch.int32)
+    q, k, v = small(5600, batch, hq, hk, prompt)
+    scale = 128 ** -0.5
+    cache = DecodeCache(module, max_tail=max_tail)
+    cache.out_dtype = torch.float32
+    run_prefill(module, q, k, v, bands, scale, decode_cache=cache)
+    codes = [O.prefill_codes(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), decode_cache=True)
+             for b in range(batch)]
+    e = cache.layers[0]
+    g = S.gen(5601)
+    e["tail_k"].copy_(S.outlier_tensor(g, batch, hk, max_tail).to(e["tail_k"].device))
+    e["tail_v"].copy_(S.outlier_tensor(g, batch, hk, max_tail).to(e["tail_v"].device))
+    ktail, vtail = bits(e["tail_k"].cpu()).copy(), bits(e["tail_v"].cpu()).copy()
+    cache.step.fill_(1021)
+    dev = torch.device("cuda")
+    for step in range(1021, 1026):
+        qd, kd, vd = S.outlier_tensor(g, batch, hq, 1), S.outlier_tensor(g, batch, hk, 1), S.outlier_tensor(g, batch, hk, 1)
+        out = cache(0, qd.to(dev), kd.to(dev), vd.to(dev), scale).float().cpu().numpy()
+        prior = min(step, max_tail - 1)
+        for b in range(batch):
+            ref = O.decode(codes[b], bands.numpy(), bits(qd[b, :, 0]), prompt, cache.split_of(0, b), scale, ktail[b],
+                           vtail[b], bits(kd[b, :, 0]), bits(vd[b, :, 0]), step)
+            assert_close(out[b, :, 0], ref, what=f"step {step} seq {b}")
+            ktail[b, :, prior] = bits(kd[b, :, 0])
+            vtail[b, :, prior] = bits(vd[b, :, 0])
+        cache.advance()
+    assert np.array_equal(bits(e["tail_k"].cpu()), ktail) and np.array_equal(bits(e["tail_v"].cpu()), vtail)
+
+
 def test_ragged_decode_batch(module):
     """Ragged cache: four prompts of different lengths stored by separate Prefill calls, served by one
     decode launch per step; every sequence matches the oracle."""

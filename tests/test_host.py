@@ -111,7 +111,7 @@ def test_balanced_partition_is_a_valid_cost_balanced_split():
         floor = int(torch.clamp((meta["count"] + 63) // 64, min=1).sum())
         assert batch * int(n.sum()) <= max(slots, batch * floor)
         if tiles == 64 and slots == 2048:
-            c = entry_costs(meta)
+            c = torch.from_numpy(entry_costs(meta))
             cum = torch.cat([torch.zeros(hk, 1, dtype=torch.float64), c.cumsum(1)], 1)
             part = (cum.gather(1, b[:, 1:].long()) - cum.gather(1, b[:, :-1].long()))[sizes > 0]
             assert float(part.max()) <= 1.1 * float(part.mean())

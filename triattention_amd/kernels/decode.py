@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from .extension import _geometry
@@ -80,30 +81,30 @@ def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor, exact_kv
                 kbase=kbase, vslot=vslot, vcode=vcode, vsel=vsel, exact=exact)
 
 
-def entry_costs(meta) -> torch.Tensor:
+def entry_costs(meta) -> np.ndarray:
     """Cost of each kept entry of one sequence [Hk, maxn] (float64, 0 past the count): the bytes of
     its K and V records plus TILE_COST."""
-    exact = meta["exact"][:, None]
-    kb = torch.where(exact, KX_BYTES, torch.where(meta["is4"], 4096, 8192))
-    vb = torch.where(exact, KX_BYTES, torch.where(meta["vcode"] == I8, 8192, 4096))
-    return torch.where(meta["valid"], kb + vb + TILE_COST, 0).to(torch.float64)
+    exact = meta["exact"].numpy()[:, None]
+    kb = np.where(exact, KX_BYTES, np.where(meta["is4"].numpy(), 4096, 8192))
+    vb = np.where(exact, KX_BYTES, np.where(meta["vcode"].numpy() == I8, 8192, 4096))
+    return np.where(meta["valid"].numpy(), kb + vb + TILE_COST, 0).astype(np.float64)
 
 
-def split_bounds(costs: torch.Tensor, valid: torch.Tensor, n: torch.Tensor) -> torch.Tensor:
+def split_bounds(costs: np.ndarray, valid: np.ndarray, n: np.ndarray) -> np.ndarray:
     """Entry bounds [Hk, max(n) + 1] cutting head h's kept entries into n[h] runs of near-equal cost:
     entry e joins the run that holds the midpoint of its cost interval.  Bounds past n[h] equal the
     count, so those splits are empty."""
     cum = costs.cumsum(1)
     mid = cum - costs / 2
-    s = torch.arange(int(n.max()) + 1, dtype=torch.float64)[None, :]
-    nf = n.to(torch.float64)[:, None]
-    thr = cum[:, -1:] * torch.minimum(s, nf) / nf
+    s = np.arange(int(n.max()) + 1, dtype=np.float64)[None, :]
+    nf = n.astype(np.float64)[:, None]
+    thr = cum[:, -1:] * np.minimum(s, nf) / nf
     return ((mid[:, None, :] < thr[:, :, None]) & valid[:, None, :]).sum(-1)
 
 
 def balanced_partition(metas, batches, slots: int):
-    """Per-sequence split bounds [Hk, splits + 1] for each metadata in ``metas`` (one per group of
-    sequences of equal length, ``batches`` sequences each), and the common split count.
+    """Per-sequence split bounds [Hk, splits + 1] (int32 tensors) for each metadata in ``metas`` (one
+    per group of sequences of equal length, ``batches`` sequences each), and the common split count.
 
     Extension (the reference splits every head into runs of one tile count, decode.py:54-55): the
     split kernel streams each split's records at about the same rate per wave, so its time is set
@@ -111,27 +112,30 @@ def balanced_partition(metas, batches, slots: int):
     n_h = ceil(cost_h / t) runs of near-equal cost, with the smallest target t whose split count
     fits ``slots`` resident workgroups, at most 64 entries per split."""
     costs = [entry_costs(m) for m in metas]
-    head = [c.sum(1) for c in costs]
-    floor = [torch.clamp((m["count"] + 63) // 64, min=1) for m in metas]
-    items = lambda t: sum(b * int(torch.maximum(torch.ceil(h / t), f).sum()) for b, h, f in zip(batches, head, floor))
-    lo, hi = max(float(c.max()) for c in costs), max(float(h.max()) for h in head) + 1.0
+    heads = [c.sum(1) for c in costs]
+    floors = [np.maximum((m["count"].numpy() + 63) // 64, 1) for m in metas]
+    h_all, f_all = np.concatenate(heads), np.concatenate(floors).astype(np.float64)
+    w_all = np.concatenate([np.full(len(h), b, np.float64) for h, b in zip(heads, batches)])
+    items = lambda t: float((w_all * np.maximum(np.ceil(h_all / t), f_all)).sum())
+    lo, hi = max(float(c.max()) for c in costs), float(h_all.max()) + 1.0
     if items(hi) <= slots:
         for _ in range(60):
             mid = (lo + hi) / 2
             lo, hi = (lo, mid) if items(mid) <= slots else (mid, hi)
     out = []
-    for m, c, h, f in zip(metas, costs, head, floor):
-        n = torch.maximum(torch.ceil(h / hi).to(torch.int64), f)
+    for m, c, h, f in zip(metas, costs, heads, floors):
+        n = np.maximum(np.ceil(h / hi).astype(np.int64), f)
+        valid = m["valid"].numpy()
         while True:
-            b = split_bounds(c, m["valid"], n)
-            over = (b.diff(dim=1) > 64).any(1)
-            if not bool(over.any()):
+            b = split_bounds(c, valid, n)
+            over = (np.diff(b, axis=1) > 64).any(1)
+            if not over.any():
                 break
-            n = n + over.to(torch.int64)
+            n = n + over
         out.append(b)
     splits = max(b.shape[1] - 1 for b in out)
-    pad = lambda b: torch.cat([b, b[:, -1:].expand(-1, splits + 1 - b.shape[1])], 1)
-    return [pad(b).to(torch.int32) for b in out], splits
+    pad = lambda b: np.concatenate([b, np.repeat(b[:, -1:], splits + 1 - b.shape[1], 1)], 1)
+    return [torch.from_numpy(pad(b).astype(np.int32)) for b in out], splits
 
 
 class DecodeCache:

@@ -6,7 +6,6 @@ import torch
 
 import oracle as O
 from triattention_amd.kernels import records as R
-from triattention_amd.kernels.decode import DecodeCache
 from triattention_amd.kernels.prefill import F16, I4, I8, Prefill
 from triattention_amd.maps import from_bands
 from triattention_amd.synthetic import bits

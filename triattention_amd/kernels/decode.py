@@ -32,7 +32,7 @@ K8_WORDS, K4_WORDS = 2048, 1024
 KX_BYTES = 16384
 NEAR_V8 = 16
 SPLITS_PER_CU = 4  # decode workgroups per CU that the split partition targets
-TILE_COST = 4096   # per-tile cost of the split kernel beyond its record bytes (instruction stream), in bytes
+TILE_COST = 8192   # per-tile cost of the split kernel beyond its record bytes (instruction stream), in bytes
 BALANCE_TILES = 16  # kept tiles per slot up to which the split partition is balanced by cost
 
 

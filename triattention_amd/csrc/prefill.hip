@@ -434,6 +434,11 @@ __global__ __launch_bounds__(256) void pack_exact_kernel(ExactPackArgs a) {
   }
 }
 
+template <int V>
+struct Tag {
+  static constexpr int value = V;
+};
+
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillArgs a) {
   // LDS: two K buffers (8 KiB) and two V buffers (8 KiB), distinct objects so
   // that the compiler can tell a read of one buffer from a load into the other;
@@ -531,24 +536,39 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
         __builtin_amdgcn_global_load_lds(static_cast<const void*>((i < n8 ? ka8 : ka4p) + col * 4),
                                          (__attribute__((address_space(3))) void*)sd, 16, 0, 0);
     };
-    // tile i: wait for its records (and for every wave to finish tile i-1,
-    // whose buffers receive tile i+1), start tile i+1's loads, compute
-    auto step = [&](int i, const uint8_t* kc, const uint8_t* vc, const float* sc, uint8_t* kn, uint8_t* vn,
-                    float* sn) {
+    // tile i of kind KIND: wait for its records (and for every wave to finish
+    // tile i-1, whose buffers receive tile i+1), start tile i+1's loads, compute
+    auto step = [&](auto kind, int i, const uint8_t* kc, const uint8_t* vc, const float* sc, uint8_t* kn,
+                    uint8_t* vn, float* sn) {
       lds_wait();
       if (i + 1 < total) issue(i + 1, kn, vn, sn);
       const int col = tile_col(i);
       const float4 k4v = *reinterpret_cast<const float4*>(sc);
       const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
-      if (i < n8) prefill_tile<KI8>(a, st, qf, qs8, ks, col, false, qrow, kc, vc);
+      if constexpr (decltype(kind)::value == KI8) prefill_tile<KI8>(a, st, qf, qs8, ks, col, false, qrow, kc, vc);
       else prefill_tile<KQ4>(a, st, q4f, qs4, ks, col, false, qrow, kc, vc);
+    };
+    // Tiles [i, end) of one kind, the first in buffer set PARITY.  Each kind has a
+    // loop of its own: with both kinds in one loop body the compiler copies the
+    // accumulators between register sets at every tile (~30 VALU per tile).
+    auto run = [&](auto kind, auto parity, int i, int end) {
+      constexpr bool p = decltype(parity)::value != 0;
+      uint8_t* k0 = p ? k_lds1 : k_lds0;
+      uint8_t* k1 = p ? k_lds0 : k_lds1;
+      uint8_t* v0 = p ? v_lds1 : v_lds0;
+      uint8_t* v1 = p ? v_lds0 : v_lds1;
+      float* s0 = p ? ks_lds1 : ks_lds0;
+      float* s1 = p ? ks_lds0 : ks_lds1;
+      for (; i < end; i += 2) {
+        step(kind, i, k0, v0, s0, k1, v1, s1);
+        if (i + 1 < end) step(kind, i + 1, k1, v1, s1, k0, v0, s0);
+      }
     };
     __syncthreads();  // every wave is done with the F16 pass's LDS
     issue(0, k_lds0, v_lds0, ks_lds0);
-    for (int i = 0; i < total; i += 2) {
-      step(i, k_lds0, v_lds0, ks_lds0, k_lds1, v_lds1, ks_lds1);
-      if (i + 1 < total) step(i + 1, k_lds1, v_lds1, ks_lds1, k_lds0, v_lds0, ks_lds0);
-    }
+    run(Tag<KI8>{}, Tag<0>{}, 0, n8);
+    if (n8 & 1) run(Tag<KQ4>{}, Tag<1>{}, n8, total);
+    else run(Tag<KQ4>{}, Tag<0>{}, n8, total);
   }
 
   // ---- epilogue: out = fma(acc / den, scale, mean) (prefill_sm80.cu:466-487)

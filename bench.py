@@ -51,7 +51,7 @@ def decode_record_bytes(cache_entry):
     e = cache_entry
     kinfo = e["kinfo"].cpu().to(torch.int64)
     count = e["count"].cpu().to(torch.int64)
-    entry = e["entry"].cpu().to(torch.int64)
+    entry = e["entry"].cpu().to(torch.int64) & ((1 << 29) - 1)  # the tile index (bits 0-28)
     fmt = e["fmt"].cpu().to(torch.int64)
     b, hk, maxn = kinfo.shape
     valid = torch.arange(maxn)[None, None, :] < count[:, :, None]

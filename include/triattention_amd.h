@@ -97,6 +97,10 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * record in kxc/vxc (tri_pack_exact layout, n_kx records of 16 KiB each); such
  * a head keeps every prompt tile (count = tiles, entry[e] = e) and attends
  * exactly over its bf16 prompt and tail.
+ * Entry words (extension): bits 0-28 hold the tile index; when bit 30 is set,
+ * bit 29 holds the tile's V format (1 = INT8 V) and must agree with fmt, and the
+ * kernel then starts streaming a split's first V record one memory round trip
+ * earlier (reference-style entries, bits 29-30 clear, read fmt).
  * Split partition (extension): bounds NULL splits every head's kept tiles into
  * runs of `per` (the reference's split); otherwise bounds is int32
  * [batch][hk][nsplit + 1] and split s of a head covers entries

@@ -189,6 +189,30 @@ def test_decode_full_1024_token_tail(module):
     assert np.array_equal(bits(e["tail_k"].cpu()), ktail) and np.array_equal(bits(e["tail_v"].cpu()), vtail)
 
 
+def test_decode_entries_without_v_format_flags(module):
+    """Entry words without the V-format flags (the reference's plain tile indices) make the kernel
+    read fmt instead; the outputs are bit-identical."""
+    from triattention_amd.kernels.decode import ENTRY_TILE
+    print("\n[parity] decode with plain tile indices in the entry table", flush=True)
+    hq, hk, prompt = 8, 2, 1100
+    bands = torch.tensor([[INF, INF], [1, INF], [2, 5], [1, 1], [3, INF], [1, 2], [INF, INF], [2, 2]],
+                         dtype=torch.int32)
+    q, k, v = small(5700, 2, hq, hk, prompt)
+    cache = DecodeCache(module, max_tail=4)
+    cache.out_dtype = torch.float32
+    run_prefill(module, q, k, v, bands, 128 ** -0.5, decode_cache=cache)
+    g = S.gen(5701)
+    dev = torch.device("cuda")
+    qd, kd, vd = (S.outlier_tensor(g, 2, hq, 1).to(dev), S.outlier_tensor(g, 2, hk, 1).to(dev),
+                  S.outlier_tensor(g, 2, hk, 1).to(dev))
+    flagged = cache(0, qd, kd, vd, 128 ** -0.5).cpu()
+    e = cache.layers[0]
+    assert bool((e["entry"] != (e["entry"] & ENTRY_TILE)).any())
+    e["entry"].bitwise_and_(ENTRY_TILE)
+    plain = cache(0, qd, kd, vd, 128 ** -0.5).cpu()
+    assert torch.equal(flagged.view(torch.int32), plain.view(torch.int32))
+
+
 def test_ragged_decode_batch(module):
     """Ragged cache: four prompts of different lengths stored by separate Prefill calls, served by one
     decode launch per step; every sequence matches the oracle."""

@@ -10,7 +10,7 @@ import torch
 import oracle as O
 from triattention_amd import maps
 from triattention_amd.kernels import records as R
-from triattention_amd.kernels.decode import DecodeCache, sequence_metadata, tile_states
+from triattention_amd.kernels.decode import ENTRY_TILE, ENTRY_V8, ENTRY_VFMT, DecodeCache, sequence_metadata, tile_states
 from triattention_amd.kernels.prefill import F16, I4, I8, Q4, BandTable
 from triattention_amd.synthetic import INF
 
@@ -149,7 +149,10 @@ def test_ragged_cache_assembly_slots_are_consistent():
         for s in range(batch):
             for kh in range(hk):
                 for n in range(int(e["count"][row, kh])):
-                    j = int(e["entry"][row, kh, n])
+                    word = int(e["entry"][row, kh, n])
+                    j = word & ENTRY_TILE
+                    # the V format travels in the entry word too, and agrees with fmt
+                    assert word & ENTRY_VFMT and bool(word & ENTRY_V8) == (int(e["fmt"][row, j]) == 1)
                     info = int(e["kinfo"][row, kh, n])
                     src, dst = (k4, e["k4"]) if (info >> 8) & 1 else (k8, e["k8"])
                     assert torch.equal(dst[info >> 9], src[s, kh, j])
@@ -219,7 +222,7 @@ def test_exact_heads_in_a_ragged_cache():
             assert int(e["xslot"][row, 1]) == -1
             for slot, h in enumerate(exact_kv):
                 assert int(e["count"][row, h]) == tiles
-                assert e["entry"][row, h, :tiles].tolist() == list(range(tiles))
+                assert (e["entry"][row, h, :tiles] & ENTRY_TILE).tolist() == list(range(tiles))
                 x0 = int(e["xslot"][row, h])
                 for j in range(tiles):
                     assert torch.equal(kxs[x0 + j], kx[s, slot, j]) and torch.equal(vxs[x0 + j], vx[s, slot, j])

@@ -52,6 +52,9 @@ struct DecodeArgs {
 };
 
 constexpr int MAX_TAIL = 1024;
+// entry words: bits 0-28 the tile index; bit 30 set (extension) marks that bit 29 holds the
+// tile's V format (1 = INT8 V), so the kernel need not read fmt for it
+constexpr int ENTRY_TILE = (1 << 29) - 1, ENTRY_V8 = 1 << 29, ENTRY_VFMT = 1 << 30;
 constexpr int MAX_PER = 64;  // kept tiles per split: one per lane of the wave's metadata
 
 // Entries [first, last) of split `split` of head hb: the uniform split of a.per
@@ -337,34 +340,46 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   // Entry first + L of the split (clamped into the entry table, so every lane
   // loads; the tile index is clamped too, as entries past the count are not
   // tiles); lanes past the split's end get the out-of-range offsets.
+  Meta mc;  // the split's first tile
   int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);  // koff, voff, info | v8 << 9 | j << 10
   float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
   {
     const bool valid = L < last - first;
     // (independent of the split's entry count, so these loads need not wait for it)
     const int64_t li = mbase + min(first + min(L, last - first - 1), a.maxn - 1);
-    const int info = a.kinfo[li], jr = a.entry[li], vs = a.slot[li];
+    const int info = a.kinfo[li], er = a.entry[li], vs = a.slot[li];
     // (keep the entry and slot loads ahead of the K loads: the tile-index loads below wait for
     // the entry, and waits count loads in issue order)
     __builtin_amdgcn_sched_barrier(0);
     const int is4 = valid ? (info >> 8) & 1 : 0;
+    const int j = min(max(er & ENTRY_TILE, 0), a.tiles_max - 1);
+    // the K scales first: waits count loads in issue order, so the wait for them (before the
+    // LDS writes below) then holds no record load
+    const float4 kl = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
+    __builtin_amdgcn_sched_barrier(0);
     if (valid) w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
     {
-      // the first tile's K streams as soon as its kinfo is in (lane 0 holds the entry), one
-      // memory round trip before its V, whose format and slot need the tile index first
+      // the first tile's K streams (lane 0 holds the entry)
       Meta m0;
       m0.koff = __builtin_amdgcn_readfirstlane(w.x);
       m0.info = __builtin_amdgcn_readfirstlane(info & 0x1ff);
       load_k(m0);
     }
-    const int j = min(max(jr, 0), a.tiles_max - 1);
-    const int vf = a.fmt[(int64_t)b * a.tiles_max + j];
-    const float4 kl = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
+    // The V format: from the entry when the cache marked it there, else from fmt, one memory
+    // round trip after the entry (a uniform branch: the marked path never waits for a fmt load).
+    // Then the first tile's V streams, while Q is quantized.
+    int vf = (er & ENTRY_V8) ? 1 : 2;
+    if (!__builtin_amdgcn_readfirstlane((int)__all(!valid || (er & ENTRY_VFMT)))) {
+      vf = a.fmt[(int64_t)b * a.tiles_max + j];
+      asm volatile("" ::"v"(vf));  // wait for it here, so that no wait follows the join
+    }
     if (valid) {
-      ka = kl;
       w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
       w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
     }
+    mc = unpack(w);
+    load_v(mc);
+    if (valid) ka = kl;
     meta[L] = w;
     metk[L] = ka;
     if (L == 0) {
@@ -372,9 +387,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
     }
   }
-  // its V streams while Q is quantized
-  Meta mc = unpack(w);
-  load_v(mc);
 
   // ---- in-kernel Q quantization of the g rows (common_device.cuh:291-315)
   {

@@ -34,6 +34,9 @@ NEAR_V8 = 16
 SPLITS_PER_CU = 4  # decode workgroups per CU that the split partition targets
 TILE_COST = 8192   # per-tile cost of the split kernel beyond its record bytes (instruction stream), in bytes
 BALANCE_TILES = 16  # kept tiles per slot up to which the split partition is balanced by cost
+# entry words: bits 0-28 the tile index (decode.py:36); extension: bit 30 marks that bit 29 holds
+# the tile's V format (1 = INT8 V), which spares the decode kernel a dependent load of fmt
+ENTRY_TILE, ENTRY_V8, ENTRY_VFMT = (1 << 29) - 1, 1 << 29, 1 << 30
 
 
 def tile_states(bands: torch.Tensor, tiles: int) -> torch.Tensor:
@@ -235,7 +238,7 @@ class DecodeCache:
             rows = slice(row, row + b)
             sq = torch.arange(b, **i64)
             s3 = sq[:, None, None]
-            entry[rows, :, :n] = torch.where(d["valid"], d["order"], 0)
+            entry[rows, :, :n] = torch.where(d["valid"], d["order"] | ENTRY_VFMT | (d["vcode"] == I8).to(torch.int64) << 29, 0)
             ks = torch.where(d["is4"], d["kslot"] + o4 + s3 * g["n4"], d["kslot"] + o8 + s3 * g["n8"])
             kinfo[rows, :, :n] = torch.where(d["valid"], d["kbase"] | (ks << 9), 0)
             vs = torch.where(d["vcode"] == I4, d["vslot"] + ov4 + s3 * g["nv"][I4], d["vslot"] + ov8 + s3 * g["nv"][I8])

@@ -1,6 +1,7 @@
 // extern "C" entry points: argument validation, launch geometry, error text.
 // One translation unit holds every kernel of the library.
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -35,6 +36,35 @@ int check_launch(const char* what) {
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
 }  // namespace
+
+// Quantized-head decode launch with NW waves per workgroup; groups of up to 4
+// q-heads use the DUP lane layout (both wave halves on rows 0..3).
+template <int NW>
+static void launch_decode(int g, dim3 grid, const tri::DecodeArgs& d, hipStream_t s) {
+  switch (g) {
+    case 1: tri::decode_kernel<1, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
+    case 2: tri::decode_kernel<2, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
+    case 3: tri::decode_kernel<3, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
+    case 4: tri::decode_kernel<4, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
+    default: tri::decode_kernel<4, false, false, NW><<<grid, 64 * NW, 0, s>>>(d); break;
+  }
+}
+
+// CU count of the current device, cached per device (devices 0..63)
+static int device_cus(int* cus) {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  const bool cacheable = e == hipSuccess && dev >= 0 && dev < 64;
+  if (cacheable && cached[dev].load(std::memory_order_relaxed) > 0) {
+    *cus = cached[dev].load(std::memory_order_relaxed);
+    return 0;
+  }
+  if (e == hipSuccess) e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return fail("device_cus: %s", hipGetErrorString(e));
+  if (cacheable) cached[dev].store(*cus, std::memory_order_relaxed);
+  return 0;
+}
 
 extern "C" {
 
@@ -302,17 +332,19 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (phase & 1) {
     const dim3 grid(splits, hk, batch);
-    // groups of up to 4 q-heads use the DUP lane layout (both wave halves on rows 0..3)
     const int g = hq / hk;
     if (xslot == nullptr) {
-      switch (g) {
-        case 1: tri::decode_kernel<1, false, true><<<grid, 64, 0, s>>>(d); break;
-        case 2: tri::decode_kernel<2, false, true><<<grid, 64, 0, s>>>(d); break;
-        case 3: tri::decode_kernel<3, false, true><<<grid, 64, 0, s>>>(d); break;
-        case 4: tri::decode_kernel<4, false, true><<<grid, 64, 0, s>>>(d); break;
-        default: tri::decode_kernel<4, false, false><<<grid, 64, 0, s>>>(d); break;
-      }
+      // Two waves per workgroup (alternate tiles of a split) when the grid exceeds one
+      // wave of resident workgroups (4 per CU): the dispatcher queues workgroups anyway,
+      // and two waves per SIMD interleave their dependency chains (C3: 138 -> 133 us).
+      // A grid of at most one resident wave keeps one wave per SIMD, which streams
+      // better (C1: 37.4 us, against 39.3 us with two waves per workgroup).
+      int cus = 0;
+      if (device_cus(&cus) != 0) return 1;
+      if ((int64_t)splits * hk * batch > 4 * (int64_t)cus) launch_decode<2>(g, grid, d, s);
+      else launch_decode<1>(g, grid, d, s);
     } else {
+      // groups of up to 4 q-heads use the DUP lane layout (both wave halves on rows 0..3)
       switch (g) {
         case 1: tri::decode_kernel<1, true, true><<<grid, 64, 0, s>>>(d); break;
         case 2: tri::decode_kernel<2, true, true><<<grid, 64, 0, s>>>(d); break;
@@ -357,11 +389,7 @@ int tri_decode_occupancy(int* blocks) {
 int tri_device_cus(int* cus) {
   g_error.clear();
   if (!cus) return fail("device_cus: null output");
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e != hipSuccess) return fail("device_cus: %s", hipGetErrorString(e));
-  return 0;
+  return device_cus(cus);
 }
 
 }  // extern "C"

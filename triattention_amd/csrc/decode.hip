@@ -201,12 +201,17 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
 // DUP (groups of at most 4 q-heads): the score rows 4..7 of the QK MFMA do not
 // exist, so the upper half of the wave takes the tile's second 32-key block
 // for rows 0..3 instead, and every lane carries R scores rather than 2R.
-template <int R, bool EXACT = false, bool DUP = false, int W = (EXACT || R >= 4 ? 2 : 3)>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
+// NW: waves per workgroup.  With NW = 2 the two waves share the split's Q
+// quantization and metadata, take its tiles alternately (wave w: entries first
+// + w, first + w + 2, ...), and combine their running (m, l, o) in LDS at the
+// end, so that each SIMD holds two waves whose dependency chains interleave.
+template <int R, bool EXACT = false, bool DUP = false, int NW = 1, int W = (EXACT || R >= 4 || NW > 1 ? 2 : 3)>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
+  static_assert(NW == 1 || (NW == 2 && !EXACT), "two waves per workgroup only for quantized heads");
   __shared__ __align__(16) int8_t q8s[MAX_GROUP][D];
   __shared__ __align__(16) int8_t q4s[MAX_GROUP][D];
   __shared__ float qsc[MAX_GROUP], qsc4[MAX_GROUP];
-  __shared__ __align__(16) uint8_t pls[MAX_GROUP][BN];
+  __shared__ __align__(16) uint8_t pls_all[NW][MAX_GROUP][BN];
   __shared__ __align__(16) int4 meta[MAX_PER + 1];     // per-tile record offsets and flags
   __shared__ __align__(16) float4 metk[MAX_PER + 1];   // per-tile K group scales
 
@@ -226,10 +231,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   }
   // A split past its head's kept tiles (ragged batches: most splits of the short sequences)
   // writes the empty partial (m = -FLT_MAX, l = 0, o = 0) and leaves.
+  const int wv = NW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
   int first, last;
   split_range(a, (int64_t)b * a.hk + kh, split, first, last);
   if (first >= last) {
-    const int L = threadIdx.x, g = a.hq / a.hk;
+    if (wv) return;
+    const int L = threadIdx.x & 63, g = a.hq / a.hk;
     for (int r = 0; r < g; ++r) {
       const int64_t idx = ((int64_t)b * a.hq + kh * g + r) * a.splits + split;
       *reinterpret_cast<float2*>(a.po + idx * D + 2 * L) = make_float2(0.f, 0.f);
@@ -246,9 +253,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       return;
     }
   }
-  const int L = threadIdx.x, lq = L & 31, half = L >> 5;
+  const int L = threadIdx.x & 63, lq = L & 31, half = L >> 5;
   const int g = a.hq / a.hk;
   const int prompt = a.prompt[b];
+  uint8_t (&pls)[MAX_GROUP][BN] = pls_all[wv];
   const int64_t hb = (int64_t)b * a.hk + kh;
 
   // The g query rows are loaded first, one row per 8 lanes, 16 channels per
@@ -359,10 +367,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
     __builtin_amdgcn_sched_barrier(0);
     if (valid) w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
     {
-      // the first tile's K streams (lane 0 holds the entry)
+      // the wave's first tile's K streams (lane wv holds entry first + wv)
       Meta m0;
-      m0.koff = __builtin_amdgcn_readfirstlane(w.x);
-      m0.info = __builtin_amdgcn_readfirstlane(info & 0x1ff);
+      m0.koff = __builtin_amdgcn_readlane(w.x, wv);
+      m0.info = __builtin_amdgcn_readlane(info & 0x1ff, wv);
       load_k(m0);
     }
     // The V format: from the entry when the cache marked it there, else from fmt, one memory
@@ -377,7 +385,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
       w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
     }
-    mc = unpack(w);
+    mc = unpack(int4{__builtin_amdgcn_readlane(w.x, wv), __builtin_amdgcn_readlane(w.y, wv),
+                     __builtin_amdgcn_readlane(w.z, wv), 0});
     load_v(mc);
     if (valid) ka = kl;
     meta[L] = w;
@@ -427,9 +436,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   }
   for (int i = L; i < MAX_GROUP * BN / 4; i += 64) reinterpret_cast<uint32_t*>(&pls[0][0])[i] = 0u;
   __syncthreads();
-  k_scales(first);
-  Meta mn = fetch(first + 1);
-  for (int e = first; e < last; ++e) {
+  k_scales(first + wv);
+  Meta mn = fetch(first + wv + NW);
+  for (int e = first + wv; e < last; e += NW) {
     const int info = mc.info;
     const int is4 = (info >> 8) & 1;
     const unsigned rowmask = info & 0xff;
@@ -465,7 +474,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       }
     const float kv0 = kav[0], kv1 = kav[1];
     load_k(mn);  // K registers are free again (past the end: no memory access)
-    k_scales(e + 1);
+    k_scales(e + NW);
     float kavc[NK];
     if constexpr (DUP) kavc[0] = half ? kv1 : kv0;
     else { kavc[0] = kv0; kavc[NK - 1] = kv1; }
@@ -552,7 +561,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       }
       den[r] = __builtin_fmaf((float)psum, bq[r], den[r]);
     }
-    __syncthreads();
+    if constexpr (NW == 1) {
+      __syncthreads();
+    } else {
+      // the P levels are this wave's own: order its LDS writes before its reads
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
     // ---- O = P V
     v4i pa[2];
 #pragma unroll
@@ -564,7 +580,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
       }
       pa[kb] = w;
     }
-    const Meta mnn = fetch(e + 2);
+    const Meta mnn = fetch(e + 2 * NW);
     if (vf == 1) {
       const v4i neg127 = {(int)0x81818181u, (int)0x81818181u, (int)0x81818181u, (int)0x81818181u};
       const v4i p0 = pa[0] ^ 0x7f7f7f7f, p1 = pa[1] ^ 0x7f7f7f7f;  // 127 - P as s8
@@ -599,6 +615,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W))) void de
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int o = 1; o < (DUP ? 64 : 32); o <<= 1) den[r] += __shfl_xor(den[r], o, 64);
+  if constexpr (NW > 1) {
+    // wave 1 hands its (m, l, o) to wave 0, which rescales both to the larger m
+    __shared__ float cm[2][4], cd[2][4];  // [half][r]
+    __shared__ float co[4][R][64];
+    if (wv == 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) co[cb][r][L] = acc[cb][r];
+        if (lq == 0) cd[half][r] = den[r];
+      }
+      if (owner && lq < 4) cm[DUP ? 0 : half][L & 3] = m_o;
+    }
+    __syncthreads();
+    if (wv == 1) return;
+    float m_new = m_o;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int hh = DUP ? 0 : half;
+      const float m0 = DUP ? readlane_f(m_o, r) : (half ? readlane_f(m_o, 32 + r) : readlane_f(m_o, r));
+      const float m1 = cm[hh][r];
+      const float mx = fmaxf(m0, m1), a0 = texp2(m0 - mx), a1 = texp2(m1 - mx);
+      den[r] = __builtin_fmaf(cd[half][r], a1, den[r] * a0);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) acc[cb][r] = __builtin_fmaf(co[cb][r][L], a1, acc[cb][r] * a0);
+      if ((L & 3) == r) m_new = mx;
+    }
+    m_o = m_new;
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int q = 4 * half + r;

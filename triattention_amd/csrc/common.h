@@ -24,6 +24,7 @@
 // 32x32 result), so a lane's probabilities feed the PV MFMA without shuffles.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <climits>
 #include <stdint.h>
 
 namespace tri {
@@ -195,6 +196,32 @@ __device__ __forceinline__ float half_max(float v, bool upper) {
   return upper ? hi : lo;
 }
 
+
+// maximum of each 16-lane row of an int, in every lane of the row (the DPP moves
+// fold into v_max_i32)
+template <int CTRL>
+__device__ __forceinline__ int dpp_move_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true);
+}
+__device__ __forceinline__ int row16_max_i(int v) {
+  v = max(v, dpp_move_i<0xB1>(v));
+  v = max(v, dpp_move_i<0x4E>(v));
+  v = max(v, dpp_move_i<0x141>(v));
+  return max(v, dpp_move_i<0x140>(v));
+}
+// maximum over the wave of a value that is uniform within each 16-lane row, as a
+// uniform value: row_bcast:15 and row_bcast:31 fold the rows into lane 63
+__device__ __forceinline__ float rows_max_wave(float v) {
+  v = fmaxf(v, dpp_rows<0x142, 0xA>(v));
+  v = fmaxf(v, dpp_rows<0x143, 0xC>(v));
+  return readlane_f(v, 63);
+}
+// the same over the lane's 32-lane half
+__device__ __forceinline__ float rows_max_half(float v, bool upper) {
+  v = fmaxf(v, dpp_rows<0x142, 0xA>(v));
+  const float lo = readlane_f(v, 31), hi = readlane_f(v, 63);
+  return upper ? hi : lo;
+}
 
 // byte 1 of each of four words, packed (P levels out of the 49152.5 magic).
 __device__ __forceinline__ uint32_t pack_byte1(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {

@@ -10,7 +10,10 @@
 // is processed); no LDS staging is needed because every fragment is consumed by
 // exactly one wave.  Quantized heads: the g <= 8 query heads of the KV group
 // are the rows of the MFMA A operand (S = Q K^T, one key per lane and row
-// block); exact heads: they are the columns of the B operand (S^T = K Q^T).
+// block); with groups of up to 4 and 4-bit keys, each lane instead scores its
+// own key against the group's rows with packed 4-bit dot products
+// (v_dot8_i32_i4, the same integers); exact heads: the q-heads are the columns
+// of the B operand (S^T = K Q^T).
 #include "common.h"
 
 namespace tri {
@@ -205,12 +208,13 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
 // quantization and metadata, take its tiles alternately (wave w: entries first
 // + w, first + w + 2, ...), and combine their running (m, l, o) in LDS at the
 // end, so that each SIMD holds two waves whose dependency chains interleave.
-template <int R, bool EXACT = false, bool DUP = false, int NW = 1, int W = (EXACT || R >= 4 || NW > 1 ? 2 : 3)>
+template <int R, bool EXACT = false, bool DUP = false, int NW = 1, int W = 2>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
   static_assert(NW == 1 || (NW == 2 && !EXACT), "two waves per workgroup only for quantized heads");
   __shared__ __align__(16) int8_t q8s[MAX_GROUP][D];
   __shared__ __align__(16) int8_t q4s[MAX_GROUP][D];
   __shared__ float qsc[MAX_GROUP], qsc4[MAX_GROUP];
+  __shared__ __align__(16) uint32_t q4w[MAX_GROUP][D / 8];  // packed 4-bit Q words (DUP score path)
   __shared__ __align__(16) uint8_t pls_all[NW][MAX_GROUP][BN];
   __shared__ __align__(16) int4 meta[MAX_PER + 1];     // per-tile record offsets and flags
   __shared__ __align__(16) float4 metk[MAX_PER + 1];   // per-tile K group scales
@@ -320,16 +324,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     kav[0] = (lq >> 4) ? s4.y : s4.x;
     kav[1] = (lq >> 4) ? s4.w : s4.z;
   };
+  // DUP layout, 4-bit keys: lane L scores key 32*half + lq itself with packed 4-bit dot products, so
+  // it loads that key's 128 features: the 16 bytes at P*1024 + 16*(32*fh + lq) for P = 2*half + i/2,
+  // fh = i%2 (fragments 2P and 2P+1 of the record, feature half fh)
+  int k4off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) k4off[i] = (2 * half + (i >> 1)) * 1024 + 512 * (i & 1) + 16 * lq;
   auto load_k = [&](const Meta& m) {
     const int is4 = (m.info >> 8) & 1;
     // The same eight 16-byte loads for either width (a per-format load sequence
     // would make the compiler wait for every outstanding load at each tile): a
-    // K8 record is fragments 0..7; a K4 record is four fragment pairs, and the
-    // upper four loads are past the end of the range (zeros, no memory access).
+    // K8 record is fragments 0..7; a K4 record takes four loads (its fragment
+    // pairs, or with DUP the lane's own key), and the upper four loads are past
+    // the end of the range (zeros, no memory access).
     const __amdgpu_buffer_rsrc_t rk = is4 ? rk4 : rk8;
     const int hi = is4 ? OUT_OF_RANGE : m.koff;
 #pragma unroll
-    for (int F = 0; F < 8; ++F) kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, L * 16 + F * 1024, F < 4 ? m.koff : hi, 0);
+    for (int F = 0; F < 8; ++F) {
+      const int vo = (DUP && F < 4 && is4) ? k4off[F] : L * 16 + F * 1024;
+      kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo, F < 4 ? m.koff : hi, 0);
+    }
   };
   auto load_v = [&](const Meta& m) {
     const bool v4 = m.vf != 1;
@@ -413,7 +427,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     mx = lanes8_max(mx);
     const bool live = qrw < g;
     const float inv = mx > 0.f ? 127.f / mx : 0.f, inv4 = mx > 0.f ? 7.f / mx : 0.f;
-    uint32_t w8[4], w4[4];
+    uint32_t w8[4], w4[4], c4[16];
 #pragma unroll
     for (int wd = 0; wd < 4; ++wd) {
       w8[wd] = 0u;
@@ -422,13 +436,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
       for (int i = 0; i < 4; ++i) {
         const float x = xv[4 * wd + i];
         w8[wd] |= ((uint32_t)(int)__builtin_rintf(x * inv) & 0xffu) << (8 * i);
-        const int c4 = (((int)__builtin_rintf(x * inv4) & 0xf) ^ 8) - 8;
-        w4[wd] |= ((uint32_t)c4 & 0xffu) << (8 * i);
+        c4[4 * wd + i] = (uint32_t)(int)__builtin_rintf(x * inv4) & 0xfu;
+        w4[wd] |= ((uint32_t)((((int)c4[4 * wd + i]) ^ 8) - 8) & 0xffu) << (8 * i);
       }
       if (!live) w8[wd] = w4[wd] = 0u;
     }
     *reinterpret_cast<uint4*>(&q8s[qrw][qt * 16]) = make_uint4(w8[0], w8[1], w8[2], w8[3]);
     *reinterpret_cast<uint4*>(&q4s[qrw][qt * 16]) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    // packed 4-bit words of features fb..fb+7 (fb = 16*qt, 16*qt + 8) in the nibble order of a K4
+    // record word: features fb, fb+4, fb+1, fb+5, fb+2, fb+6, fb+3, fb+7
+    uint32_t pw[2] = {0u, 0u};
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int n = 0; n < 8; ++n) pw[h] |= c4[8 * h + (n >> 1) + 4 * (n & 1)] << (4 * n);
+    *reinterpret_cast<uint2*>(&q4w[qrw][2 * qt]) = live ? make_uint2(pw[0], pw[1]) : make_uint2(0u, 0u);
     if (qt == 0) {
       qsc[qrw] = (live && mx > 0.f) ? mx / 127.f * a.sm_log2 : 1.17549435e-38f;
       qsc4[qrw] = (live && mx > 0.f) ? mx / 7.f * a.sm_log2 : 1.17549435e-38f;
@@ -436,6 +458,38 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   }
   for (int i = L; i < MAX_GROUP * BN / 4; i += 64) reinterpret_cast<uint32_t*>(&pls[0][0])[i] = 0u;
   __syncthreads();
+  // DUP: the Q operands stay in registers for the whole split.  INT8 keys: the A operand of the QK
+  // MFMA (row lq is q-head lq, rows 4..7 repeat q-heads 0..3, rows 8.. zero).  INT4 keys: the packed
+  // words of rows 0..R-1, in the order of the lane's four K loads (load i, word w: feature
+  // 32*(2*(i/2) + w/2) + 16*(i%2) + 8*(w%2)).
+  // (two waves per workgroup with 4 rows: the packed words are read from LDS at each tile instead,
+  // as 64 more registers would not fit two waves per SIMD)
+  constexpr bool QW_REGS = !(NW > 1 && R >= 4);
+  v4i q8a[4];
+  uint32_t qw[QW_REGS ? R : 1][16];
+  if constexpr (DUP) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const v4i z = {0, 0, 0, 0};
+      q8a[ks] = lq < MAX_GROUP ? *reinterpret_cast<const v4i*>(&q8s[lq & 3][ks * 32 + 16 * half]) : z;
+    }
+    if constexpr (QW_REGS) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) qw[r][4 * i + w] = q4w[r][4 * (2 * (i >> 1) + (w >> 1)) + 2 * (i & 1) + (w & 1)];
+    }
+  }
+  // Q scales in registers: per row of the lane, and the owner row's
+  float qsr8[R], qsr4[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    qsr8[r] = qsc[qrow(r)];
+    qsr4[r] = qsc4[qrow(r)];
+  }
+  const float qs8_own = orow < g ? qsc[orow] : 1.17549435e-38f, qs4_own = orow < g ? qsc4[orow] : 1.17549435e-38f;
   k_scales(first + wv);
   Meta mn = fetch(first + wv + NW);
   for (int e = first + wv; e < last; e += NW) {
@@ -446,32 +500,54 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     const int vf = mc.vf;
     const float cur_kmax = kmax;
     // ---- S = Q K^T
-    v4i qa[4];
-    const int8_t* qsrc = is4 ? &q4s[0][0] : &q8s[0][0];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      v4i z = {0, 0, 0, 0};
-      // A-operand row lq is q-head lq; with DUP rows 4..7 repeat q-heads 0..3, so the upper
-      // half of the result holds rows 0..3 against the second key block
-      const int qr = DUP ? (lq & 3) : lq;
-      qa[ks] = lq < MAX_GROUP ? *reinterpret_cast<const v4i*>(qsrc + qr * D + ks * 32 + 16 * half) : z;
-    }
-    v16i s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s[kb] = mfma_i8(qa[ks], is4 ? frag4(kf, kb * 4 + ks) : kf[kb * 4 + ks], s[kb]);
-    }
     int dot[R][NK];
+    if (DUP && is4) {
+      // 4-bit keys: packed 4-bit dot products of the lane's key against each row (exact integers)
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+      for (int r = 0; r < R; ++r) dot[r][0] = 0;
 #pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        const int v = DUP ? (half ? s[1][r] : s[0][r]) : s[t][r];
-        dot[r][t] = is4 ? (v >> 4) : v;
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int word = 4 * (2 * (i >> 1) + (w >> 1)) + 2 * (i & 1) + (w & 1);
+            const uint32_t qv = QW_REGS ? qw[QW_REGS ? r : 0][4 * i + w] : q4w[r][word];
+            dot[r][0] = __builtin_amdgcn_sdot8((int)qv, kf[i][w], dot[r][0], false);
+          }
+    } else {
+      v4i qa[4];
+      if constexpr (DUP) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qa[ks] = q8a[ks];
+      } else {
+        const int8_t* qsrc = is4 ? &q4s[0][0] : &q8s[0][0];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          v4i z = {0, 0, 0, 0};
+          // A-operand row lq is q-head lq
+          qa[ks] = lq < MAX_GROUP ? *reinterpret_cast<const v4i*>(qsrc + lq * D + ks * 32 + 16 * half) : z;
+        }
       }
+      // with DUP rows 4..7 repeat q-heads 0..3, so the upper half of the result holds rows 0..3
+      // against the second key block
+      v16i s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] = 0;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          s[kb] = mfma_i8(qa[ks], (!DUP && is4) ? frag4(kf, kb * 4 + ks) : kf[kb * 4 + ks], s[kb]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < NK; ++t) {
+          const int v = DUP ? (half ? s[1][r] : s[0][r]) : s[t][r];
+          dot[r][t] = (!DUP && is4) ? (v >> 4) : v;
+        }
+    }
     const float kv0 = kav[0], kv1 = kav[1];
     load_k(mn);  // K registers are free again (past the end: no memory access)
     k_scales(e + NW);
@@ -484,58 +560,66 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     for (int r = 0; r < R; ++r) {
       const int q = qrow(r);
       const bool on = q < g && ((rowmask >> q) & 1u);
-      const float qs = is4 ? qsc4[q] : qsc[q];
+      const float qs4 = qsr4[r], qs8 = qsr8[r];
+      const float qs = is4 ? qs4 : qs8;
       trow[r] = -__builtin_inff();
 #pragma unroll
       for (int t = 0; t < NK; ++t) {
         const int kb = DUP ? half : t;
         ok[r][t] = on && (j * BN + kb * 32 + lq < prompt);
         slope[r][t] = qs * kavc[t];
-        if (ok[r][t]) trow[r] = fmaxf(trow[r], slope[r][t] * (float)dot[r][t]);
+        // The 16 lanes of a DPP row hold keys of one 16-key group, so one slope (>= 0): the row's
+        // largest scaled score is the slope times its largest integer dot product.
+        const int dm = row16_max_i(ok[r][t] ? dot[r][t] : INT_MIN);
+        if (dm != INT_MIN) trow[r] = fmaxf(trow[r], slope[r][t] * (float)dm);
       }
-      trow[r] = DUP ? wave_max(trow[r]) : half_max(trow[r], half);
+      trow[r] = DUP ? rows_max_wave(trow[r]) : rows_max_half(trow[r], half);
     }
     // ---- per-row scalars on the owner lane (common_device.cuh:222-238)
     const float levels = vf == 1 ? 255.f : 15.f;
-    float alpha_r[R], base_r[R], bq_r[R], restore_r[R];
+    float base_r[R], bq_r[R], restore_r[R];
+    bool moved_any;
+    float alpha = 1.f;
     {
       float tile_o = -__builtin_inff();
 #pragma unroll
       for (int r = 0; r < R; ++r) tile_o = (L & 3) == r ? trow[r] : tile_o;
-      const float qs_o = orow < g ? (is4 ? qsc4[orow] : qsc[orow]) : 1.17549435e-38f;
-      const float n = fmaxf(m_o, tile_o), alpha = texp2(m_o - n);
+      const float qs_o = is4 ? qs4_own : qs8_own;
+      // Reference max: the P levels are relative to the tile's own base and bq carries 2^(base - m),
+      // so m only scales acc and den alike; it moves when a tile's max exceeds it by more than 16
+      // (bq <= 2^(16 + margin)), and most tiles skip the rescale.
+      const float n = tile_o > m_o + 16.f ? tile_o : m_o;
+      moved_any = __any(n != m_o);
+      if (moved_any) alpha = texp2(m_o - n);
       m_o = n;
       const bool any = tile_o > -__builtin_inff();
       float base = any ? tile_o : n;
       base += __builtin_fmaf(qs_o * cur_kmax, 0.75f, fabsf(base) * 2.4e-7f);
-      const float bq = any ? texp2(base - n) / levels : 0.f;
+      // the reference divides by the level count under fast math; here: times its reciprocal
+      const float bq = any ? texp2(base - n) * (vf == 1 ? 1.f / 255.f : 1.f / 15.f) : 0.f;
       const float restore = vf == 1 ? bq : bq * (127.f / 7.f);
       // row q's scalars are in lane q (q < 4) or 32 + q - 4; every lane reads its rows' by readlane
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         if constexpr (DUP) {
-          alpha_r[r] = readlane_f(alpha, r);
           base_r[r] = readlane_f(base, r);
           bq_r[r] = readlane_f(bq, r);
           restore_r[r] = readlane_f(restore, r);
         } else {
-          alpha_r[r] = half ? readlane_f(alpha, 32 + r) : readlane_f(alpha, r);
           base_r[r] = half ? readlane_f(base, 32 + r) : readlane_f(base, r);
           bq_r[r] = half ? readlane_f(bq, 32 + r) : readlane_f(bq, r);
           restore_r[r] = half ? readlane_f(restore, 32 + r) : readlane_f(restore, r);
         }
       }
     }
-    const float (&alpha)[R] = alpha_r, (&base)[R] = base_r, (&bq)[R] = bq_r, (&restore)[R] = restore_r;
-    bool rescale = false;
-#pragma unroll
-    for (int r = 0; r < R; ++r) rescale |= alpha[r] != 1.f;
-    if (__any(rescale)) {
+    const float (&base)[R] = base_r, (&bq)[R] = bq_r, (&restore)[R] = restore_r;
+    if (moved_any) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        den[r] *= alpha[r];
+        const float al = DUP ? readlane_f(alpha, r) : (half ? readlane_f(alpha, 32 + r) : readlane_f(alpha, r));
+        den[r] *= al;
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[cb][r] *= alpha[r];
+        for (int cb = 0; cb < 4; ++cb) acc[cb][r] *= al;
       }
     }
     // ---- dithered P levels (common_device.cuh:239-246), transposed through LDS
@@ -546,14 +630,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
       for (int t = 0; t < NK; ++t) {
         const int kb = DUP ? half : t;
         const int d = dot[r][t];
-        float arg = -__builtin_inff();
-        uint32_t dith = 0x47400000u;
-        if (ok[r][t]) {
-          const float c = is4 ? -base[r] : (-slope[r][t] * MAGIC) - base[r];
-          arg = is4 ? __builtin_fmaf(slope[r][t], (float)d, c)
-                    : __builtin_fmaf(slope[r][t], __uint_as_float(MAGIC_BITS + (uint32_t)d), c);
-          dith |= (uint32_t)d & 0xffu;
-        }
+        // both forms of the score, selected by the tile's K width (selects, no branches): the
+        // 8-bit form is the reference's magic float 1.5*2^23 + d with the bias folded into c
+        const float x = is4 ? (float)d : __uint_as_float(MAGIC_BITS + (uint32_t)d);
+        const float c = is4 ? -base[r] : (-slope[r][t] * MAGIC) - base[r];
+        const float arg = ok[r][t] ? __builtin_fmaf(slope[r][t], x, c) : -__builtin_inff();
+        const uint32_t dith = 0x47400000u | (ok[r][t] ? (uint32_t)d & 0xffu : 0u);
         const uint32_t y = __float_as_uint(__builtin_fmaf(pexp2(arg), levels, __uint_as_float(dith)));
         const uint32_t p = (y >> 8) & 0xffu;
         psum += p;

@@ -107,11 +107,20 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int hg = 0; hg < 2; ++hg) {
-      float mx = score(kb, hg * 8);
+      if constexpr (KIND == KF16) {
+        float mx = score(kb, hg * 8);
 #pragma unroll
-      for (int r = 1; r < 8; ++r) mx = fmaxf(mx, score(kb, hg * 8 + r));
-      if (mx > -__builtin_inff()) {
-        const float d = KIND == KQ4 ? mx : mx - MAGIC;
+        for (int r = 1; r < 8; ++r) mx = fmaxf(mx, score(kb, hg * 8 + r));
+        if (mx > -__builtin_inff()) tile = fmaxf(tile, slope[kb * 2 + hg] * (mx - MAGIC));
+      } else {
+        // never masked: the group's largest integer accumulator (the magic-offset dot product, or
+        // 16 * dot), whose order is the scores' order, converted once
+        const int g0 = hg * 8;
+        int mx = max(max(s[kb][g0], s[kb][g0 + 1]), s[kb][g0 + 2]);
+        mx = max(max(mx, s[kb][g0 + 3]), s[kb][g0 + 4]);
+        mx = max(max(mx, s[kb][g0 + 5]), s[kb][g0 + 6]);
+        mx = max(mx, s[kb][g0 + 7]);
+        const float d = KIND == KQ4 ? (float)mx : (float)(mx - (int)MAGIC_BITS);
         tile = fmaxf(tile, slope[kb * 2 + hg] * d);
       }
     }
@@ -228,6 +237,21 @@ __device__ __forceinline__ void lds_copy_async(const uint8_t* src, uint8_t* dst)
     const int off = i * 2048 + wave * 1024;
     __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + off + lane),
                                      (__attribute__((address_space(3))) void*)(dst + off), 16, 0, 0);
+  }
+}
+
+// The same copy from a buffer resource at byte offset soff (uniform): the lane
+// offsets are constants, so no per-copy address arithmetic.
+template <int BYTES>
+__device__ __forceinline__ void lds_copy_buf(__amdgpu_buffer_rsrc_t src, int soff, uint8_t* dst) {
+  static_assert(BYTES % 2048 == 0, "copies move 2 KiB per step");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = (threadIdx.x & 63) * 16;
+#pragma unroll
+  for (int i = 0; i < BYTES / 2048; ++i) {
+    const int off = i * 2048 + wave * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (__attribute__((address_space(3))) void*)(dst + off), 16, lane,
+                                             soff + off, 0, 0);
   }
 }
 
@@ -525,11 +549,18 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
       if (row_ok) qs4 = a.qa4[qrow_idx] * a.sm_log2;
     }
     auto tile_col = [&](int i) { return i < n8 ? lo8 + i : lo4 + (i - n8); };
+    // the (sequence, KV head)'s record ranges as buffer resources: tile col at byte col * size
+    const __amdgpu_buffer_rsrc_t rk8 =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.k8 + rec0 * K8_BYTES), (short)0, tiles * K8_BYTES, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rk4 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.k4 ? a.k4 + rec0 * K4_BYTES : a.k8), (short)0, a.k4 ? tiles * K4_BYTES : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv8 =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.v8 + rec0 * V8_BYTES), (short)0, tiles * V8_BYTES, 0x00020000);
     auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd) {
       const int col = tile_col(i);
-      if (i < n8) lds_copy_async<K8_BYTES>(a.k8 + (rec0 + col) * K8_BYTES, kd);
-      else lds_copy_async<K4_BYTES>(a.k4 + (rec0 + col) * K4_BYTES, kd);
-      lds_copy_async<V8_BYTES>(a.v8 + (rec0 + col) * V8_BYTES, vd);
+      if (i < n8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd);
+      else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd);
+      lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd);
       // the scales ride along in the same kind of copy, so reading them later
       // waits on nothing but the records' own wait
       if (tid == 0)

@@ -48,7 +48,10 @@ struct DecodeArgs {
   const float* kstat;   // [B][Hk][3][128]: K mean (the frame of the merge's tail scores)
   const float* vstat;   // [B][Hk][3][128]: V mean, scale, 1/scale
   int kx_bytes;
-  int scatter;          // prime coprime to the grid size: workgroup lin takes work item lin * scatter mod grid
+  // work scatter: the grid is 1-D with `launched` = items | 1 workgroups (odd); workgroup lin takes work
+  // item lin * scatter mod launched (a permutation), and the one padding item (>= items) exits
+  int64_t scatter;
+  int items, launched;
   // split partition (extension): null for the reference's uniform split of `per` tiles, else
   // [B][Hk][splits + 1] entry bounds, split s of a head covering entries [bounds[s], bounds[s + 1])
   const int32_t* bounds;
@@ -220,15 +223,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   __shared__ __align__(16) float4 metk[MAX_PER + 1];   // per-tile K group scales
 
   // Workgroups are dealt to the 8 XCDs round-robin by linear id.  Work item w = lin * scatter mod
-  // grid scatters each head's splits over the XCDs and CUs: the last splits of a head hold its
-  // INT8-V tiles, and in a ragged batch the long sequences' splits would otherwise crowd the
-  // XCDs that receive them.  (Splits share no data but Q, so nothing is lost in L2.)
+  // launched spreads each head's splits over the XCDs and CUs (the host picks the multiplier, and a
+  // golden-ratio one with an odd launch count where a plain one would pin split indices to XCDs).
+  // Splits share no data but Q, so nothing is lost in L2.
   int split, kh, b;
   {
-    const int nsplit = gridDim.x, nkh = gridDim.y;
-    const int total = nsplit * nkh * gridDim.z;
-    const int lin = blockIdx.x + nsplit * (blockIdx.y + nkh * blockIdx.z);
-    const int w = (int)(((int64_t)lin * a.scatter) % total);
+    const int w = (int)(((int64_t)blockIdx.x * a.scatter) % a.launched);
+    if (w >= a.items) return;  // the padding item (whole workgroup, before any barrier)
+    const int nsplit = a.splits, nkh = a.hk;
     split = w % nsplit;
     kh = (w / nsplit) % nkh;
     b = w / (nsplit * nkh);

@@ -281,9 +281,10 @@ class DecodeCache:
         #   long as its costliest split, and balanced_partition cuts the heads by cost (C1:
         #   36.9 us vs 39.6 us for runs of 16 tiles).
         # - Above that (C3: 48.8k tiles), runs of `per` tiles, as the reference splits
-        #   (decode.py:54-55), over one wave of slots with every average head in at least 4
+        #   (decode.py:54-55), over one wave of slots with every average head in at least 3
         #   splits: the dispatcher then balances the waves itself, and no partition tried did
-        #   better (C3: 134 us at 24 tiles per split; balanced over 2560-8192 slots 134-141 us).
+        #   better (C3, two waves per workgroup: 121.5 us at 32 tiles per split, 127-128 at 24 or
+        #   36, 129 at 16, 134 at 64; balanced over 4096-8192 slots 138-168 us).
         # - self.per set: always runs of that many tiles.  At most 64 tiles per split.
         kept = sum(g["batch"] * int(g["meta"]["count"].sum()) for g in groups)
         if self.per is None and kept <= BALANCE_TILES * self.wave:
@@ -293,7 +294,7 @@ class DecodeCache:
             bounds = bounds_host.to(device)
         else:
             mean = kept / max(1, total * hk)
-            per = self.per or min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 4))))
+            per = self.per or min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 3))))
             bounds_host = bounds = None
             splits = max(1, -(-maxn // per))
         to = lambda x: x.to(torch.int32).to(device)

@@ -32,7 +32,10 @@ K8_WORDS, K4_WORDS = 2048, 1024
 KX_BYTES = 16384
 NEAR_V8 = 16
 SPLITS_PER_CU = 4  # decode workgroups per CU that the split partition targets
-TILE_COST = 8192   # per-tile cost of the split kernel beyond its record bytes (instruction stream), in bytes
+# Split-kernel time per kept tile by record kind (hundredths of a us; C1, one wave per SIMD, per-workgroup
+# timestamps): 133 for INT4 K and INT4 V, +20 for INT8 K, +43 for INT8 V (its 8 KiB record and P.V);
+# exact bf16 tiles (16 KiB K + 16 KiB V) are priced at 2.5x an INT4/INT4 tile.
+TILE_COST, K8_COST, V8_COST, EXACT_COST = 133, 20, 43, 333
 BALANCE_TILES = 16  # kept tiles per slot up to which the split partition is balanced by cost
 # entry words: bits 0-28 the tile index (decode.py:36); extension: bit 30 marks that bit 29 holds
 # the tile's V format (1 = INT8 V), which spares the decode kernel a dependent load of fmt
@@ -85,12 +88,12 @@ def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor, exact_kv
 
 
 def entry_costs(meta) -> np.ndarray:
-    """Cost of each kept entry of one sequence [Hk, maxn] (float64, 0 past the count): the bytes of
-    its K and V records plus TILE_COST."""
+    """Cost of each kept entry of one sequence [Hk, maxn] (float64, 0 past the count): the split
+    kernel's measured time per tile of its kind (TILE_COST, plus K8_COST for INT8 K and V8_COST for
+    INT8 V; EXACT_COST for an exact head's tile)."""
     exact = meta["exact"].numpy()[:, None]
-    kb = np.where(exact, KX_BYTES, np.where(meta["is4"].numpy(), 4096, 8192))
-    vb = np.where(exact, KX_BYTES, np.where(meta["vcode"].numpy() == I8, 8192, 4096))
-    return np.where(meta["valid"].numpy(), kb + vb + TILE_COST, 0).astype(np.float64)
+    quant = TILE_COST + np.where(meta["is4"].numpy(), 0, K8_COST) + np.where(meta["vcode"].numpy() == I8, V8_COST, 0)
+    return np.where(meta["valid"].numpy(), np.where(exact, EXACT_COST, quant), 0).astype(np.float64)
 
 
 def split_bounds(costs: np.ndarray, valid: np.ndarray, n: np.ndarray) -> np.ndarray:
@@ -111,7 +114,7 @@ def balanced_partition(metas, batches, slots: int):
 
     Extension (the reference splits every head into runs of one tile count, decode.py:54-55): the
     split kernel streams each split's records at about the same rate per wave, so its time is set
-    by the largest split.  Heads are cut by cost (record bytes, TILE_COST per tile) into
+    by the largest split.  Heads are cut by cost (the measured time of each tile's kind) into
     n_h = ceil(cost_h / t) runs of near-equal cost, with the smallest target t whose split count
     fits ``slots`` resident workgroups, at most 64 entries per split."""
     costs = [entry_costs(m) for m in metas]

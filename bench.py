@@ -8,7 +8,7 @@ token per sequence.  ``value`` = algorithmic HBM bytes of the step / step time
 resident in HBM; the timed ops alternate between two layers' caches so that the
 records stream from HBM rather than from the 256 MB Infinity Cache.  Also
 reported: tokens/s, the decode kernel's roofline
-(HIP events around that kernel inside the timed region), the CPU oracle timed
+(HIP events that the kernel's own launch records, inside the timed region), the CPU oracle timed
 on a bounded sample, prefill attention TOPS on configs[0] and configs[2] (C0, C2),
 and the ragged decode of configs[3] (C3).
 
@@ -76,6 +76,19 @@ def measured_traffic():
     return None
 
 
+def kernel_events(n, stream):
+    """n (start, stop) HIP event pairs for the split-KV kernel: the launch records them as the kernel's
+    own start and stop (hipExtLaunchKernel through tri_decode_partials_timed), so the timed loop holds
+    no event commands of its own.  Each event is recorded once here so that it exists."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for pair in evs:
+        for e in pair:
+            e.record(stream)
+    torch.cuda.synchronize()
+    return evs
+
+
 def copy_probe():
     import torch
     n = COPY_PROBE_BYTES // 4
@@ -119,15 +132,13 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
         cache.advance()
     out = torch.empty((batch, hq, 1, 128), dtype=torch.bfloat16, device=dev)
     plan = cache.plan(0, toks[0][0], toks[0][1], out, 128 ** -0.5)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    evs = kernel_events(steps, stream)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
     for i in range(steps):
         qd, kd, vd = toks[warmup + i]
-        evs[i][0].record(stream)
-        plan.run(qd, kd, vd, out, 1)
-        evs[i][1].record(stream)
+        plan.run(qd, kd, vd, out, 1, events=evs[i])
         plan.run(qd, kd, vd, out, 2)
         cache.advance()
     end.record(stream)
@@ -373,9 +384,7 @@ def main():
         if ev is None:
             plan.run(qd, kd, vd, out)
         else:
-            ev[0].record(stream)
-            plan.run(qd, kd, vd, out, 1)
-            ev[1].record(stream)
+            plan.run(qd, kd, vd, out, 1, events=ev)
             plan.run(qd, kd, vd, out, 2)
         if i % layers == layers - 1:
             cache.advance()
@@ -401,7 +410,7 @@ def main():
     log(f"warmup {args.warmup} steps")
     for i in range(1, 1 + args.warmup):
         step(i)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    evs = kernel_events(args.steps, stream)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     step0 = int(cache.step.item())

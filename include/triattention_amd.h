@@ -142,6 +142,23 @@ int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c,
                      const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
                      void* stream);
 
+/* Measurement (no reference counterpart): tri_decode_partials with the split-KV
+ * kernel launched through hipExtLaunchKernel, which records the two hipEvent_t
+ * handles (either may be null) as the kernel's own start and stop, so that a
+ * caller can time the kernel without event commands of its own in the stream. */
+int tri_decode_partials_timed(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c,
+                              const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
+                              const int32_t* count, const int32_t* fmt, const int32_t* slot, const void* v8c,
+                              const void* v4c, const float* vstat, const float* kstat, void* ktail, void* vtail,
+                              int64_t t_sb, int64_t t_sh, int64_t t_st, int max_tail, const void* kcur,
+                              const void* vcur, int64_t c_sb, int64_t c_sh, const int64_t* step, void* out,
+                              int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
+                              const int32_t* prompt, int batch, int hq, int hk, int maxn, int per,
+                              int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4,
+                              const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
+                              const int32_t* bounds, int nsplit, double scale, void* stream, void* ev_start,
+                              void* ev_stop);
+
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */
 int tri_decode_occupancy(int* blocks);

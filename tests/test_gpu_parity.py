@@ -229,6 +229,36 @@ def test_decode_entries_without_v_format_flags(module):
     assert torch.equal(flagged.view(torch.int32), plain.view(torch.int32))
 
 
+def test_timed_split_launch_matches_untimed(module):
+    """tri_decode_partials_timed (the split-KV kernel launched with its own start/stop events) followed
+    by the merge gives the untimed decode's outputs bit for bit, and the events hold a positive time."""
+    print("\n[parity] timed split-KV launch", flush=True)
+    hq, hk, prompt = 6, 2, 700
+    bands = torch.tensor(MIXED, dtype=torch.int32)
+    q, k, v = small(5800, 2, hq, hk, prompt)
+    cache = DecodeCache(module, max_tail=4)
+    cache.out_dtype = torch.float32
+    run_prefill(module, q, k, v, bands, 128 ** -0.5, decode_cache=cache)
+    g = S.gen(5801)
+    dev = torch.device("cuda")
+    qd, kd, vd = (S.outlier_tensor(g, 2, hq, 1).to(dev), S.outlier_tensor(g, 2, hk, 1).to(dev),
+                  S.outlier_tensor(g, 2, hk, 1).to(dev))
+    untimed = cache(0, qd, kd, vd, 128 ** -0.5).cpu()
+    out = torch.empty((2, hq, 1, 128), dtype=torch.float32, device=dev)
+    plan = cache.plan(0, qd, kd, out, 128 ** -0.5)
+    stream = torch.cuda.current_stream()
+    events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    for e in events:
+        e.record(stream)
+    plan.run(qd, kd, vd, out, 1, events=events)
+    plan.run(qd, kd, vd, out, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(untimed.view(torch.int32), out.cpu().view(torch.int32))
+    assert events[0].elapsed_time(events[1]) > 0.0
+    with pytest.raises(RuntimeError):
+        plan.run(qd, kd, vd, out, 3, events=events)
+
+
 def test_ragged_decode_batch(module):
     """Ragged cache: four prompts of different lengths stored by separate Prefill calls, served by one
     decode launch per step; every sequence matches the oracle."""

@@ -9,6 +9,8 @@
 #include <cstring>
 #include <string>
 
+#include <hip/hip_ext.h>
+
 #include "../../include/triattention_amd.h"
 #include "decode.hip"
 #include "prefill.hip"
@@ -41,14 +43,21 @@ bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) %
 
 // Quantized-head decode launch with NW waves per workgroup; groups of up to 4
 // q-heads use the DUP lane layout (both wave halves on rows 0..3).
+// With events, the launch goes through hipExtLaunchKernel, which records them as the kernel's
+// own start and stop.
+template <int NW, typename K>
+static void launch_one(K kernel, dim3 grid, const tri::DecodeArgs& d, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+  if (e0 || e1) hipExtLaunchKernelGGL(kernel, grid, dim3(64 * NW), 0, s, e0, e1, 0, d);
+  else kernel<<<grid, 64 * NW, 0, s>>>(d);
+}
 template <int NW>
-static void launch_decode(int g, dim3 grid, const tri::DecodeArgs& d, hipStream_t s) {
+static void launch_decode(int g, dim3 grid, const tri::DecodeArgs& d, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
   switch (g) {
-    case 1: tri::decode_kernel<1, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
-    case 2: tri::decode_kernel<2, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
-    case 3: tri::decode_kernel<3, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
-    case 4: tri::decode_kernel<4, false, true, NW><<<grid, 64 * NW, 0, s>>>(d); break;
-    default: tri::decode_kernel<4, false, false, NW><<<grid, 64 * NW, 0, s>>>(d); break;
+    case 1: launch_one<NW>(tri::decode_kernel<1, false, true, NW>, grid, d, s, e0, e1); break;
+    case 2: launch_one<NW>(tri::decode_kernel<2, false, true, NW>, grid, d, s, e0, e1); break;
+    case 3: launch_one<NW>(tri::decode_kernel<3, false, true, NW>, grid, d, s, e0, e1); break;
+    case 4: launch_one<NW>(tri::decode_kernel<4, false, true, NW>, grid, d, s, e0, e1); break;
+    default: launch_one<NW>(tri::decode_kernel<4, false, false, NW>, grid, d, s, e0, e1); break;
   }
 }
 
@@ -229,7 +238,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
                        const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
-                       void* stream, int phase) {
+                       void* stream, int phase, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr) {
   g_error.clear();
   if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
       !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
@@ -365,16 +374,16 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
       // better (C1: 37.4 us, against 39.3 us with two waves per workgroup).
       int cus = 0;
       if (device_cus(&cus) != 0) return 1;
-      if ((int64_t)d.items > 4 * (int64_t)cus) launch_decode<2>(g, grid, d, s);
-      else launch_decode<1>(g, grid, d, s);
+      if ((int64_t)d.items > 4 * (int64_t)cus) launch_decode<2>(g, grid, d, s, ev_start, ev_stop);
+      else launch_decode<1>(g, grid, d, s, ev_start, ev_stop);
     } else {
       // groups of up to 4 q-heads use the DUP lane layout (both wave halves on rows 0..3)
       switch (g) {
-        case 1: tri::decode_kernel<1, true, true><<<grid, 64, 0, s>>>(d); break;
-        case 2: tri::decode_kernel<2, true, true><<<grid, 64, 0, s>>>(d); break;
-        case 3: tri::decode_kernel<3, true, true><<<grid, 64, 0, s>>>(d); break;
-        case 4: tri::decode_kernel<4, true, true><<<grid, 64, 0, s>>>(d); break;
-        default: tri::decode_kernel<4, true, false><<<grid, 64, 0, s>>>(d); break;
+        case 1: launch_one<1>(tri::decode_kernel<1, true, true>, grid, d, s, ev_start, ev_stop); break;
+        case 2: launch_one<1>(tri::decode_kernel<2, true, true>, grid, d, s, ev_start, ev_stop); break;
+        case 3: launch_one<1>(tri::decode_kernel<3, true, true>, grid, d, s, ev_start, ev_stop); break;
+        case 4: launch_one<1>(tri::decode_kernel<4, true, true>, grid, d, s, ev_start, ev_stop); break;
+        default: launch_one<1>(tri::decode_kernel<4, true, false>, grid, d, s, ev_start, ev_stop); break;
       }
     }
   }
@@ -399,6 +408,9 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
 int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
 int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }
 int tri_decode_merge(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 2); }
+int tri_decode_partials_timed(TRI_DECODE_PARAMS, void* ev_start, void* ev_stop) {
+  return decode_impl(TRI_DECODE_ARGS, 1, static_cast<hipEvent_t>(ev_start), static_cast<hipEvent_t>(ev_stop));
+}
 
 int tri_decode_occupancy(int* blocks) {
   g_error.clear();

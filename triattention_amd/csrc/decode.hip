@@ -769,10 +769,11 @@ struct MergeArgs {
 // tails and more splits continue in loops.  Tail scores: 8 lanes per token (16
 // channels each); tail values: 16 lanes per token (8 channels each).
 __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
-  __shared__ float ts[MAX_TAIL];  // tail scores, then their weights texp2(score - m)
+  __shared__ float ts[MAX_TAIL];  // tail scores
   __shared__ float vo[16][D];     // tail value sums of the 16 token groups
   __shared__ float wo[4][D];      // split sums of the four waves
-  __shared__ float wred[4][3];    // per wave: max, split weight sum, tail weight sum
+  __shared__ float wred[4][2];    // per wave: max, split weight sum
+  __shared__ float ltg[16];       // tail weight sums of the 16 token groups
   int hq, b;
   {
     const int total = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
@@ -861,13 +862,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   if (lane == 0) wred[wave][0] = m;
   __syncthreads();
   m = fmaxf(fmaxf(wred[0][0], wred[1][0]), fmaxf(wred[2][0], wred[3][0]));
-  // tail weights, in place
-  float lt = 0.f;
-  for (int t = tid; t < tail; t += 256) {
-    const float e = texp2(ts[t] - m);
-    ts[t] = e;
-    lt += e;
-  }
   // split sums: wave w takes splits w, w + 4, ... in order
   float l = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
@@ -886,20 +880,17 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
     o0 = __builtin_fmaf(p.x, w, o0);
     o1 = __builtin_fmaf(p.y, w, o1);
   }
-#pragma unroll
-  for (int o = 32; o; o >>= 1) lt += __shfl_xor(lt, o, 64);
-  if (lane == 0) {
-    wred[wave][1] = l;
-    wred[wave][2] = lt;
-  }
+  if (lane == 0) wred[wave][1] = l;
   wo[wave][lane * 2] = o0;
   wo[wave][lane * 2 + 1] = o1;
-  __syncthreads();
-  // ---- tail values
+  // ---- tail values: each token's weight texp2(score - m) is computed by the 16 lanes that
+  // accumulate its values (no separate pass and barrier); lane 0 of the group sums the weights
   {
     float av[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float lt = 0.f;
     auto accum = [&](const uint4& raw, int t) {
-      const float e = t < tail ? ts[t] : 0.f;
+      const float e = t < tail ? texp2(ts[t] - m) : 0.f;
+      lt += e;
       const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) av[i] = __builtin_fmaf(e, bf16f((uint16_t)(w[i >> 1] >> (16 * (i & 1)))), av[i]);
@@ -918,6 +909,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) vo[vgrp][vc0 + i] = av[i];
+    if ((tid & 15) == 0) ltg[vgrp] = lt;
   }
   __syncthreads();
   if (tid >= D) return;
@@ -925,11 +917,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     lsum += wred[w][1];
-    tsum += wred[w][2];
     osum += wo[w][tid];
   }
 #pragma unroll
-  for (int grp = 0; grp < 16; ++grp) vsum += vo[grp][tid];
+  for (int grp = 0; grp < 16; ++grp) {
+    vsum += vo[grp][tid];
+    tsum += ltg[grp];
+  }
   const float acc = __builtin_fmaf(osum, vsv, lsum * vmv) + vsum;
   const float r = acc / (lsum + tsum);
   if (a.out_dtype == 0) static_cast<float*>(a.out)[b * a.osb + hq * a.osh + tid] = r;

@@ -36,7 +36,8 @@ STAT_BLOCKS = 64
 K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
-           "tri_decode_partials", "tri_decode_merge", "tri_decode_occupancy", "tri_device_cus")
+           "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_occupancy",
+           "tri_device_cus")
 KX_BYTES = 16384
 
 
@@ -65,6 +66,7 @@ def load_library() -> ctypes.CDLL:
                    P, P, P, I64, P, I, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
         getattr(lib, name).argtypes = decode_args
+    lib.tri_decode_partials_timed.argtypes = decode_args + [P, P]
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:
@@ -300,7 +302,10 @@ class DecodePlan:
         self.device = q.device
         self.fns = {3: module.lib.tri_decode, 1: module.lib.tri_decode_partials, 2: module.lib.tri_decode_merge}
 
-    def run(self, q, kcur, vcur, out, phase=3):
+    def run(self, q, kcur, vcur, out, phase=3, events=None):
+        """Launch ``phase`` (3: both kernels, 1: the split-KV kernel, 2: the merge).  ``events`` (phase 1
+        only): a pair of recorded torch.cuda.Event objects that the split-KV kernel's launch records as
+        its own start and stop (``tri_decode_partials_timed``)."""
         if _geometry(q) != self.qgeom or _geometry(kcur) != self.cgeom or _geometry(vcur) != self.cgeom or \
                 _geometry(out) != self.ogeom:
             raise RuntimeError("decode plan: q / k / v / out differ in shape, strides, dtype or device from the plan")
@@ -308,11 +313,16 @@ class DecodePlan:
         a[self.Q], a[self.KC], a[self.VC], a[self.OUT] = q.data_ptr(), kcur.data_ptr(), vcur.data_ptr(), out.data_ptr()
         index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         a[self.STREAM] = torch.cuda.current_stream(index).cuda_stream
+        fn, extra = self.fns[phase], ()
+        if events is not None:
+            if phase != 1:
+                raise RuntimeError("decode plan: events time the split-KV kernel (phase 1) only")
+            fn, extra = self.module.lib.tri_decode_partials_timed, tuple(e.cuda_event for e in events)
         if torch.cuda.current_device() != index:
             with torch.cuda.device(index):
-                self.module._call(self.fns[phase], *a)
+                self.module._call(fn, *a, *extra)
         else:
-            self.module._call(self.fns[phase], *a)
+            self.module._call(fn, *a, *extra)
         return out
 
 

@@ -161,21 +161,13 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
 def c4_config():
     """C4 model, prompt and map: random-init Qwen2-7B shape, 4096 random
     prompt ids, a seeded per-(layer, KV head) draw over INT8 / INT4 / bf16."""
-    import torch
     import transformers
 
-    from triattention_amd.maps import INF, from_bands
+    from triattention_amd import synthetic as S
+    from triattention_amd.maps import from_bands
 
-    cfg = transformers.Qwen2Config(vocab_size=152064, hidden_size=3584, intermediate_size=18944,
-                                   num_hidden_layers=28, num_attention_heads=28, num_key_value_heads=4,
-                                   max_position_embeddings=32768, rope_theta=1e6, initializer_range=0.02,
-                                   tie_word_embeddings=False)
-    g = torch.Generator().manual_seed(1004)
-    ids = torch.randint(152064, (1, 4096), generator=g)
-    kinds = torch.randint(3, (28, 4), generator=g)  # 0 INT8, 1 INT4, 2 bf16
-    band = {0: [INF, INF], 1: [1, INF], 2: [INF, INF]}
-    bands = {str(l): [band[int(kinds[l, h // 7])] for h in range(28)] for l in range(28)}
-    bf16 = {str(l): [h for h in range(4) if int(kinds[l, h]) == 2] for l in range(28)}
+    kw, ids, bands, bf16, kinds = S.config4()
+    cfg = transformers.Qwen2Config(**kw)
     mixed = from_bands(bands, bf16=bf16)
     exact = from_bands(bands, bf16={str(l): [0, 1, 2, 3] for l in range(28)})
     share = {name: float((kinds == i).float().mean()) for i, name in enumerate(("int8", "int4", "bf16"))}

@@ -66,6 +66,13 @@ def lib():
         L.ora_decode_vfmt.argtypes = [I, I]
         L.ora_decode.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I, P]
         L.ora_num_threads.restype = I
+        L.ora_set_mutation.argtypes = [I]
+        L.ora_prefill_rows.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, P, I64, P, I]
+        L.ora_prefill_trace.restype = I
+        L.ora_prefill_trace.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, I, I, I, P, P, P, P, P, P, P]
+        L.ora_decode_trace.restype = I
+        L.ora_decode_trace.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I,
+                                       I, I, P, P, P, P, P, P, P, P, P, P, P]
         _lib = L
     return _lib
 
@@ -201,8 +208,9 @@ def decode_vcodes(rows: int):
 # --------------------------------------------------------------------- prefill
 def prefill_codes(q_bits, k_bits, v_bits, bands, decode_cache: bool = False):
     """The operand preparation of one Prefill call (kernels/prefill.py:87-101):
-    which formats exist, the V identity rule, and every code/scale array."""
-    hq, t, _ = q_bits.shape
+    which formats exist, the V identity rule, and every code/scale array.
+    ``q_bits`` may be None (the Q codes are then omitted: a decode needs only K and V)."""
+    t = k_bits.shape[1]
     rows = (t + BN - 1) // BN
     formats = formats_for(bands, rows)
     int4 = Q4 in formats
@@ -210,7 +218,7 @@ def prefill_codes(q_bits, k_bits, v_bits, bands, decode_cache: bool = False):
         formats |= set(decode_vcodes(rows).tolist())
     want8 = I8 in formats or int4
     want4 = I4 in formats
-    q8, qa, q4, qa4 = quantize_q(q_bits, int4)
+    q8, qa, q4, qa4 = quantize_q(q_bits, int4) if q_bits is not None else (None,) * 4
     _, kstat = stats(k_bits)
     k8, ka, k4, ka4 = quantize_k(k_bits, kstat, int4)
     identity = not want8 and not want4
@@ -229,6 +237,45 @@ def prefill_attention(codes, bands, hq: int, hk: int, t: int, scale: float, thre
                       _p(codes["qa4"]), _p(codes["k8"]), _p(codes["ka"]), _p(codes["k4"]), _p(codes["ka4"]),
                       _p(codes["v16"]), _p(v8), _p(codes["vstat"]), _p(out), int(threads))
     return out
+
+
+def _prefill_operands(codes, bands, hq, scale):
+    b = _c(bands, np.int32).reshape(hq, 2)
+    v8 = codes["v8"] if codes["v8"] is not None else np.zeros((1,), np.int8)
+    return (_p(b), sm_log2(scale), _p(codes["q8"]), _p(codes["qa"]), _p(codes["q4"]), _p(codes["qa4"]),
+            _p(codes["k8"]), _p(codes["ka"]), _p(codes["k4"]), _p(codes["ka4"]), _p(codes["v16"]), _p(v8),
+            _p(codes["vstat"])), (b, v8)
+
+
+def prefill_rows(codes, bands, hq: int, hk: int, t: int, scale: float, rows, threads: int = 0):
+    """Rows ``rows`` (flat q-head * t + token indices) of ``prefill_attention``'s output, [len(rows), 128]."""
+    rows = _c(rows, np.int64).reshape(-1)
+    out = np.empty((rows.size, D), np.float32)
+    args, keep = _prefill_operands(codes, bands, hq, scale)
+    lib().ora_prefill_rows(hq, hk, t, *args, _p(rows), rows.size, _p(out), int(threads))
+    return out
+
+
+def prefill_trace(codes, bands, hq: int, hk: int, t: int, scale: float, qh: int, i: int):
+    """One output row with its per-tile record: dict(col, kind, m, base, bq, p [tiles, 64], out)."""
+    cap = (t + BN - 1) // BN + 2
+    col, kind = np.zeros(cap, np.int32), np.zeros(cap, np.int32)
+    m, base, bq = np.zeros(cap, np.float32), np.zeros(cap, np.float32), np.zeros(cap, np.float32)
+    p = np.zeros((cap, BN), np.int32)
+    out = np.zeros(D, np.float32)
+    args, keep = _prefill_operands(codes, bands, hq, scale)
+    n = lib().ora_prefill_trace(hq, hk, t, *args, int(qh), int(i), cap, _p(col), _p(kind), _p(m), _p(base), _p(bq),
+                                _p(p), _p(out))
+    return dict(col=col[:n], kind=kind[:n], m=m[:n], base=base[:n], bq=bq[:n], p=p[:n], out=out)
+
+
+def set_mutation(value: int) -> None:
+    """Plant one of the oracle's test mistakes (0 = none); only the tests of the oracle's pins use it."""
+    lib().ora_set_mutation(int(value))
+
+
+MUTATIONS = dict(no_margin=1, no_half=2, dither_byte=3, no_rel_margin=4, bq_levels=5, v4_restore=6, no_dither=7,
+                 slope_group=8)
 
 
 def prefill(q_bits, k_bits, v_bits, bands, scale: float, decode_cache: bool = False, threads: int = 0):
@@ -272,6 +319,44 @@ def decode(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vtail, k
                      _p(_c(kcur, np.uint16)), _p(_c(vcur, np.uint16)), int(step),
                      None if bounds is None else _p(bounds), int(nsplit), _p(out))
     return out
+
+
+def decode_trace(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vtail, kcur, vcur, step: int,
+                 qh: int):
+    """``decode`` for q-head ``qh`` with its record: per kept tile (split order) col, kind (K width 8/4 |
+    V format << 4), split, m, base, bq, p [tiles, 64]; the split partials pm, pl, po [splits, 128]; out."""
+    if np.ndim(per) == 0:
+        bounds, nsplit, per = None, 0, int(per)
+        splits = None
+    else:
+        bounds = _c(per, np.int32)
+        nsplit, per = bounds.shape[1] - 1, 1
+        splits = nsplit
+    hq = q_bits.shape[0]
+    b = _c(bands, np.int32).reshape(hq, 2)
+    tiles = (int(prompt) + BN - 1) // BN
+    cap = max(1, tiles)
+    if splits is None:
+        splits = max(1, -(-tiles // per))
+    col, kind, split = np.zeros(cap, np.int32), np.zeros(cap, np.int32), np.zeros(cap, np.int32)
+    m, base, bq = np.zeros(cap, np.float32), np.zeros(cap, np.float32), np.zeros(cap, np.float32)
+    p = np.zeros((cap, BN), np.int32)
+    pm, pl, po = np.zeros(splits, np.float32), np.zeros(splits, np.float32), np.zeros((splits, D), np.float32)
+    out = np.zeros(D, np.float32)
+    ktail, vtail = _c(ktail, np.uint16), _c(vtail, np.uint16)
+    dummy = np.zeros((1,), np.int8)
+    v4 = codes["v4"] if codes["v4"] is not None else dummy
+    v8 = codes["v8"] if codes["v8"] is not None else dummy
+    q = _c(q_bits, np.uint16)
+    kc, vc = _c(kcur, np.uint16), _c(vcur, np.uint16)
+    n = lib().ora_decode_trace(hq, codes["kstat"].shape[0], int(prompt), _p(b), int(per), sm_log2(scale), _p(q),
+                               _p(codes["k8"]), _p(codes["ka"]), _p(codes["k4"]), _p(codes["ka4"]), _p(v8), _p(v4),
+                               _p(codes["vstat"]), _p(codes["kstat"]), _p(ktail), _p(vtail), int(ktail.shape[1]),
+                               _p(kc), _p(vc), int(step), None if bounds is None else _p(bounds), int(nsplit),
+                               int(qh), cap, _p(col), _p(kind), _p(split), _p(m), _p(base), _p(bq), _p(p), _p(pm),
+                               _p(pl), _p(po), _p(out))
+    return dict(col=col[:n], kind=kind[:n], split=split[:n], m=m[:n], base=base[:n], bq=bq[:n], p=p[:n], pm=pm,
+                pl=pl, po=po, out=out)
 
 
 def num_threads() -> int:

@@ -319,11 +319,56 @@ int ora_band_tiles(int w8, int w4, int qb, int* cols, int* kind) {
   return n;
 }
 
-static inline float tile_base_margin(float slope, float base) { return fmaf(slope, 0.75f, fabsf(base) * 2.4e-7f); }
+/* Planted mistakes for the tests of the oracle's own pins (never set outside those tests): each
+ * value replaces one step of the quantized-P rules by a plausible wrong form, so that a test can show
+ * that its independent check detects it.  0 = the reference's rules. */
+enum {
+  MUT_NONE = 0,
+  MUT_NO_MARGIN = 1,     /* base = tile max, no margin */
+  MUT_NO_HALF = 2,       /* prefill P levels: floor(x) instead of floor(x + 0.5) */
+  MUT_DITHER_BYTE = 3,   /* decode dither from bits 8-15 of the dot product, not bits 0-7 */
+  MUT_NO_REL_MARGIN = 4, /* margin without its |base| * 2.4e-7 term */
+  MUT_BQ_LEVELS = 5,     /* bq = 2^(base - m) / 256 instead of / levels */
+  MUT_V4_RESTORE = 6,    /* INT4-V tiles weighted by bq, without the 127/7 restore */
+  MUT_NO_DITHER = 7,     /* decode P levels without the dither (plain truncation) */
+  MUT_SLOPE_GROUP = 8,   /* P-level arguments all use the first 16-key group's slope */
+};
+static int g_mutation = MUT_NONE;
+void ora_set_mutation(int m) { g_mutation = m; }
+
+static inline float tile_base_margin(float slope, float base) {
+  if (g_mutation == MUT_NO_MARGIN) return 0.f;
+  if (g_mutation == MUT_NO_REL_MARGIN) return slope * 0.75f;
+  return fmaf(slope, 0.75f, fabsf(base) * 2.4e-7f);
+}
 
 /* P level of one key: byte 1 of fma(e, levels, dither) (prefill_sm80.cu:398-403,
  * common_device.cuh:243-244). */
 static inline int p_level(float e, float levels, float dither) { return (int)((fbits(fmaf(e, levels, dither)) >> 8) & 0xffu); }
+
+static inline float pmagic_half(void) { return g_mutation == MUT_NO_HALF ? 49152.0f : PMAGIC_HALF; }
+static inline float level_scale(float levels) { return g_mutation == MUT_BQ_LEVELS ? 256.f : levels; }
+
+/* Per-tile record of one query row (prefill) or one q-head (decode), for the tests that check the
+ * oracle's quantized-P rules tile by tile against an independent float64 evaluation. */
+typedef struct {
+  int cap, n;
+  int32_t *col, *kind, *split;
+  float *m, *base, *bq;
+  int32_t* p; /* [cap][64]: P levels (quantized tiles) or the fp16 bits of p (F16 tiles) */
+} ora_trace;
+
+static void trace_tile(ora_trace* tr, int col, int kind, int split, float m, float base, float bq, const int* p) {
+  if (!tr || tr->n >= tr->cap) return;
+  const int e = tr->n++;
+  tr->col[e] = col;
+  tr->kind[e] = kind;
+  if (tr->split) tr->split[e] = split;
+  tr->m[e] = m;
+  tr->base[e] = base;
+  tr->bq[e] = bq;
+  for (int k = 0; k < BN; ++k) tr->p[(int64_t)e * BN + k] = p[k];
+}
 
 /* ------------------------------------------------------------- prefill */
 /* One query row of run_task (prefill_sm80.cu:259-488), exact-accumulator form.
@@ -339,7 +384,7 @@ typedef struct {
   const uint16_t* v16;
 } prefill_args;
 
-static void prefill_row(const prefill_args* a, int qh, int i, float* out_row) {
+static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, ora_trace* tr) {
   const int g = a->hq / a->hk, kh = qh / g, tiles = (a->t + BN - 1) / BN, qb = i / BN;
   const int64_t qrow = (int64_t)qh * a->t + i;
   int cols[4096], kind[4096];
@@ -401,6 +446,11 @@ static void prefill_row(const prefill_args* a, int qh, int i, float* out_row) {
         p16[k] = ora_f32_to_f16(ora_texp2(arg));
         pf[k] = ora_f16_to_f32(p16[k]);
       }
+      if (tr) {
+        int pb[BN];
+        for (int k = 0; k < BN; ++k) pb[k] = p16[k];
+        trace_tile(tr, col, 0, 0, m, 0.f, 0.f, pb);
+      }
       for (int kc16 = 0; kc16 < 4; ++kc16) {
         double s = 0.0;
         for (int k = kc16 * 16; k < kc16 * 16 + 16; ++k) s += (double)pf[k];
@@ -418,17 +468,19 @@ static void prefill_row(const prefill_args* a, int qh, int i, float* out_row) {
       float ksmax = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
       float base = tile > -INFINITY ? tile : m;
       base += tile_base_margin(qs * ksmax, base);
-      const float bq = ora_texp2(base - m) / 255.f;
+      const float bq = ora_texp2(base - m) / level_scale(255.f);
       int P[BN];
       int rs = 0;
       for (int k = 0; k < BN; ++k) {
         const float x = valid[k] ? (float)dot[k] : -INFINITY;
+        const float sl = g_mutation == MUT_SLOPE_GROUP ? slope[0] : slope[k / 16];
         float arg;
-        if (four) arg = fmaf(slope[k / 16], x, -base);
-        else arg = fmaf(slope[k / 16], x + MAGIC_F, fmaf(-slope[k / 16], MAGIC_F, -base));
-        P[k] = p_level(ora_texp2(arg), 255.f, PMAGIC_HALF);
+        if (four) arg = fmaf(sl, x, -base);
+        else arg = fmaf(sl, x + MAGIC_F, fmaf(-sl, MAGIC_F, -base));
+        P[k] = p_level(ora_texp2(arg), 255.f, pmagic_half());
         rs += P[k];
       }
+      trace_tile(tr, col, kd, 0, m, base, bq, P);
       denom = fmaf((float)rs, bq, denom * alpha);
       const int8_t* vt = a->v8 + ((int64_t)kh * tiles + col) * BN * D;
       int32_t pv[D];
@@ -457,9 +509,38 @@ void ora_prefill(int hq, int hk, int t, const int32_t* bands, float sm_log2, con
 #endif
   for (int64_t r = 0; r < (int64_t)hq * t; ++r) {
     const int qh = (int)(r / t), i = (int)(r % t);
-    prefill_row(&a, qh, i, out + r * D);
+    prefill_row(&a, qh, i, out + r * D, NULL);
   }
   (void)nthreads;
+}
+
+/* The rows rows[0..nrows) (flat index qh * t + i) of ora_prefill's output, into out [nrows][128]:
+ * every row is computed on its own, so a sample of a long prompt costs only its rows. */
+void ora_prefill_rows(int hq, int hk, int t, const int32_t* bands, float sm_log2, const int8_t* q8, const float* qa,
+                      const uint8_t* q4, const float* qa4, const int8_t* k8, const float* ka, const int8_t* k4,
+                      const float* ka4, const uint16_t* v16, const int8_t* v8, const float* vstat,
+                      const int64_t* rows, int64_t nrows, float* out, int nthreads) {
+  prefill_args a = {hq, hk, t, bands, sm_log2, q8, k8, k4, v8, q4, qa, ka, qa4, ka4, vstat, v16};
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+  for (int64_t r = 0; r < nrows; ++r) prefill_row(&a, (int)(rows[r] / t), (int)(rows[r] % t), out + r * D, NULL);
+  (void)nthreads;
+}
+
+/* One row of ora_prefill with its per-tile record (visit order): tile, kind (0 F16, 1 I8, 2 Q4),
+ * running max after the tile, base and bq (quantized tiles), and per key the P level or the fp16
+ * bits of p.  Returns the number of visited tiles (at most cap are recorded). */
+int ora_prefill_trace(int hq, int hk, int t, const int32_t* bands, float sm_log2, const int8_t* q8, const float* qa,
+                      const uint8_t* q4, const float* qa4, const int8_t* k8, const float* ka, const int8_t* k4,
+                      const float* ka4, const uint16_t* v16, const int8_t* v8, const float* vstat, int qh, int i,
+                      int cap, int32_t* col, int32_t* kind, float* m, float* base, float* bq, int32_t* p,
+                      float* out_row) {
+  prefill_args a = {hq, hk, t, bands, sm_log2, q8, k8, k4, v8, q4, qa, ka, qa4, ka4, vstat, v16};
+  ora_trace tr = {cap, 0, col, kind, NULL, m, base, bq, p};
+  prefill_row(&a, qh, i, out_row, &tr);
+  return tr.n;
 }
 
 /* --------------------------------------------------------------- decode */
@@ -506,7 +587,8 @@ typedef struct {
 } decode_args;
 
 /* One query head of decode_kernel + decode_merge_kernel. */
-static void decode_head(const decode_args* a, int qh, float* out_row) {
+static void decode_head(const decode_args* a, int qh, float* out_row, ora_trace* tr, float* tpm, float* tpl,
+                        float* tpo) {
   const int g = a->hq / a->hk, kh = qh / g, tiles = (a->prompt + BN - 1) / BN;
   /* kept-tile list of this KV head: ascending tiles whose group state > 0 */
   int* entry = (int*)malloc(sizeof(int) * (tiles > 0 ? tiles : 1));
@@ -604,13 +686,15 @@ static void decode_head(const decode_args* a, int qh, float* out_row) {
       const int any = tile > -INFINITY;
       float base = any ? tile : nmax;
       base += tile_base_margin(slope1, base);
-      const float bq = any ? ora_texp2(base - nmax) / levels : 0.f;
-      const float restore = fmt == 1 ? bq : bq * (127.f / 7.f);
+      const float bq = any ? ora_texp2(base - nmax) / level_scale(levels) : 0.f;
+      const float restore = (fmt == 1 || g_mutation == MUT_V4_RESTORE) ? bq : bq * (127.f / 7.f);
       int P[BN];
       for (int k = 0; k < BN; ++k) {
-        const int w = k / 16;
+        const int w = g_mutation == MUT_SLOPE_GROUP ? 0 : k / 16;
         const float xm = valid[k] ? (float)dot[k] + MAGIC_F : -INFINITY;
-        const float dither = bitsf((fbits(xm) & 0xffu) | 0x47400000u);
+        float dither = bitsf((fbits(xm) & 0xffu) | 0x47400000u);
+        if (g_mutation == MUT_DITHER_BYTE) dither = bitsf(((fbits(xm) >> 8) & 0xffu) | 0x47400000u);
+        if (g_mutation == MUT_NO_DITHER) dither = 49152.0f;
         float arg;
         if (!four) {
           const float bias = -slope[w] * MAGIC_F;
@@ -620,6 +704,7 @@ static void decode_head(const decode_args* a, int qh, float* out_row) {
         }
         P[k] = p_level(ora_texp2(arg), levels, dither);
       }
+      trace_tile(tr, j, kprec[e] | fmt << 4, s, m, base, bq, P);
       /* denominators per 16-key group, as 4 lanes x 4 keys with a butterfly
        * (common_device.cuh:246-251) */
       for (int w = 0; w < 4; ++w) {
@@ -644,6 +729,11 @@ static void decode_head(const decode_args* a, int qh, float* out_row) {
     pm[s] = m;
     pl[s] = dw[0] + dw[1] + dw[2] + dw[3];
     for (int c = 0; c < D; ++c) po[(int64_t)s * D + c] = out[c];
+  }
+  if (tpm) {
+    memcpy(tpm, pm, sizeof(float) * splits);
+    memcpy(tpl, pl, sizeof(float) * splits);
+    memcpy(tpo, po, sizeof(float) * splits * D);
   }
 
   /* merge (common_device.cuh:373-469) */
@@ -692,7 +782,23 @@ void ora_decode(int hq, int hk, int prompt, const int32_t* bands, int per, float
                 const int32_t* bounds, int nsplit, float* out) {
   decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, bounds, nsplit < 1 ? 1 : nsplit, bands, sm_log2,
                    q, k8, k4, v8, v4, ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
-  for (int qh = 0; qh < hq; ++qh) decode_head(&a, qh, out + (int64_t)qh * D);
+  for (int qh = 0; qh < hq; ++qh) decode_head(&a, qh, out + (int64_t)qh * D, NULL, NULL, NULL, NULL);
+}
+
+/* ora_decode for one q-head with its record: per kept tile (split order) the tile, kprec | fmt << 4,
+ * split, running max after the tile, base, bq and the 64 P levels; the split partials pm / pl
+ * [splits] and po [splits][128]; returns the number of tiles visited (at most cap recorded). */
+int ora_decode_trace(int hq, int hk, int prompt, const int32_t* bands, int per, float sm_log2, const uint16_t* q,
+                     const int8_t* k8, const float* ka, const int8_t* k4, const float* ka4, const int8_t* v8,
+                     const int8_t* v4, const float* vstat, const float* kstat, const uint16_t* ktail,
+                     const uint16_t* vtail, int max_tail, const uint16_t* kcur, const uint16_t* vcur, int64_t step,
+                     const int32_t* bounds, int nsplit, int qh, int cap, int32_t* col, int32_t* kind, int32_t* split,
+                     float* m, float* base, float* bq, int32_t* p, float* pm, float* pl, float* po, float* out_row) {
+  decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, bounds, nsplit < 1 ? 1 : nsplit, bands, sm_log2,
+                   q, k8, k4, v8, v4, ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
+  ora_trace tr = {cap, 0, col, kind, split, m, base, bq, p};
+  decode_head(&a, qh, out_row, &tr, pm, pl, po);
+  return tr.n;
 }
 
 int ora_num_threads(void) {

@@ -300,3 +300,67 @@ def test_every_head_exact_keeps_one_placeholder_record_per_kind():
     assert e["v"][I8].shape == (1, 2048) and e["v"][I4].shape == (1, 1024)
     assert e["xslot"].tolist() == [[0, tiles]]
     assert e["count"].tolist() == [[tiles, tiles]]
+
+
+def test_ragged_store_keeps_each_groups_scales_and_statistics():
+    """A Prefill hands the cache the same scale/statistics buffers for every call of one shape
+    (two prompts of 150 and 190 tokens both have 3 tiles).  Each stored group must keep the values
+    it was given, not whatever a later call wrote into the shared buffers."""
+    cache = DecodeCache(FakeModule(), max_tail=8)
+    cache.ragged = True
+    hk, bands = 2, torch.tensor([[1, INF], [1, INF], [2, 4], [1, 1]], dtype=torch.int32)
+    tiles, batch = 3, 1
+    z32 = lambda n: torch.zeros(n, dtype=torch.int32).to(torch.uint32)
+    ka, ka4 = torch.empty(batch * hk * tiles * 4), torch.empty(batch * hk * tiles * 4)
+    kstat, vstat = torch.empty(batch * hk * 3 * 128), torch.empty(batch, hk, 3, 128)
+    codes, _ = cache.codes(tiles)
+    for prompt in (150, 190):
+        for buf in (ka, ka4, kstat, vstat):
+            buf.fill_(float(prompt))  # "statistics" of this prompt, written into the shared buffers
+        packed = {F16: None, I8: z32(batch * hk * tiles * 2048), I4: z32(batch * hk * tiles * 1024)}
+        cache.store(0, prompt, z32(batch * hk * tiles * 2048), ka, kstat, vstat, packed, codes, bands,
+                    z32(batch * hk * tiles * 1024), ka4)
+    e = cache.layers[0]
+    for row, prompt in enumerate((150, 190)):
+        for name in ("ka", "ka4", "kstat", "vstat"):
+            assert bool((e[name][row] == float(prompt)).all()), (name, row)
+
+
+def _decode_plan_tensors(b=2, hq=4, hk=2, maxn=3, tiles=3, max_tail=8, splits=2):
+    i32 = lambda *s: torch.zeros(*s, dtype=torch.int32)
+    f32 = lambda *s: torch.zeros(*s, dtype=torch.float32)
+    bf = lambda *s: torch.zeros(*s, dtype=torch.bfloat16)
+    u32 = lambda *s: torch.zeros(*s, dtype=torch.int32).to(torch.uint32)
+    return dict(q=bf(b, hq, 1, 128), k8c=u32(4, 2048), k4c=u32(4, 1024), ka=f32(b * hk * tiles * 4),
+                ka4=f32(b * hk * tiles * 4), entry=i32(b, hk, maxn), kinfo=i32(b, hk, maxn), count=i32(b, hk),
+                fmt=i32(b, tiles), slot=i32(b, hk, maxn), v8=u32(4, 2048), v4=u32(4, 1024), vstat=f32(b, hk, 3, 128),
+                kstat=f32(b, hk, 3, 128), ktail=bf(b, hk, max_tail, 128), vtail=bf(b, hk, max_tail, 128),
+                kcur=bf(b, hk, 1, 128), vcur=bf(b, hk, 1, 128), step=torch.zeros(1, dtype=torch.int64),
+                out=f32(b, hq, 1, 128), pm=f32(b * hq * splits), pl=f32(b * hq * splits),
+                po=f32(b * hq * splits * 128), prompt=i32(b), per=2, scale=128 ** -0.5)
+
+
+@pytest.mark.parametrize("bad, message", [
+    (dict(out=torch.zeros(1, 4, 1, 128)), "out must be"),
+    (dict(kcur=torch.zeros(2, 1, 1, 128, dtype=torch.bfloat16), vcur=torch.zeros(2, 1, 1, 128, dtype=torch.bfloat16)),
+     "new token must be bf16"),
+    (dict(kcur=torch.zeros(2, 2, 1, 128), vcur=torch.zeros(2, 2, 1, 128)), "new token must be bf16"),
+    (dict(ktail=torch.zeros(2, 2, 4, 128, dtype=torch.bfloat16)), "tails must be"),
+    (dict(vtail=torch.zeros(2, 2, 8, 128)), "tails must be"),
+    (dict(vtail=torch.zeros(2, 2, 16, 128, dtype=torch.bfloat16)[:, :, ::2]), "tails must be"),
+    (dict(pl=torch.zeros(3)), "split partials"),
+    (dict(po=torch.zeros(8)), "split partials"),
+    (dict(fmt=torch.zeros(5, dtype=torch.int32)), "fmt"),
+    (dict(prompt=torch.zeros(3, dtype=torch.int32)), "prompt length"),
+    (dict(count=torch.zeros(2, 3, dtype=torch.int32)), "decode geometry/buffers"),
+    (dict(step=torch.zeros(1, dtype=torch.int32)), "decode geometry/buffers"),
+    ({}, "on q's device"),  # every shape right: the CPU tensors themselves are refused
+])
+def test_plan_decode_rejects_mismatched_buffers(bad, message):
+    """The merge kernel writes out / ktail / vtail and reads kcur / vcur at sequence and head offsets
+    derived from q's shape, so the plan refuses any of them that does not span that shape."""
+    from triattention_amd.kernels.extension import Module, load_library
+    args = _decode_plan_tensors()
+    args.update(bad)
+    with pytest.raises(RuntimeError, match=message):
+        Module(load_library()).plan_decode(**args)

@@ -184,8 +184,12 @@ class DecodeCache:
                          if bool(meta["is4"].any()) else None),
                      v={code: (packed[code].view(batch * hk * tiles, WORDS[code]).index_select(0, pick(code))
                                if bool(meta["vsel"][code].any()) else None) for code in (I8, I4)},
-                     ka=ka.view(batch, hk, tiles, 4), ka4=ka4.view(batch, hk, tiles, 4) if ka4 is not None else None,
-                     kstat=kstat.view(batch, hk, 3, 128), vstat=vstat.view(batch, hk, 3, 128), exact=exact_kv,
+                     # copies, not views: the Prefill reuses these buffers for its next call with the
+                     # same shape, and a ragged cache re-reads every stored group
+                     ka=ka.view(batch, hk, tiles, 4).clone(),
+                     ka4=ka4.view(batch, hk, tiles, 4).clone() if ka4 is not None else None,
+                     kstat=kstat.view(batch, hk, 3, 128).clone(), vstat=vstat.view(batch, hk, 3, 128).clone(),
+                     exact=exact_kv,
                      kx=kx.reshape(-1)[:nbytes].clone() if exact_kv else None,
                      vx=vx.reshape(-1)[:nbytes].clone() if exact_kv else None)
         if self.step is None:

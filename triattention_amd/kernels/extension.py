@@ -248,17 +248,40 @@ class Module:
                    vxc is not None and kxc.numel() * kxc.element_size() % KX_BYTES == 0 and
                    kxc.numel() * kxc.element_size() == vxc.numel() * vxc.element_size(), "exact heads: xslot / KX / VX")
         _check(_geometry(vcur) == _geometry(kcur), "decode: k and v of the new token must have the same shape and strides")
-        _check(step.dtype == torch.int64 and step.is_cuda and kcur.stride(3) == 1 and
+        # the merge kernel writes out, ktail and vtail at sequence / head offsets and reads kcur / vcur
+        # the same way: every one of them must span the whole [B, H, ., 128] it addresses
+        _check(kcur.dtype == torch.bfloat16 and kcur.dim() == 4 and tuple(kcur.shape) == (b, hk, 1, D),
+               "decode: k / v of the new token must be bf16 [B,Hk,1,128]")
+        _check(ktail.dtype == torch.bfloat16 and ktail.dim() == 4 and tuple(ktail.shape) == (b, hk, max_tail, D) and
+               ktail.stride(3) == 1 and _geometry(vtail) == _geometry(ktail),
+               "decode: tails must be bf16 [B,Hk,max_tail,128], K and V alike")
+        _check(out.dim() == 4 and tuple(out.shape) == (b, hq, 1, D), "decode: out must be [B,Hq,1,128]")
+        _check(prompt_t.numel() == b and prompt_t.dtype == torch.int32, "decode: one int32 prompt length per sequence")
+        _check(fmt.numel() % b == 0 and tiles_max >= 1, "decode: fmt [B, tiles]")
+        _check(pm.dtype == pl.dtype == po.dtype == torch.float32 and pm.numel() >= b * hq * splits and
+               pl.numel() >= b * hq * splits and po.numel() >= b * hq * splits * D,
+               "decode: split partials pm / pl [B*Hq*splits], po [B*Hq*splits*128] (fp32)")
+        _check(ka.dtype == torch.float32 and (ka4 is None or ka4.dtype == torch.float32) and
+               vstat.dtype == kstat.dtype == torch.float32 and vstat.numel() == b * hk * 3 * D,
+               "decode: K scales and statistics (fp32)")
+        _check(step.dtype == torch.int64 and step.numel() >= 1 and
                entry.dtype == torch.int32 and kinfo.dtype == torch.int32 and count.dtype == torch.int32 and
-               slot.dtype == torch.int32 and fmt.dtype == torch.int32 and prompt_t.dtype == torch.int32 and
+               slot.dtype == torch.int32 and fmt.dtype == torch.int32 and
                entry.numel() == b * hk * maxn and kinfo.numel() == entry.numel() and slot.numel() == entry.numel() and
                count.numel() == b * hk and ka.numel() == b * hk * tiles_max * 4 and
                k8c.dim() == 2 and k8c.size(1) == K8_WORDS and v8.dim() == 2 and v8.size(1) == V8_WORDS and
                v4.dim() == 2 and v4.size(1) == V4_WORDS and (k4c is None) == (ka4 is None) and
                (k4c is None or (k4c.dim() == 2 and k4c.size(1) == K4_WORDS and ka4.numel() == ka.numel())) and
-               pm.numel() >= b * hq * splits and po.numel() >= b * hq * splits * D and
                out.dtype in (torch.bfloat16, torch.float32) and out.stride(3) == 1,
                "decode geometry/buffers")
+        for name, t in (("q", q), ("k", kcur), ("tail", ktail), ("out", out), ("step", step), ("prompt", prompt_t),
+                        ("entry", entry), ("kinfo", kinfo), ("slot", slot), ("count", count), ("fmt", fmt),
+                        ("ka", ka), ("ka4", ka4), ("vstat", vstat), ("kstat", kstat), ("pm", pm), ("pl", pl),
+                        ("po", po), ("k8", k8c), ("k4", k4c), ("v8", v8), ("v4", v4)):
+            contiguous = name in ("q", "k", "tail", "out") or t is None or t.is_contiguous()
+            _check(t is None or (t.is_cuda and t.device == q.device and contiguous),
+                   f"decode: {name} must be a{'' if name in ('q', 'k', 'tail', 'out') else ' contiguous'} tensor "
+                   f"on q's device")
         kc = kcur.view(b, hk, -1, D) if kcur.dim() == 4 else kcur
         args = [0, q.stride(0), q.stride(1), _ptr(k8c), _ptr(k4c), _ptr(ka),
                 _ptr(ka4), _ptr(entry), _ptr(kinfo), _ptr(count), _ptr(fmt), _ptr(slot), _ptr(v8), _ptr(v4),

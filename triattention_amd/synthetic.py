@@ -8,10 +8,13 @@ device, so CPU and GPU runs see identical bits.
       bands: a seeded half of the KV heads INT8 (INF, INF), the rest INT4 (1, INF).
   C1  decode B32, Hq24/Hk8, prompt 4096: K/V as C0, 25% INT8 / 75% INT4 KV heads.
   C2  prefill B4, Hq28/Hk4, T8192: per (tensor, head, channel) scale exp(U(0, ln 30));
-      one seeded KV head bf16, the others INT8 or INT4 with p = 0.5.
+      one seeded KV head bf16; of the others, in a seeded order, one INT8, one INT4 and the
+      rest INT8 or INT4 with p = 0.5.
   C3  ragged decode B64, Hq32/Hk8: prompt lengths round(exp(U(ln 512, ln 32768))),
       per-KV-head Bernoulli(0.5) INT8 / INT4.  At full size its prompt K/V are drawn on
-      the device (``outlier_tensor_device``); the parity tests use host draws.
+      the device (``outlier_tensor_device``); the parity tests copy those draws to the host.
+  C4  random-init Qwen2-7B architecture (``config4``): 4096 random prompt ids, a seeded
+      per-(layer, KV head) draw over INT8 / INT4 / bf16.
 """
 from __future__ import annotations
 
@@ -92,8 +95,13 @@ def config2(seed: int = 1002, batch: int = 4, t: int = 8192, hq: int = 28, hk: i
     k = loguniform_scaled_tensor(g, batch, hk, t)
     v = loguniform_scaled_tensor(g, batch, hk, t)
     bf16_head = int(torch.randint(hk, (1,), generator=g))
-    kinds = ["i8" if float(torch.rand(1, generator=g)) < 0.5 else "i4" for _ in range(hk)]
-    kinds[bf16_head] = "bf16"
+    # the other KV heads split 50/50 between INT8 and INT4: a seeded order of them, the first INT8, the
+    # second INT4 (so both kinds always occur), any further ones Bernoulli(0.5)
+    rest = [h for h in range(hk) if h != bf16_head]
+    rest = [rest[i] for i in torch.randperm(len(rest), generator=g).tolist()]
+    kinds = ["bf16"] * hk
+    for n, h in enumerate(rest):
+        kinds[h] = "i8" if n == 0 else "i4" if n == 1 else ("i8" if float(torch.rand(1, generator=g)) < 0.5 else "i4")
     return dict(q=q, k=k, v=v, kinds=kinds, bands=kv_head_bands(kinds, hq // hk), scale=128 ** -0.5)
 
 
@@ -140,3 +148,19 @@ def bits(x: torch.Tensor):
     """uint16 numpy view of a bf16 CPU tensor."""
     import numpy as np
     return x.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def config4(seed: int = 1004, prompt: int = 4096):
+    """C4 model configuration (keyword arguments of transformers.Qwen2Config), prompt ids [1, prompt], and
+    the map: per (layer, KV head) a uniform draw over INT8 / INT4 / bf16 -> (bands by layer, bf16 KV heads
+    by layer, kinds [28, 4] with 0 INT8, 1 INT4, 2 bf16)."""
+    cfg = dict(vocab_size=152064, hidden_size=3584, intermediate_size=18944, num_hidden_layers=28,
+               num_attention_heads=28, num_key_value_heads=4, max_position_embeddings=32768, rope_theta=1e6,
+               initializer_range=0.02, tie_word_embeddings=False)
+    g = gen(seed)
+    ids = torch.randint(152064, (1, prompt), generator=g)
+    kinds = torch.randint(3, (28, 4), generator=g)
+    band = {0: [INF, INF], 1: [1, INF], 2: [INF, INF]}
+    bands = {str(l): [band[int(kinds[l, h // 7])] for h in range(28)] for l in range(28)}
+    bf16 = {str(l): [h for h in range(4) if int(kinds[l, h]) == 2] for l in range(28)}
+    return cfg, ids, bands, bf16, kinds

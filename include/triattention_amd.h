@@ -159,6 +159,25 @@ int tri_decode_partials_timed(const void* q, int64_t q_sb, int64_t q_sh, const v
                               const int32_t* bounds, int nsplit, double scale, void* stream, void* ev_start,
                               void* ev_stop);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): tri_decode with the split
+ * partials pm / pl / po held in a scratch array inside the library (24 MiB of fp32 per GPU, held until
+ * the process ends) instead of caller buffers; every other argument as for tri_decode, and the
+ * same kernels.  Calls whose batch x hq x splits partials do not fit (more than 48,395) are rejected
+ * with an error.  No memory is allocated or freed.  Every call on one GPU shares that GPU's scratch
+ * (each call writes every partial it reads), so calls that overlap on one GPU, e.g. on two streams,
+ * race. */
+int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
+                       const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
+                       const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
+                       const float* kstat, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh, int64_t t_st,
+                       int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh,
+                       const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh,
+                       const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
+                       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
+                       const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
+                       double scale, void* stream);
+
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */
 int tri_decode_occupancy(int* blocks);

@@ -76,3 +76,16 @@ def test_oracle_library_loads():
 def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_noalloc_decode_rejects_partials_beyond_its_scratch():
+    """batch x q-heads x splits partials beyond the library's scratch are refused before any device
+    work (64 x 32 x 64 = 131072 > 48395)."""
+    lib = load_library()
+    fake = ctypes.c_void_p(4096)
+    args = list(_decode_args(fake, per=1))
+    del args[31:34]
+    # batch, hq, hk, maxn, per sit right after prompt (index 31 once pm / pl / po are gone)
+    args[32], args[33], args[34], args[35], args[36] = 64, 32, 8, 64, 1
+    assert lib.tri_decode_noalloc(*args) != 0
+    assert b"exceed" in lib.tri_last_error() and b"48395" in lib.tri_last_error()

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include <hip/hip_ext.h>
@@ -391,6 +392,32 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   return check_launch("decode");
 }
 
+// ---- decode without allocation (tri_decode_noalloc)
+// The split partials pm, pl, po of one call live in this file-scope device array: one copy per GPU,
+// held until the process ends.  Host code never passes `scratch` itself (its host-side name is not a
+// device address); it passes the address hipGetSymbolAddress returns, taken once per device.
+constexpr int64_t NOALLOC_FLOATS = (int64_t)24 << 18;  // 24 MiB of fp32
+static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
+
+static int noalloc_scratch(float** out) {
+  static std::mutex mu;
+  static float* ptrs[64] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail("decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail("decode_noalloc: device %d beyond the 64 this library tracks", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail("decode_noalloc: hipGetSymbolAddress of the scratch array: %s", hipGetErrorString(e));
+    ptrs[dev] = static_cast<float*>(p);
+  }
+  *out = ptrs[dev];
+  return 0;
+}
+
 #define TRI_DECODE_ARGS                                                                                      \
   q, q_sb, q_sh, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8c, v4c, vstat, kstat, ktail, vtail, t_sb, t_sh, \
       t_st, max_tail, kcur, vcur, c_sb, c_sh, step, out, out_dtype, o_sb, o_sh, pm, pl, po, prompt, batch, hq, hk,  \
@@ -410,6 +437,40 @@ int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS,
 int tri_decode_merge(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 2); }
 int tri_decode_partials_timed(TRI_DECODE_PARAMS, void* ev_start, void* ev_stop) {
   return decode_impl(TRI_DECODE_ARGS, 1, static_cast<hipEvent_t>(ev_start), static_cast<hipEvent_t>(ev_stop));
+}
+
+int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
+                       const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
+                       const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
+                       const float* kstat, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh, int64_t t_st,
+                       int max_tail, const void* kcur, const void* vcur, int64_t c_sb, int64_t c_sh,
+                       const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh,
+                       const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
+                       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
+                       const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
+                       double scale, void* stream) {
+  g_error.clear();
+  if (batch < 1 || hq < 1 || hk < 1 || maxn < 1) return fail("decode_noalloc: empty shape");
+  if (!bounds && (per < 1 || per > tri::MAX_PER)) return fail("decode_noalloc: per (tiles per split) must be in [1, 64]");
+  if (bounds && (nsplit < 1 || nsplit > 65535)) return fail("decode_noalloc: nsplit must be in [1, 65535]");
+  const int64_t splits = bounds ? nsplit : std::max(1, (maxn + per - 1) / per);
+  // split partials: (m, l) and o[128] each; pl and po start on 256-byte boundaries
+  auto floats = [](int64_t n) { return 2 * ((n + 63) / 64 * 64) + n * tri::D; };
+  const int64_t n = (int64_t)batch * hq * splits;
+  const int64_t pad = (n + 63) / 64 * 64;
+  if (floats(n) > NOALLOC_FLOATS) {
+    int64_t most = NOALLOC_FLOATS / (tri::D + 2);
+    while (floats(most + 1) <= NOALLOC_FLOATS) ++most;
+    return fail("decode_noalloc: %lld split partials (batch %d x q-heads %d x splits %lld) exceed the %lld-float "
+                "scratch (at most %lld); use tri_decode with caller buffers",
+                (long long)n, batch, hq, (long long)splits, (long long)NOALLOC_FLOATS, (long long)most);
+  }
+  float* s = nullptr;
+  if (noalloc_scratch(&s) != 0) return 1;
+  float* pm = s;
+  float* pl = s + pad;
+  float* po = s + 2 * pad;
+  return decode_impl(TRI_DECODE_ARGS, 3);
 }
 
 int tri_decode_occupancy(int* blocks) {

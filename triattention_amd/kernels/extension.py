@@ -36,8 +36,8 @@ STAT_BLOCKS = 64
 K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
-           "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_occupancy",
-           "tri_device_cus")
+           "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_noalloc",
+           "tri_decode_occupancy", "tri_device_cus")
 KX_BYTES = 16384
 
 
@@ -67,6 +67,8 @@ def load_library() -> ctypes.CDLL:
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
         getattr(lib, name).argtypes = decode_args
     lib.tri_decode_partials_timed.argtypes = decode_args + [P, P]
+    # tri_decode without pm / pl / po (arguments 31-33 of tri_decode)
+    lib.tri_decode_noalloc.argtypes = decode_args[:31] + decode_args[34:]
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:

@@ -44,6 +44,14 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_threads():
+    """Host threads for the CPU baseline: every core this process may use (OMP_NUM_THREADS caps it where
+    the host shares its cores)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(cap)) if cap and cap.isdigit() else n)
+
+
 def decode_record_bytes(cache_entry):
     """Algorithmic record bytes of one decode step: for every kept (sequence, KV head, tile),
     its K record (8 or 4 KiB), its V record (8 or 4 KiB) and 16 B of group scales."""
@@ -174,9 +182,11 @@ def c4_config():
     return cfg, ids, mixed, exact, share
 
 
-def c4_e2e(args):
-    """C4: greedy generation of 256 tokens after a 4096-token prompt through TriAttention, on the mixed
-    map and, for comparison, with every KV head exact (bf16) on the same kernels."""
+def c4_runs(which=("mixed", "mixed_eager", "all_bf16"), reps=2):
+    """C4: greedy generation of 256 tokens after a 4096-token prompt through TriAttention on the model
+    of configs[4], per run: "mixed" (the map, the one-token forward replayed as a HIP graph),
+    "mixed_eager" (the same without the graph), "all_bf16" (every KV head exact, graph).  The last of
+    ``reps`` repetitions is reported (the first also builds the per-layer plans and buffers)."""
     import torch
     import transformers
 
@@ -192,9 +202,11 @@ def c4_e2e(args):
     ids = ids.to(dev)
     new = 256
     runs = {}
-    for name, fn, graph in (("mixed", mixed, True), ("mixed_eager", mixed, False), ("all_bf16", exact, True)):
+    maps = {"mixed": (mixed, True), "mixed_eager": (mixed, False), "all_bf16": (exact, True)}
+    for name in which:
+        fn, graph = maps[name]
         tri = TriAttention(model, fn, max_new_tokens=new)
-        for rep in range(2):  # the first run also builds the per-layer plans and buffers
+        for rep in range(reps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             with torch.inference_mode():
@@ -225,27 +237,37 @@ def c4_e2e(args):
                       "generate_tokens_per_s": round(new / (t2 - t0), 2), "hip_graph": graph,
                       "tokens_head": tokens[:8]}
         log(f"C4 {name}: prefill {runs[name]['prefill_ms']} ms, decode {runs[name]['decode_tokens_per_s']} tokens/s")
-    assert runs["mixed"]["tokens_head"] == runs["mixed_eager"]["tokens_head"], "graph replay changed the tokens"
+        del tri
+    if "mixed" in runs and "mixed_eager" in runs:
+        assert runs["mixed"]["tokens_head"] == runs["mixed_eager"]["tokens_head"], "graph replay changed the tokens"
+    del model
+    torch.cuda.empty_cache()
+    workload = ("C4 e2e: Qwen2-7B architecture (28 layers, hidden 3584, Hq 28 / Hk 4, FFN 18944, vocab 152064, "
+                "rope 1e6), prompt 4096 + 256 greedy steps, batch 1, HF modules without the HF KV cache (the "
+                "decode cache holds K/V)")
+    return runs, share, new, workload
+
+
+def c4_e2e(args):
+    runs, share, new, workload = c4_runs()
     result = {
         "metric": "C4 end-to-end greedy decode tokens/s (prefill time reported separately)",
         "value": runs["mixed"]["decode_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": new,
         "warmup": 1, "ms_per_step": round(runs["mixed"]["decode_s"] / (new - 1) * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 model; int8/int4/bf16 attention per map",
         "data": "synthetic (random-init weights N(0, 0.02), 4096 random prompt ids, seed 1004)",
-        "config": {"workload": "C4 e2e: Qwen2-7B architecture (28 layers, hidden 3584, Hq 28 / Hk 4, FFN 18944, "
-                               "vocab 152064, rope 1e6), prompt 4096 + 256 greedy steps, batch 1, HF modules "
-                               "without the HF KV cache (the decode cache holds K/V); value: the one-token "
-                               "forward replayed as a HIP graph (mixed_eager: the same without it)",
+        "config": {"workload": workload + "; value: the one-token forward replayed as a HIP graph (mixed_eager: "
+                               "the same without it)",
                    "map_share": share, "global_batch": 1, "seq_len": 4096, "parallelism": "single GPU"},
         "runs": runs,
     }
     print(json.dumps(result))
 
 
-def calibration_sweep(args):
+def calibration_run():
     """configs-adjacent consumer measurement (calibrate.py:44-64): every distance-band configuration of
     the calibration grid as its own Prefill executor, all sharing one scratch dict, over one
-    Qwen2-7B-shape attention layer (B 1, Hq 28 / Hk 4, T 4096).  Reports the sweep's time."""
+    Qwen2-7B-shape attention layer (B 1, Hq 28 / Hk 4, T 4096).  Returns the sweep's time and sizes."""
     import torch
 
     from triattention_amd import synthetic as S
@@ -279,15 +301,21 @@ def calibration_sweep(args):
     sweep_ms = (time.perf_counter() - t0) / reps * 1e3
     scratch = sum(b.numel() * b.element_size() for b in shared.values())
     log(f"calibration sweep: {len(grid)} executors, {sweep_ms:.1f} ms per sweep, shared scratch {scratch / 2**20:.1f} MiB")
+    return {"sweep_ms": round(sweep_ms, 3), "executors": len(grid), "per_executor_ms": round(sweep_ms / len(grid), 4),
+            "shared_scratch_bytes": scratch, "reps": reps,
+            "workload": f"calibrate.py pattern: {len(grid)} Prefill executors with uniform bands sharing one scratch "
+                        "dict, one Qwen2-7B-shape layer (B 1, Hq 28 / Hk 4, T 4096)"}
+
+
+def calibration_sweep(args):
+    r = calibration_run()
     print(json.dumps({
         "metric": "calibration sweep time (all band configurations of one layer, shared scratch)",
-        "value": round(sweep_ms, 3), "unit": "ms", "n_gpus": 1, "steps": reps, "warmup": 1,
-        "ms_per_step": round(sweep_ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "value": r["sweep_ms"], "unit": "ms", "n_gpus": 1, "steps": r["reps"], "warmup": 1,
+        "ms_per_step": r["sweep_ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8/int4 codes, fp32 softmax", "data": "synthetic (device-drawn N(0,1) with outlier channels)",
-        "config": {"workload": f"calibrate.py pattern: {len(grid)} Prefill executors with uniform bands sharing one "
-                               "scratch dict, one Qwen2-7B-shape layer (B 1, Hq 28 / Hk 4, T 4096)",
-                   "executors": len(grid), "per_executor_ms": round(sweep_ms / len(grid), 4),
-                   "shared_scratch_bytes": scratch, "parallelism": "single GPU"}}))
+        "config": {"workload": r["workload"], "executors": r["executors"], "per_executor_ms": r["per_executor_ms"],
+                   "shared_scratch_bytes": r["shared_scratch_bytes"], "parallelism": "single GPU"}}))
 
 
 def main():
@@ -297,9 +325,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--cpu-seqs", type=int, default=8)
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--no-c3", action="store_true")
+    ap.add_argument("--no-c4", action="store_true", help="leave out the C4 generation from the default run")
+    ap.add_argument("--no-calibrate", action="store_true", help="leave out the calibration sweep from the default run")
     ap.add_argument("--c4", action="store_true", help="run the C4 end-to-end generation instead")
     ap.add_argument("--calibrate", action="store_true", help="time the calibration sweep's Prefill executors instead")
     args = ap.parse_args()
@@ -448,38 +477,37 @@ def main():
     }
 
     # ------------------------------------------------------------- CPU baseline
+    threads = cpu_threads()
     if not args.no_cpu:
         import oracle as O
-        ns = min(args.cpu_seqs, batch)
-        log(f"CPU oracle: codes for {ns} sequences")
-        qd, kd, vd = toks[0]
-        sample = []
-        for b in range(ns):
-            s = c1["seqs"][b]
-            codes = O.prefill_codes(S.bits(s["q"][0]), S.bits(s["k"][0]), S.bits(s["v"][0]), bands.numpy(),
-                                    decode_cache=True)
-            sample.append(codes)
+        from concurrent.futures import ThreadPoolExecutor
+        bn = bands.numpy()
+        log(f"CPU oracle: K/V codes of the {batch} sequences ({threads} threads)")
+        qd, kd, vd = (x.cpu() for x in toks[0])
         zeros = np.zeros((hk, 256, 128), np.uint16)
-        qb, kb, vb = qd.cpu(), kd.cpu(), vd.cpu()
-        times, errs = [], []
-        for rep in range(3):
-            t0 = time.perf_counter()
-            outs = [O.decode(sample[b], bands.numpy(), S.bits(qb[b, :, 0]), prompt, cache.split_of(0, b), scale, zeros, zeros,
-                             S.bits(kb[b, :, 0]), S.bits(vb[b, :, 0]), 0) for b in range(ns)]
-            times.append(time.perf_counter() - t0)
-        for b in range(ns):
-            # GPU step-0 output is bf16; compare within one bf16 ulp of the rounded oracle value
-            ref = torch.from_numpy(outs[b]).to(torch.bfloat16).float()
-            errs.append(float((out0[b, :, 0] - ref).abs().max()))
-        per_seq = statistics.median(times) / ns
-        cpu_step = per_seq * batch
+        # one sequence per task; the oracle's C calls release the GIL, so the pool runs them in parallel
+        with ThreadPoolExecutor(threads) as pool:
+            codes = list(pool.map(lambda b: O.prefill_codes(None, S.bits(c1["seqs"][b]["k"][0]),
+                                                            S.bits(c1["seqs"][b]["v"][0]), bn, decode_cache=True),
+                                  range(batch)))
+            one = lambda b: O.decode(codes[b], bn, S.bits(qd[b, :, 0]), prompt, cache.split_of(0, b), scale, zeros,
+                                     zeros, S.bits(kd[b, :, 0]), S.bits(vd[b, :, 0]), 0)
+            times = []
+            for rep in range(3):
+                t0 = time.perf_counter()
+                outs = list(pool.map(one, range(batch)))
+                times.append(time.perf_counter() - t0)
+        # GPU step-0 output is bf16: compare within one bf16 ulp of the rounded oracle value
+        errs = [float((out0[b, :, 0] - torch.from_numpy(outs[b]).to(torch.bfloat16).float()).abs().max())
+                for b in range(batch)]
+        cpu_step = statistics.median(times)
         result["cpu_baseline"] = {
-            "value": round(step_bytes / cpu_step / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle decode (C, 1 thread) of {ns} of the {batch} sequences at step 0, median of 3, "
-                      f"scaled to the full step",
+            "value": round(step_bytes / cpu_step / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the C oracle's decode of all {batch} sequences at step 0 (the whole C1 step, no "
+                      f"extrapolation), one sequence per task on {threads} threads, median of 3",
             "ms_per_step": round(cpu_step * 1e3, 2), "tokens_per_s": round(batch / cpu_step, 2),
             "host_cpu_count": os.cpu_count()}
-        result["parity_spot_check"] = {"sequences": ns, "max_abs_vs_oracle_bf16": max(errs)}
+        result["parity_spot_check"] = {"sequences": batch, "max_abs_vs_oracle_bf16": max(errs)}
 
     # ----------------------------------------------------------------- prefill
     if not args.no_prefill:
@@ -540,6 +568,22 @@ def main():
         c0["kinds"] = []
         r0 = prefill_case("C0", c0, 20)
         r0["workload"] = "C0 prefill: batch 1, Hq 24 / Hk 8, T 1024, 50/50 INT8/INT4 KV heads"
+        if not args.no_cpu:
+            import oracle as O
+            # the same unit on the host: one whole Prefill call (codes, statistics, records and the
+            # attention) of C0 by the C oracle, its attention rows on every thread, median of 3
+            times = []
+            for rep in range(3):
+                t0 = time.perf_counter()
+                O.prefill(S.bits(c0["q"][0]), S.bits(c0["k"][0]), S.bits(c0["v"][0]), c0["bands"].numpy(),
+                          c0["scale"], threads=threads)
+                times.append(time.perf_counter() - t0)
+            cpu_ms = statistics.median(times) * 1e3
+            result.setdefault("cpu_baseline", {})["prefill_C0"] = {
+                "ms_per_call": round(cpu_ms, 2), "tokens_per_s": round(1024 / (cpu_ms * 1e-3), 1),
+                "int8_tops": round(r0["algorithmic_ops"] / (cpu_ms * 1e-3) / 1e12, 4), "threads": threads,
+                "gpu_speedup_full_call": round(cpu_ms * 1e3 / r0["prefill_call_us"], 1)}
+            log(f"CPU oracle C0 prefill: {cpu_ms:.1f} ms per call ({threads} threads)")
         log("prefill C2 (generating 4 x 8192 tokens)")
         c2 = S.config2()
         r2 = prefill_case("C2", c2, 5)
@@ -550,6 +594,16 @@ def main():
     # ------------------------------------------------------- C3 ragged decode
     if not args.no_c3:
         result["c3_decode"] = c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands)
+
+    # ------------------------------------------- calibration consumer, C4 end to end
+    if not args.no_calibrate:
+        result["calibration"] = calibration_run()
+    if not args.no_c4:
+        del cache, plans, toks
+        torch.cuda.empty_cache()
+        runs, share, new, workload = c4_runs(("mixed",), reps=2)
+        result["c4_e2e"] = dict(runs["mixed"], workload=workload + "; the one-token forward replayed as a HIP graph",
+                                map_share=share, steps=new)
 
     print(json.dumps(result))
 

@@ -412,21 +412,28 @@ def test_config2_shape_slice(module):
 
 
 def test_shared_scratch_executors(module):
-    """Calibration's pattern (calibrate.py:44-48): many Prefill executors with different uniform bands
-    share one scratch dict; each must return what an executor with its own scratch returns."""
+    """Calibration's pattern (calibrate.py:44-64): many Prefill executors with different uniform bands
+    share one scratch dict and run one after another on the same layer inputs.  Each must match the
+    oracle for its own bands, and return exactly what an executor with its own scratch returns."""
     print("\n[parity] shared-scratch Prefill executors", flush=True)
     from triattention_amd.maps import uniform
-    q, k, v = small(6100, 1, 6, 2, 300)
+    hq, hk, t = 6, 2, 300
+    qh, kh, vh = small(6100, 1, hq, hk, t)
     dev = torch.device("cuda")
-    q, k, v = q.to(dev), k.to(dev), v.to(dev)
-    configs = [(1, 2), (2, 8), (INF, INF), (1, INF), (4, 4), (16, INF)]
+    q, k, v = qh.to(dev), kh.to(dev), vh.to(dev)
+    # a slice of calibrate.py:14-19's grid: sink/diagonal only, short and long INT8 bands, INT4 bands, all INT8
+    configs = [(1, 1), (1, 2), (2, 8), (INF, INF), (1, INF), (4, 4), (16, INF), (2, 2048)]
     shared = {}
     outs = []
     for w8, w4 in configs:
         pre = Prefill(module, uniform(w8, w4), out_dtype=torch.float32)
         pre.buffers = shared
         outs.append(pre(0, q, k, v, 128 ** -0.5).clone())
-    # a second pass over the same executors, then fresh executors with their own scratch
+    for (w8, w4), got in zip(configs, outs):
+        bands = torch.tensor([[w8, w4]] * hq, dtype=torch.int32)
+        ref, _ = oracle_prefill(qh, kh, vh, bands, 128 ** -0.5)
+        assert_close(got.cpu().numpy(), ref, what=f"executor ({w8}, {w4}) with shared scratch")
+    # fresh executors with their own scratch return the same bits
     for (w8, w4), first in zip(configs, outs):
         alone = Prefill(module, uniform(w8, w4), out_dtype=torch.float32)(0, q, k, v, 128 ** -0.5)
         assert torch.equal(first, alone), (w8, w4)

@@ -1,9 +1,9 @@
 """Hugging Face integration: the attention hook, prefill/decode dispatch and
 greedy generation on the gfx950 kernels.
 
-Mirrors triattention/models.py (load_tokenizer :15-18, load_model :21-32,
-render_prompt :35-37, eos_ids :40-42, exact_attention :45-47, use_attention
-:50-55, TriAttention :58-85) with the same names, arguments and behaviour:
+Mirrors the attention half of triattention/models.py (exact_attention :45-47,
+use_attention :50-55, TriAttention :58-85) with the same names, arguments and
+behaviour:
 
 * a model's attention calls go to ``Prefill`` for a prompt and to
   ``DecodeCache`` for a one-token query of a layer whose prompt is stored;
@@ -18,7 +18,10 @@ fp32 accumulation.
 
 Extensions: ``TriAttention`` accepts a map path or a ``bands_fn`` (as built by
 ``triattention_amd.maps``), and an optional ``module`` (the loaded extension).
-Model loaders read local paths only.
+
+Loading checkpoints and tokenizers, chat templates and end-of-sequence ids
+(models.py:16-42) are the caller's: any HF causal LM whose attention modules
+call the registered attention function can be handed to ``TriAttention``.
 """
 from __future__ import annotations
 
@@ -28,44 +31,6 @@ from .kernels.decode import DecodeCache
 from .kernels.extension import load_extension
 from .kernels.prefill import Prefill
 from .maps import INF, load_map, preset
-
-
-def load_tokenizer(path):
-    """Tokenizer of a local model directory (models.py:15-18)."""
-    from transformers import AutoConfig, AutoTokenizer
-
-    mistral = AutoConfig.from_pretrained(path).model_type == "mistral3"
-    return AutoTokenizer.from_pretrained(path, **({"fix_mistral_regex": True} if mistral else {}))
-
-
-def load_model(path):
-    """bf16 causal LM from a local model directory, on the GPU, in eval mode (models.py:21-32).
-
-    Qwen2 models get the reference's YaRN extension (factor 4 over 32768 positions)."""
-    import transformers
-    from transformers import AutoConfig
-
-    config = AutoConfig.from_pretrained(path)
-    if config.model_type == "qwen2":
-        theta = config.rope_parameters["rope_theta"]
-        config.rope_parameters = dict(rope_type="yarn", factor=4.0, original_max_position_embeddings=32768,
-                                      rope_theta=theta)
-        config.max_position_embeddings = 4 * 32768
-    loader = transformers.AutoModelForImageTextToText if hasattr(config, "vision_config") else \
-        transformers.AutoModelForCausalLM
-    return loader.from_pretrained(path, config=config, dtype=torch.bfloat16).cuda().eval()
-
-
-def render_prompt(tokenizer, prompt):
-    """Chat-template rendering of one user turn (models.py:35-37)."""
-    return tokenizer.apply_chat_template([{"role": "user", "content": prompt}], tokenize=False,
-                                         add_generation_prompt=True, date_string="30 Jul 2026")
-
-
-def eos_ids(tokenizer, model):
-    """Union of the tokenizer's and the generation config's end-of-sequence ids (models.py:40-42)."""
-    as_set = lambda ids: set(ids if isinstance(ids, list) else [ids])
-    return as_set(tokenizer.eos_token_id) | as_set(model.generation_config.eos_token_id)
 
 
 class _AllExact:

@@ -119,15 +119,28 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
     hq, hk = 32, 8
     log(f"C3: storing {len(lengths)} ragged prompts ({sum(lengths)} tokens)")
     gdev = torch.Generator(device=dev).manual_seed(1003)
-    cache = DecodeCache(module, max_tail=256)
-    cache.ragged = True
-    pre = Prefill(module, from_bands({"0": bands.tolist()}), cache)
+    kvs = []
     for n in lengths:
         k = S.outlier_tensor_device(gdev, 1, hk, n)
-        v = S.outlier_tensor_device(gdev, 1, hk, n)
-        pre.store_only(0, k, v, hq)
-    del pre
-    torch.cuda.synchronize()
+        kvs.append((k, S.outlier_tensor_device(gdev, 1, hk, n)))
+    # the cache build: one store_only per prompt (quantize K, pack V, and the device-side store that
+    # classifies the tiles and appends the records), timed twice, the second on a warm allocator
+    for rep in range(2):
+        cache = DecodeCache(module, max_tail=256)
+        cache.ragged = True
+        pre = Prefill(module, from_bands({"0": bands.tolist()}), cache)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        b0.record(stream)
+        for k, v in kvs:
+            pre.store_only(0, k, v, hq)
+        b1.record(stream)
+        torch.cuda.synchronize()
+        build_wall_ms = (time.perf_counter() - t0) * 1e3
+        build_gpu_ms = b0.elapsed_time(b1)
+    del pre, kvs
+    log(f"C3 cache build: {build_wall_ms:.1f} ms wall, {build_gpu_ms:.1f} ms on the GPU")
     e = cache.layers[0]
     rec_bytes, kept = decode_record_bytes(e)
     batch = len(lengths)
@@ -160,6 +173,8 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
             "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
             "record_bytes_per_step": rec_bytes, "kept_tiles": kept,
             "decode_kv_gbs": round(rec_bytes / (ms * 1e-3) / 1e9, 2),
+            "cache_build_ms": {"wall": round(build_wall_ms, 2), "gpu": round(build_gpu_ms, 2),
+                               "what": "64 Prefill.store_only calls: quantize, pack and the device-side store"},
             "split_kernel_us": round(dec_ms * 1e3, 2),
             "split_kernel_gbs": round(rec_bytes / (dec_ms * 1e-3) / 1e9, 2),
             "frac_hbm_peak": round(rec_bytes / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -159,6 +159,31 @@ int tri_decode_partials_timed(const void* q, int64_t q_sb, int64_t q_sh, const v
                               const int32_t* bounds, int nsplit, double scale, void* stream, void* ev_start,
                               void* ev_stop);
 
+/* Replaces the host-side assembly of DecodeCache.store (kernels/decode.py:24-67): one launch appends
+ * the decode-cache entries of a Prefill call's batch (batch sequences of t tokens each) as rows row0 ..
+ * row0 + batch - 1 of a cache with `rows` rows, computing the kept-tile metadata on the device from
+ * bands int32 [hq][2] and compacting the records.
+ * Sources (the Prefill outputs): kp / k4p K8 / K4 records, v8p / v4p V8 / V4 records [batch][hk][tiles],
+ * ka / ka4 f32 [batch][hk][tiles][4], kstat / vstat f32 [batch][hk][3][128]; k4p / ka4 / v4p may be NULL
+ * when no tile needs them.  exact: NULL, or int32 [hk] on the device, -1 for a quantized KV head and
+ * otherwise the head's slot (< nx) in kx / vx [batch][nx][tiles] (16 KiB bf16 records, tri_pack_exact).
+ * Destinations, as tri_decode reads them: entry / kinfo / slot [rows][hk][maxn] (entries past a head's
+ * count zero), count [rows][hk], fmt [rows][tiles_max] (1 = INT8 V, 2 = INT4 V, 1 past the prompt),
+ * prompt [rows], xslot [rows][hk] (may be NULL without exact heads), ka_c / ka4_c [rows][hk][tiles_max][4]
+ * (1.0 past the prompt; ka4_c may be NULL), kstat_c / vstat_c [rows][hk][3][128], and the compacted
+ * record arrays k8c / k4c / v8c / v4c / kxc / vxc whose first free records are o8 / o4 / ov8 / ov4 / ox
+ * and which hold cap8 / cap4 / capv8 / capv4 / capx records (records past a capacity are not written;
+ * k4c / v4c NULL with capacity 0 when absent).  Within a sequence, records are numbered in (KV head,
+ * entry) order and each sequence takes as many as its metadata selects, after the previous sequence's. */
+int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int hq, int hk, int t, int nx,
+                    const void* kp, const void* k4p, const float* ka, const float* ka4, const float* kstat,
+                    const float* vstat, const void* v8p, const void* v4p, const void* kx, const void* vx, int row0,
+                    int rows, int maxn, int tiles_max, int32_t* entry, int32_t* kinfo, int32_t* slot, int32_t* count,
+                    int32_t* fmt, int32_t* prompt, int32_t* xslot, float* ka_c, float* ka4_c, float* kstat_c,
+                    float* vstat_c, void* k8c, int64_t o8, int64_t cap8, void* k4c, int64_t o4, int64_t cap4,
+                    void* v8c, int64_t ov8, int64_t capv8, void* v4c, int64_t ov4, int64_t capv4, void* kxc,
+                    void* vxc, int64_t ox, int64_t capx, void* stream);
+
 /* No counterpart in the reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): tri_decode with the split
  * partials pm / pl / po held in a scratch array inside the library (24 MiB of fp32 per GPU, held until

@@ -114,7 +114,8 @@ def test_kernel_codes_match_golden(module, t):
     cache = DecodeCache(module, max_tail=8)
     out, ops, pre = run_prefill(module, bf16(g["q"]), bf16(g["k"]), bf16(g["v"]), torch.from_numpy(g["bands"]),
                                 128 ** -0.5, decode_cache=cache)
-    compare_codes(ops, codes, 0, 1, 6, 2, t, kept=next(iter(pre.layer_buffers.values())))
+    e = cache.layers[0]
+    compare_codes(ops, codes, 0, 1, 6, 2, t, kept=(e["ka"], e["kstat"], e["vstat"], e["ka4"]))
     if t == 200:
         assert_close(out[0].numpy(), load("prefill_T200.npz")["out"], what="prefill T200 vs golden")
 

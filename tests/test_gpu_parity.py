@@ -98,7 +98,8 @@ def _decode_case(module, prompt, bands, batch=1, steps=3, max_tail=8, seed=5000,
     _, ops, pre = run_prefill(module, q, k, v, bands, scale, decode_cache=cache)
     ref_codes = [O.prefill_codes(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), decode_cache=True)
                  for b in range(batch)]
-    kept = next(iter(pre.layer_buffers.values()))
+    e = cache.layers[0]
+    kept = (e["ka"], e["kstat"], e["vstat"], e["ka4"])  # the copies the cache keeps
     for b in range(batch):
         compare_codes(ops, ref_codes[b], b, batch, hq, hk, prompt, kept=kept)
     g = S.gen(seed + 1)

@@ -82,12 +82,7 @@ def test_tile_states_closed_form():
     assert s.tolist() == [[8, 0, 4, 4, 8, 8], [8] * 6, [8, 4, 4, 4, 4, 8], [8, 0, 0, 0, 0, 0]]
 
 
-class FakeModule:
-    def device_cus(self):
-        return 4
-
-    def decode_occupancy(self):
-        return 2
+from cache_host import HostCacheModule as FakeModule  # noqa: E402
 
 
 def test_balanced_partition_is_a_valid_cost_balanced_split():

@@ -13,6 +13,7 @@
 #include <hip/hip_ext.h>
 
 #include "../../include/triattention_amd.h"
+#include "cache.hip"
 #include "decode.hip"
 #include "prefill.hip"
 #include "quantize.hip"
@@ -471,6 +472,93 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   float* pl = s + pad;
   float* po = s + 2 * pad;
   return decode_impl(TRI_DECODE_ARGS, 3);
+}
+
+int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int hq, int hk, int t, int nx,
+                    const void* kp, const void* k4p, const float* ka, const float* ka4, const float* kstat,
+                    const float* vstat, const void* v8p, const void* v4p, const void* kx, const void* vx, int row0,
+                    int rows, int maxn, int tiles_max, int32_t* entry, int32_t* kinfo, int32_t* slot, int32_t* count,
+                    int32_t* fmt, int32_t* prompt, int32_t* xslot, float* ka_c, float* ka4_c, float* kstat_c,
+                    float* vstat_c, void* k8c, int64_t o8, int64_t cap8, void* k4c, int64_t o4, int64_t cap4,
+                    void* v8c, int64_t ov8, int64_t capv8, void* v4c, int64_t ov4, int64_t capv4, void* kxc,
+                    void* vxc, int64_t ox, int64_t capx, void* stream) {
+  g_error.clear();
+  const int tiles = (t + tri::BN - 1) / tri::BN;
+  if (!bands || !kp || !ka || !kstat || !vstat || !v8p || !entry || !kinfo || !slot || !count || !fmt || !prompt ||
+      !ka_c || !kstat_c || !vstat_c || !k8c || !v8c)
+    return fail("cache_store: null buffer");
+  if (batch < 1 || hq < 1 || hk < 1 || t < 1) return fail("cache_store: empty shape");
+  if (hq % hk != 0 || hq / hk > tri::MAX_GROUP || hq > tri::STORE_MAX_HQ)
+    return fail("cache_store: q heads must be a multiple of the kv heads, groups of at most 8, at most 256 q heads");
+  if (tiles > tri::MAX_TILES) return fail("cache_store: at most 131072 tokens");
+  if (row0 < 0 || (int64_t)row0 + batch > rows) return fail("cache_store: rows %d..%d beyond the %d allocated", row0,
+                                                             row0 + batch - 1, rows);
+  if (maxn < 1 || tiles_max < tiles) return fail("cache_store: maxn >= 1 and tiles_max >= the prompt's tiles");
+  if (exact && (nx < 1 || nx > hk || !kx || !vx || !kxc || !vxc || !xslot))
+    return fail("cache_store: exact heads need nx in [1, hk], KX/VX sources, destinations and xslot");
+  if (o8 < 0 || o4 < 0 || ov8 < 0 || ov4 < 0 || ox < 0) return fail("cache_store: negative record offset");
+  if ((k4c == nullptr) != (cap4 == 0) || (v4c == nullptr) != (capv4 == 0))
+    return fail("cache_store: INT4 K / V destinations and capacities (both or neither)");
+  if (cap8 * tri::K8_BYTES >= ((int64_t)1 << 31) || cap4 * tri::K4_BYTES >= ((int64_t)1 << 31) ||
+      capv8 * tri::V8_BYTES >= ((int64_t)1 << 31) || capv4 * tri::V4_BYTES >= ((int64_t)1 << 31) ||
+      capx * tri::KX_BYTES >= ((int64_t)1 << 31))
+    return fail("cache_store: compacted record arrays must stay below 2 GiB each");
+  for (const void* p : {kp, k4p, v8p, v4p, kx, vx, (const void*)k8c, (const void*)k4c, (const void*)v8c,
+                        (const void*)v4c, (const void*)kxc, (const void*)vxc})
+    if (p && !aligned(p, 16)) return fail("cache_store: record arrays must be 16-byte aligned");
+  tri::CacheStoreArgs a;
+  a.bands = bands;
+  a.exact = exact;
+  a.hq = hq;
+  a.hk = hk;
+  a.t = t;
+  a.tiles = tiles;
+  a.nx = exact ? nx : 0;
+  a.batch = batch;
+  a.kp = static_cast<const uint8_t*>(kp);
+  a.k4p = static_cast<const uint8_t*>(k4p);
+  a.v8p = static_cast<const uint8_t*>(v8p);
+  a.v4p = static_cast<const uint8_t*>(v4p);
+  a.kx = static_cast<const uint8_t*>(kx);
+  a.vx = static_cast<const uint8_t*>(vx);
+  a.ka = ka;
+  a.ka4 = ka4;
+  a.kstat = kstat;
+  a.vstat = vstat;
+  a.row0 = row0;
+  a.rows = rows;
+  a.maxn = maxn;
+  a.tiles_max = tiles_max;
+  a.entry = entry;
+  a.kinfo = kinfo;
+  a.slot = slot;
+  a.count = count;
+  a.fmt = fmt;
+  a.prompt = prompt;
+  a.xslot = xslot;
+  a.ka_c = ka_c;
+  a.ka4_c = ka4_c;
+  a.kstat_c = kstat_c;
+  a.vstat_c = vstat_c;
+  a.k8c = static_cast<uint8_t*>(k8c);
+  a.k4c = static_cast<uint8_t*>(k4c);
+  a.v8c = static_cast<uint8_t*>(v8c);
+  a.v4c = static_cast<uint8_t*>(v4c);
+  a.kxc = static_cast<uint8_t*>(kxc);
+  a.vxc = static_cast<uint8_t*>(vxc);
+  a.o8 = o8;
+  a.o4 = o4;
+  a.ov8 = ov8;
+  a.ov4 = ov4;
+  a.ox = ox;
+  a.cap8 = cap8;
+  a.cap4 = cap4;
+  a.capv8 = capv8;
+  a.capv4 = capv4;
+  a.capx = exact ? capx : 0;
+  const dim3 grid((tiles + tri::STORE_CHUNK - 1) / tri::STORE_CHUNK, hk, batch);
+  tri::cache_store_kernel<<<grid, tri::STORE_THREADS, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch("cache_store");
 }
 
 int tri_decode_occupancy(int* blocks) {

@@ -144,6 +144,78 @@ def balanced_partition(metas, batches, slots: int):
     return [torch.from_numpy(pad(b).astype(np.int32)) for b in out], splits
 
 
+class _LayerStore:
+    """A layer's decode-cache arrays on the device, with room to append sequences: per-sequence rows
+    (metadata [rows][hk][maxn], scales [rows][hk][tiles_max][4], statistics, bf16 tails) and the
+    compacted record arrays.  ``n`` counts the records in use, ``cap`` what each array holds.  Growing
+    copies what is stored (amortised by doubling in ragged mode); nothing stored is recomputed."""
+
+    RECORD = dict(k8=(K8_WORDS, torch.uint32), k4=(K4_WORDS, torch.uint32), v8=(WORDS[I8], torch.uint32),
+                  v4=(WORDS[I4], torch.uint32))
+
+    def __init__(self, hk, max_tail, device):
+        self.hk, self.max_tail, self.device = hk, max_tail, device
+        self.rows = self.maxn = self.tiles_max = 0
+        self.n = dict(k8=0, k4=0, v8=0, v4=0, x=0)
+        self.cap = dict(rows=0, k8=0, k4=0, v8=0, v4=0, x=0)
+        self.arrays = {name: None for name in ("entry", "kinfo", "slot", "count", "fmt", "prompt", "xslot", "ka",
+                                               "ka4", "kstat", "vstat", "tail_k", "tail_v", "k8", "k4", "v8", "v4",
+                                               "kx", "vx")}
+        self.groups = []
+
+    def _regrow(self, name, shape, fill, dtype):
+        """Array ``name`` at ``shape``, filled with ``fill`` and holding the old contents in its corner."""
+        old = self.arrays[name]
+        if old is not None and tuple(old.shape) == tuple(shape):
+            return
+        new = torch.full(shape, fill, dtype=dtype, device=self.device) if fill is not None else \
+            torch.zeros(shape, dtype=dtype, device=self.device)
+        if old is not None:
+            new[tuple(slice(0, min(o, n)) for o, n in zip(old.shape, shape))] = \
+                old[tuple(slice(0, min(o, n)) for o, n in zip(old.shape, shape))]
+        self.arrays[name] = new
+
+    def reserve(self, rows, maxn, tiles_max, records, int4, exact, ragged):
+        """Make room for ``rows`` sequences with metadata rows of ``maxn`` entries over ``tiles_max``
+        tiles and ``records`` (per kind) records."""
+        grow = (lambda need, cap: max(need, 2 * cap) if need > cap else cap) if ragged else \
+            (lambda need, cap: max(need, cap))
+        cap_rows = grow(rows, self.cap["rows"])
+        relayout = cap_rows != self.cap["rows"] or maxn != self.maxn or tiles_max != self.tiles_max
+        self.cap["rows"], self.maxn, self.tiles_max = cap_rows, maxn, tiles_max
+        hk, i32, f32 = self.hk, torch.int32, torch.float32
+        if relayout:
+            for name in ("entry", "kinfo", "slot"):
+                self._regrow(name, (cap_rows, hk, maxn), 0, i32)
+            self._regrow("count", (cap_rows, hk), 0, i32)
+            self._regrow("fmt", (cap_rows, tiles_max), 1, i32)
+            self._regrow("prompt", (cap_rows,), 0, i32)
+            self._regrow("ka", (cap_rows, hk, tiles_max, 4), 1.0, f32)
+            self._regrow("kstat", (cap_rows, hk, 3, 128), 0.0, f32)
+            self._regrow("vstat", (cap_rows, hk, 3, 128), 0.0, f32)
+            for name in ("tail_k", "tail_v"):
+                self._regrow(name, (cap_rows, hk, self.max_tail, 128), 0.0, torch.bfloat16)
+        if (int4 or self.arrays["ka4"] is not None) and (relayout or self.arrays["ka4"] is None):
+            self._regrow("ka4", (cap_rows, hk, tiles_max, 4), 1.0, f32)
+        if (exact or self.arrays["xslot"] is not None) and (relayout or self.arrays["xslot"] is None):
+            self._regrow("xslot", (cap_rows, hk), -1, i32)
+        for kind, (words, dtype) in self.RECORD.items():
+            # the decode op takes non-empty K8 / V8 / V4 arrays: at least one (zero) record each
+            need = max(records[kind], 1 if kind != "k4" else 0)
+            if kind == "k4" and not int4 and self.arrays["k4"] is None:
+                continue
+            cap = grow(max(need, 1), self.cap[kind])
+            if cap != self.cap[kind] or self.arrays[kind] is None:
+                self._regrow(kind, (cap, words), None, dtype)
+                self.cap[kind] = cap
+        if exact or self.arrays["kx"] is not None:
+            cap = grow(max(records["x"], 1), self.cap["x"])
+            if cap != self.cap["x"] or self.arrays["kx"] is None:
+                self._regrow("kx", (cap * KX_BYTES,), None, torch.uint8)
+                self._regrow("vx", (cap * KX_BYTES,), None, torch.uint8)
+                self.cap["x"] = cap
+
+
 class DecodeCache:
     def __init__(self, module, max_tail=256):
         self.module, self.max_tail = module, max_tail
@@ -164,120 +236,66 @@ class DecodeCache:
 
     def store(self, layer, prompt, kp, ka, kstat, vstat, packed, codes, bands, k4, ka4, exact_kv=(), kx=None,
               vx=None):
-        """Keep one Prefill call's records (decode.py:24-67).  Extension: ``exact_kv``
-        lists the KV heads kept in bf16, whose KX/VX records ``kx``/``vx``
-        ([B][len(exact_kv)][tiles], tri_pack_exact layout) are copied whole."""
+        """Keep one Prefill call's records (decode.py:24-67).
+
+        One device launch (``cache_store``) classifies the prompt's tiles, writes the batch's metadata
+        rows and copies the kept records, scales and statistics into the layer's own arrays, so the
+        Prefill may reuse every buffer it passed here.  With ``ragged = True`` the batch is appended
+        after the layer's earlier sequences (arrays grow geometrically; earlier rows are never
+        rebuilt); otherwise it replaces them.  Extension: ``exact_kv`` lists the KV heads kept in
+        bf16, whose KX/VX records ``kx``/``vx`` ([B][len(exact_kv)][tiles], tri_pack_exact layout)
+        are copied whole."""
         tiles = (prompt + 63) // 64
         batch = vstat.shape[0]
         hk, device = vstat.shape[1], ka.device
         exact_kv = sorted(set(int(h) for h in exact_kv))
         meta, dev = self._metadata(bands, tiles, hk, codes, exact_kv, device)
-        nbytes = batch * len(exact_kv) * tiles * KX_BYTES
-        # record indices of every sequence of the batch, sequence-major, built on the device
-        seq = torch.arange(batch, dtype=torch.int64, device=device)[:, None] * (hk * tiles)
-        pick = lambda kind: (seq + dev["pick"][kind][None, :]).flatten()
-        group = dict(prompt=prompt, batch=batch, hk=hk, tiles=tiles, meta=meta, dev=dev,
-                     n8=int(meta["is8"].sum()), n4=int(meta["is4"].sum()),
-                     nv={code: int(meta["vsel"][code].sum()) for code in (I8, I4)},
-                     k8=kp.view(batch * hk * tiles, K8_WORDS).index_select(0, pick("k8")),
-                     k4=(k4.view(batch * hk * tiles, K4_WORDS).index_select(0, pick("k4"))
-                         if bool(meta["is4"].any()) else None),
-                     v={code: (packed[code].view(batch * hk * tiles, WORDS[code]).index_select(0, pick(code))
-                               if bool(meta["vsel"][code].any()) else None) for code in (I8, I4)},
-                     # copies, not views: the Prefill reuses these buffers for its next call with the
-                     # same shape, and a ragged cache re-reads every stored group
-                     ka=ka.view(batch, hk, tiles, 4).clone(),
-                     ka4=ka4.view(batch, hk, tiles, 4).clone() if ka4 is not None else None,
-                     kstat=kstat.view(batch, hk, 3, 128).clone(), vstat=vstat.view(batch, hk, 3, 128).clone(),
-                     exact=exact_kv,
-                     kx=kx.reshape(-1)[:nbytes].clone() if exact_kv else None,
-                     vx=vx.reshape(-1)[:nbytes].clone() if exact_kv else None)
+        hq = dev["bands"].shape[0]
+        seq = dict(k8=int(meta["is8"].sum()), k4=int(meta["is4"].sum()), v8=int(meta["vsel"][I8].sum()),
+                   v4=int(meta["vsel"][I4].sum()), x=len(exact_kv) * tiles)
+        entry = self.layers.get(layer)
+        st = entry["store"] if (self.ragged and entry is not None) else _LayerStore(hk, self.max_tail, device)
+        if st.hk != hk:
+            raise ValueError(f"decode cache layer {layer}: {hk} KV heads after {st.hk}")
+        row0 = st.rows
+        st.reserve(row0 + batch, max(st.maxn, meta["maxn"]), max(st.tiles_max, tiles),
+                   {k: st.n[k] + batch * seq[k] for k in seq}, k4 is not None or ka4 is not None, bool(exact_kv),
+                   ragged=self.ragged)
+        self.module.cache_store(dev["bands"], dev["exact"], prompt, kp, k4, ka, ka4, kstat, vstat, packed[I8],
+                                packed.get(I4), kx, vx, len(exact_kv), row0, st.arrays, st.n, st.cap)
+        st.rows += batch
+        for k in seq:
+            st.n[k] += batch * seq[k]
+        st.groups.append(dict(prompt=prompt, batch=batch, hk=hk, tiles=tiles, meta=meta, exact=exact_kv))
         if self.step is None:
             self.step = torch.zeros(1, dtype=torch.int64, device=device)
         self.step.zero_()
-        entry = self.layers.get(layer)
-        groups = entry["groups"] + [group] if (self.ragged and entry is not None) else [group]
-        self.layers[layer] = self._assemble(groups, device)
+        st.arrays["tail_k"][:st.rows].zero_()
+        st.arrays["tail_v"][:st.rows].zero_()
+        self.layers[layer] = self._assemble(st)
 
     def _metadata(self, bands, tiles, hk, codes, exact_kv, device):
-        """One sequence's metadata (host, closed-form integer code) and its device copy, cached per
-        (bands, tiles, KV heads, exact heads, device): every sequence of the same length shares it."""
-        b = torch.as_tensor(bands, dtype=torch.int32).cpu()
+        """One sequence's metadata (host, closed-form integer code: the record counts that size the
+        cache's arrays and the entry costs of the split partition) with the device copies the store
+        launch reads, cached per (bands, tiles, KV heads, exact heads, device): every sequence of the
+        same length shares it."""
+        b = torch.as_tensor(bands, dtype=torch.int32).cpu().contiguous()
         key = (b.numpy().tobytes(), tiles, hk, tuple(exact_kv), str(device))
         hit = self.meta_cache.get(key)
         if hit is None:
             meta = sequence_metadata(b, tiles, hk, codes, exact_kv)
-            to = lambda x: x.to(device)
-            dev = dict(valid=to(meta["valid"]), order=to(meta["order"]), is4=to(meta["is4"]),
-                       kslot=to(meta["kslot"]), kbase=to(meta["kbase"]), vcode=to(meta["vcode"]),
-                       vslot=to(meta["vslot"]), count=to(meta["count"]), fmt=to(codes.to(torch.int64) - 1),
-                       pick={kind: to(meta["rows"][select]) for kind, select in
-                             (("k8", meta["is8"]), ("k4", meta["is4"]), (I8, meta["vsel"][I8]),
-                              (I4, meta["vsel"][I4]))})
+            flags = torch.full((hk,), -1, dtype=torch.int32)
+            for xs, h in enumerate(exact_kv):
+                flags[h] = xs
+            dev = dict(bands=b.to(device), exact=flags.to(device) if exact_kv else None)
             hit = self.meta_cache[key] = (meta, dev)
         return hit
 
-    def _assemble(self, groups, device):
-        """Batched metadata and concatenated records over every stored sequence: a few device
-        operations per group (a store's sequences share one length), none per sequence."""
-        hk = groups[0]["hk"]
-        total = sum(g["batch"] for g in groups)
-        tiles_max = max(g["tiles"] for g in groups)
-        maxn = max(g["meta"]["maxn"] for g in groups)
-        i64 = dict(dtype=torch.int64, device=device)
-        entry = torch.zeros((total, hk, maxn), **i64)
-        kinfo = torch.zeros_like(entry)
-        slot = torch.zeros_like(entry)
-        count = torch.zeros((total, hk), **i64)
-        fmt = torch.ones((total, tiles_max), **i64)
-        prompt = torch.zeros(total, **i64)
-        has4 = any(g["k4"] is not None for g in groups)
-        ka = torch.ones((total, hk, tiles_max, 4), dtype=torch.float32, device=device)
-        ka4 = torch.ones_like(ka) if has4 else None
-        kstat = torch.empty((total, hk, 3, 128), dtype=torch.float32, device=device)
-        vstat = torch.empty_like(kstat)
-        k8s, k4s, v8s, v4s, kxs, vxs = [], [], [], [], [], []
-        xslot = torch.full((total, hk), -1, **i64)
-        o8 = o4 = ov8 = ov4 = ox = 0
-        row = 0
-        for g in groups:
-            d, n, b, tiles = g["dev"], g["meta"]["maxn"], g["batch"], g["tiles"]
-            rows = slice(row, row + b)
-            sq = torch.arange(b, **i64)
-            s3 = sq[:, None, None]
-            entry[rows, :, :n] = torch.where(d["valid"], d["order"] | ENTRY_VFMT | (d["vcode"] == I8).to(torch.int64) << 29, 0)
-            ks = torch.where(d["is4"], d["kslot"] + o4 + s3 * g["n4"], d["kslot"] + o8 + s3 * g["n8"])
-            kinfo[rows, :, :n] = torch.where(d["valid"], d["kbase"] | (ks << 9), 0)
-            vs = torch.where(d["vcode"] == I4, d["vslot"] + ov4 + s3 * g["nv"][I4], d["vslot"] + ov8 + s3 * g["nv"][I8])
-            slot[rows, :, :n] = torch.where(d["valid"], vs, 0)
-            count[rows] = d["count"]
-            fmt[rows, :tiles] = d["fmt"]
-            prompt[rows] = g["prompt"]
-            for xs, h in enumerate(g["exact"]):
-                xslot[rows, h] = ox + (sq * len(g["exact"]) + xs) * tiles
-            ka[rows, :, :tiles] = g["ka"]
-            if g["ka4"] is not None and ka4 is not None:
-                ka4[rows, :, :tiles] = g["ka4"]
-            kstat[rows] = g["kstat"]
-            vstat[rows] = g["vstat"]
-            k8s.append(g["k8"])
-            if g["k4"] is not None:
-                k4s.append(g["k4"])
-            if g["v"][I8] is not None:
-                v8s.append(g["v"][I8])
-            if g["v"][I4] is not None:
-                v4s.append(g["v"][I4])
-            if g["exact"]:
-                kxs.append(g["kx"])
-                vxs.append(g["vx"])
-                ox += b * len(g["exact"]) * tiles
-            o8 += b * g["n8"]
-            o4 += b * g["n4"]
-            ov8 += b * g["nv"][I8]
-            ov4 += b * g["nv"][I4]
-            row += b
-        cat = lambda parts, words: (torch.cat(parts) if sum(p.shape[0] for p in parts) else
-                                    torch.zeros((1, words), dtype=torch.uint32, device=device))
+    def _assemble(self, st):
+        """The layer entry the decode op reads: views of the store's arrays over its sequences, and the
+        split partition over every stored group (host metadata, no device sync)."""
+        groups, device = st.groups, st.device
+        a, rows = st.arrays, st.rows
         if self.wave is None:
             cus = self.module.device_cus() if hasattr(self.module, "device_cus") else \
                 torch.cuda.get_device_properties(device).multi_processor_count
@@ -300,20 +318,23 @@ class DecodeCache:
             per = int(bounds_host.diff(dim=2).max())
             bounds = bounds_host.to(device)
         else:
-            mean = kept / max(1, total * hk)
+            mean = kept / max(1, rows * st.hk)
             per = self.per or min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 3))))
             bounds_host = bounds = None
-            splits = max(1, -(-maxn // per))
-        to = lambda x: x.to(torch.int32).to(device)
-        tail_k = torch.zeros((total, hk, self.max_tail, 128), dtype=torch.bfloat16, device=device)
-        return dict(groups=groups, prompt=to(prompt), maxn=maxn, per=per, splits=splits, bounds=bounds,
-                    bounds_host=None if bounds_host is None else bounds_host.numpy(), fmt=to(fmt), slot=to(slot),
-                    entry=to(entry),
-                    kinfo=to(kinfo), count=to(count), k8=cat(k8s, K8_WORDS), k4=cat(k4s, K4_WORDS) if has4 else None,
-                    ka=ka, ka4=ka4, kstat=kstat, vstat=vstat, v={I8: cat(v8s, WORDS[I8]), I4: cat(v4s, WORDS[I4])},
-                    tail_k=tail_k, tail_v=torch.zeros_like(tail_k), batch=total, tiles_max=tiles_max,
-                    xslot=to(xslot) if kxs else None, kx=torch.cat(kxs) if kxs else None,
-                    vx=torch.cat(vxs) if vxs else None)
+            splits = max(1, -(-st.maxn // per))
+        some = lambda name, n: a[name][:max(1, n)]
+        has_x = any(g["exact"] for g in groups)
+        return dict(groups=groups, store=st, prompt=a["prompt"][:rows], maxn=st.maxn, per=per, splits=splits,
+                    bounds=bounds, bounds_host=None if bounds_host is None else bounds_host.numpy(),
+                    fmt=a["fmt"][:rows], slot=a["slot"][:rows], entry=a["entry"][:rows], kinfo=a["kinfo"][:rows],
+                    count=a["count"][:rows], k8=some("k8", st.n["k8"]),
+                    k4=some("k4", st.n["k4"]) if a["k4"] is not None else None, ka=a["ka"][:rows],
+                    ka4=a["ka4"][:rows] if a["ka4"] is not None else None, kstat=a["kstat"][:rows],
+                    vstat=a["vstat"][:rows], v={I8: some("v8", st.n["v8"]), I4: some("v4", st.n["v4"])},
+                    tail_k=a["tail_k"][:rows], tail_v=a["tail_v"][:rows], batch=rows, tiles_max=st.tiles_max,
+                    xslot=a["xslot"][:rows] if has_x else None,
+                    kx=a["kx"][:st.n["x"] * KX_BYTES] if has_x else None,
+                    vx=a["vx"][:st.n["x"] * KX_BYTES] if has_x else None)
 
     def __call__(self, layer, q, k, v, scale):
         e = self.layers[layer]

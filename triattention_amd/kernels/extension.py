@@ -37,7 +37,7 @@ K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
            "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_noalloc",
-           "tri_decode_occupancy", "tri_device_cus")
+           "tri_cache_store", "tri_decode_occupancy", "tri_device_cus")
 KX_BYTES = 16384
 
 
@@ -69,6 +69,9 @@ def load_library() -> ctypes.CDLL:
     lib.tri_decode_partials_timed.argtypes = decode_args + [P, P]
     # tri_decode without pm / pl / po (arguments 31-33 of tri_decode)
     lib.tri_decode_noalloc.argtypes = decode_args[:31] + decode_args[34:]
+    lib.tri_cache_store.argtypes = [P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P,
+                                    P, P, P, P, P, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, P, I64, I64,
+                                    P]
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:
@@ -297,6 +300,55 @@ class Module:
         keep = (k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, step, pm, pl,
                 po, prompt_t, xslot, kxc, vxc, bounds)
         return DecodePlan(self, args, q, kcur, out, keep)
+
+    def cache_store(self, bands, exact, t, kp, k4p, ka, ka4, kstat, vstat, v8p, v4p, kx, vx, nx, row0, dst, used,
+                    cap):
+        """Append one Prefill call's batch to a decode cache on the device (extension; the reference
+        assembles its cache on the host, kernels/decode.py:24-67).  Sources as ``store`` receives them;
+        ``dst`` the cache's arrays (entry / kinfo / slot [rows][hk][maxn], count, fmt, prompt, xslot, ka,
+        ka4, kstat, vstat, compacted k8 / k4 / v8 / v4 records and kx / vx bytes), ``used`` / ``cap`` the
+        records in use and held per kind (k8, k4, v8, v4, x), sequence rows from ``row0``."""
+        b, hk = vstat.shape[0], vstat.shape[1]
+        hq = bands.shape[0]
+        rows, maxn = dst["entry"].shape[0], dst["entry"].shape[2]
+        tiles_max = dst["fmt"].shape[1]
+        tiles = (t + 63) // 64
+        _check(bands.dtype == torch.int32 and bands.is_cuda and bands.is_contiguous() and bands.dim() == 2 and
+               bands.size(1) == 2, "cache_store: bands int32 [Hq,2] on the device")
+        _check(exact is None or (exact.dtype == torch.int32 and exact.is_cuda and exact.numel() == hk),
+               "cache_store: exact flags int32 [Hk] on the device")
+        _check(kp.numel() * kp.element_size() >= b * hk * tiles * K8_WORDS * 4 and
+               v8p.numel() * v8p.element_size() >= b * hk * tiles * V8_WORDS * 4 and
+               (k4p is None or k4p.numel() * k4p.element_size() >= b * hk * tiles * K4_WORDS * 4) and
+               (v4p is None or v4p.numel() * v4p.element_size() >= b * hk * tiles * V4_WORDS * 4) and
+               ka.numel() >= b * hk * tiles * 4 and (ka4 is None or ka4.numel() >= b * hk * tiles * 4) and
+               kstat.numel() == b * hk * 3 * D and vstat.numel() == b * hk * 3 * D,
+               "cache_store: source records and scales [B,Hk,tiles]")
+        _check(exact is None or (kx is not None and vx is not None and
+                                 kx.numel() * kx.element_size() >= b * nx * tiles * KX_BYTES and
+                                 vx.numel() * vx.element_size() >= b * nx * tiles * KX_BYTES),
+               "cache_store: KX/VX records of the exact heads")
+        for name in ("entry", "kinfo", "slot"):
+            _check(tuple(dst[name].shape) == (rows, hk, maxn) and dst[name].dtype == torch.int32, f"cache_store: {name}")
+        _check(tuple(dst["ka"].shape) == (rows, hk, tiles_max, 4) and
+               (dst["ka4"] is None or tuple(dst["ka4"].shape) == (rows, hk, tiles_max, 4)) and
+               tuple(dst["count"].shape) == (rows, hk) and dst["prompt"].numel() == rows and
+               tuple(dst["kstat"].shape) == (rows, hk, 3, D) and tuple(dst["vstat"].shape) == (rows, hk, 3, D) and
+               (dst["xslot"] is None or tuple(dst["xslot"].shape) == (rows, hk)), "cache_store: cache rows")
+        for kind, words in (("k8", K8_WORDS), ("k4", K4_WORDS), ("v8", V8_WORDS), ("v4", V4_WORDS)):
+            x = dst[kind]
+            _check((x is None and cap[kind] == 0) or (x is not None and x.shape[0] >= cap[kind] and x.shape[1] == words),
+                   f"cache_store: {kind} record array")
+        _check(dst["kx"] is None or dst["kx"].numel() >= cap["x"] * KX_BYTES, "cache_store: KX/VX record arrays")
+        p = _ptr
+        with torch.cuda.device(vstat.device):
+            self._call(self.lib.tri_cache_store, p(bands), p(exact), b, hq, hk, int(t), int(nx), p(kp), p(k4p), p(ka),
+                       p(ka4), p(kstat), p(vstat), p(v8p), p(v4p), p(kx), p(vx), int(row0), rows, maxn, tiles_max,
+                       p(dst["entry"]), p(dst["kinfo"]), p(dst["slot"]), p(dst["count"]), p(dst["fmt"]),
+                       p(dst["prompt"]), p(dst["xslot"]), p(dst["ka"]), p(dst["ka4"]), p(dst["kstat"]),
+                       p(dst["vstat"]), p(dst["k8"]), used["k8"], cap["k8"], p(dst["k4"]), used["k4"], cap["k4"],
+                       p(dst["v8"]), used["v8"], cap["v8"], p(dst["v4"]), used["v4"], cap["v4"], p(dst["kx"]),
+                       p(dst["vx"]), used["x"], cap["x"], self._stream(vstat.device))
 
     def decode_occupancy(self) -> int:
         """Resident decode workgroups per compute unit."""

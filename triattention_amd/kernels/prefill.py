@@ -58,6 +58,44 @@ class BandTable:
         return cls(order.to(torch.int32).to(device), host32.to(device), frozenset(formats), host32)
 
 
+@dataclass(frozen=True)
+class Layout:
+    """Shape of one Prefill call: everything its scratch buffers depend on."""
+    batch: int
+    hq: int
+    hk: int
+    t: int
+    int4: bool           # INT4 Q/K operands exist (some band has INT4 key tiles)
+    formats: frozenset   # V record formats the call writes
+
+    @property
+    def tiles(self):
+        return (self.t + 63) // 64
+
+
+# The scratch of a Prefill call, one row per buffer: the name it is pooled under (Prefill.buffers, which
+# executors may share), its element count and dtype for a layout, and whether the layout needs it.
+# Word counts per (KV head, tile) are the reference's record sizes (decode.py:7-8).
+SCRATCH = (
+    ("q8", lambda L: L.batch * L.hq * L.t * 128, torch.int8, lambda L: True),
+    ("qa", lambda L: L.batch * L.hq * L.t, torch.float32, lambda L: True),
+    ("k", lambda L: L.batch * L.hk * L.tiles * 2048, torch.uint32, lambda L: True),
+    ("ka", lambda L: L.batch * L.hk * L.tiles * 4, torch.float32, lambda L: True),
+    ("partial", lambda L: L.batch * L.hk * 64 * 3 * 128, torch.float32, lambda L: True),
+    ("kstat", lambda L: L.batch * L.hk * 3 * 128, torch.float32, lambda L: True),
+    ("vstat", lambda L: L.batch * L.hk * 3 * 128, torch.float32, lambda L: True),
+    ("q4", lambda L: L.batch * L.hq * L.t * 64, torch.uint8, lambda L: L.int4),
+    ("qa4", lambda L: L.batch * L.hq * L.t, torch.float32, lambda L: L.int4),
+    ("k4", lambda L: L.batch * L.hk * L.tiles * 1024, torch.uint32, lambda L: L.int4),
+    ("ka4", lambda L: L.batch * L.hk * L.tiles * 4, torch.float32, lambda L: L.int4),
+    # V records: FP16 always; INT8 for INT8 bands and for every INT4 band (INT4 key tiles pair with
+    # INT8 V, prefill_sm80.cu:462-465); INT4 when the decode cache asks for it
+    (f"v{F16}", lambda L: L.batch * L.hk * L.tiles * WORDS[F16], torch.uint32, lambda L: F16 in L.formats),
+    (f"v{I8}", lambda L: L.batch * L.hk * L.tiles * WORDS[I8], torch.uint32, lambda L: I8 in L.formats or L.int4),
+    (f"v{I4}", lambda L: L.batch * L.hk * L.tiles * WORDS[I4], torch.uint32, lambda L: I4 in L.formats),
+)
+
+
 class Prefill:
     """Callable ``prefill(layer, q, k, v, scale) -> out`` for HF attention hooks.
 
@@ -66,12 +104,17 @@ class Prefill:
     selects fp32 output for parity testing; the default is q's dtype.  Maps
     whose ``bands_fn.bf16(layer)`` lists KV heads (the map's optional "bf16"
     key) get exact attention for those heads' q-heads in the same launch.
+
+    Scratch lives in ``buffers`` (name -> flat device tensor, grown on demand), which executors may
+    share (calibrate.py:44-48 assigns one dict to all of them); ``views`` caches each layout's typed
+    views of it.  A decode cache copies what it keeps at ``store`` time, so the scratch is free for
+    the next call as soon as the call's launches are queued.
     """
 
     def __init__(self, module, bands_fn, decode_cache=None, out_dtype=None):
         self.module, self.bands_fn, self.decode_cache = module, bands_fn, decode_cache
         self.out_dtype = out_dtype
-        self.tables, self.buffers, self.views, self.layer_buffers = {}, {}, {}, {}
+        self.tables, self.buffers, self.views = {}, {}, {}
         self.exact_flags = {}
         self.records = None
 
@@ -104,55 +147,37 @@ class Prefill:
         return cur[0][:nbytes], cur[1][:nbytes]
 
     def table(self, layer, heads, kv_heads, rows, device):
-        key = (None if getattr(self.bands_fn, "layer_independent", False) else layer, heads, rows)
-        if key not in self.tables:
-            self.tables[key] = BandTable.build(self.bands_fn(layer, heads), rows, kv_heads, device)
-        return self.tables[key]
+        """The band table of (layer, heads, rows); maps marked ``layer_independent`` share one per shape."""
+        per_layer = not getattr(self.bands_fn, "layer_independent", False)
+        key = (layer if per_layer else None, heads, rows)
+        found = self.tables.get(key)
+        if found is None:
+            found = self.tables[key] = BandTable.build(self.bands_fn(layer, heads), rows, kv_heads, device)
+        return found
 
-    def buffer(self, name, numel, dtype, device):
-        current = self.buffers.get(name)
-        if current is None or current.numel() < numel or current.dtype != dtype or current.device != device:
-            current = self.buffers[name] = torch.empty(numel, dtype=dtype, device=device)
-            self.views.clear()
-        return current[:numel]
-
-    def kept(self, layer, batch, hk, rows, int4, device):
-        """Per-layer scale/statistics buffers that the decode cache keeps (kernels/prefill.py:49-58)."""
-        key = (layer, batch, hk, rows, int4)
-        if key not in self.layer_buffers:
-            self.layer_buffers[key] = (
-                torch.empty(batch * hk * rows * 4, dtype=torch.float32, device=device),
-                torch.empty(batch * hk * 3 * 128, dtype=torch.float32, device=device),
-                torch.empty((batch, hk, 3, 128), dtype=torch.float32, device=device),
-                torch.empty(batch * hk * rows * 4, dtype=torch.float32, device=device) if int4 else None,
-            )
-        return self.layer_buffers[key]
-
-    def operands(self, batch, hq, hk, t, int4, formats, device):
-        key = (batch, hq, hk, t, int4, formats, device)
-        if key in self.views:
-            return self.views[key]
-        rows = (t + 63) // 64
-        buf = lambda name, n, dtype: self.buffer(name, n, dtype, device)
-        ops = dict(
-            q8=buf("q8", batch * hq * t * 128, torch.int8).view(batch, hq, t, 128),
-            qa=buf("qa", batch * hq * t, torch.float32),
-            kp=buf("k", batch * hk * rows * 2048, torch.uint32),
-            ka=buf("ka", batch * hk * rows * 4, torch.float32),
-            partial=buf("partial", batch * hk * 64 * 3 * 128, torch.float32),
-            kstat=buf("kstat", batch * hk * 3 * 128, torch.float32),
-            vstat=buf("vstat", batch * hk * 3 * 128, torch.float32).view(batch, hk, 3, 128),
-            q4=buf("q4", batch * hq * t * 64, torch.uint8) if int4 else None,
-            qa4=buf("qa4", batch * hq * t, torch.float32) if int4 else None,
-            k4=buf("k4", batch * hk * rows * 1024, torch.uint32) if int4 else None,
-            ka4=buf("ka4", batch * hk * rows * 4, torch.float32) if int4 else None,
-        )
-        packed = {code: buf(f"v{code}", batch * hk * rows * words, torch.uint32) if code in formats else None
-                  for code, words in WORDS.items()}
-        if int4 and packed[I8] is None:
-            packed[I8] = buf(f"v{I8}", batch * hk * rows * 2048, torch.uint32)
-        ops["packed"] = packed
-        self.views[key] = ops
+    def operands(self, layout, device):
+        """Typed views of the pooled scratch for ``layout`` (None for buffers the layout does not need).
+        A pool buffer too small or of another dtype or device is replaced, which invalidates every
+        cached view."""
+        found = self.views.get((layout, device))
+        if found is not None:
+            return found
+        ops = {}
+        for name, count, dtype, needed in SCRATCH:
+            if not needed(layout):
+                ops[name] = None
+                continue
+            n = count(layout)
+            pool = self.buffers.get(name)
+            if pool is None or pool.numel() < n or pool.dtype != dtype or pool.device != device:
+                pool = self.buffers[name] = torch.empty(n, dtype=dtype, device=device)
+                self.views.clear()
+            ops[name] = pool[:n]
+        ops["q8"] = ops["q8"].view(layout.batch, layout.hq, layout.t, 128)
+        ops["vstat"] = ops["vstat"].view(layout.batch, layout.hk, 3, 128)
+        ops["kp"] = ops.pop("k")
+        ops["packed"] = {code: ops.pop(f"v{code}") for code in (F16, I8, I4)}
+        self.views[(layout, device)] = ops
         return ops
 
     def __call__(self, layer, q, k, v, scale):
@@ -169,21 +194,21 @@ class Prefill:
         self._run(layer, q, k, v, None, attend=False)
 
     def _run(self, layer, q, k, v, scale, attend):
+        """The reference's op sequence (kernels/prefill.py:87-108): quantize Q/K, pack V, attend,
+        then hand the records to the decode cache."""
         batch, hq, t, _ = q.shape
         hk, rows, device = k.shape[1], (t + 63) // 64, q.device
         table = self.table(layer, hq, hk, rows, device)
-        int4 = Q4 in table.formats
         decode = self.decode_cache.codes(rows) if self.decode_cache is not None else None
         formats = table.formats | decode[1] if decode is not None else table.formats
-        ops = self.operands(batch, hq, hk, t, int4, formats, device)
-        ka, kstat, vstat, ka4 = ops["ka"], ops["kstat"], ops["vstat"], ops["ka4"]
-        if decode is not None:
-            ka, kstat, vstat, ka4 = self.kept(layer, batch, hk, rows, int4, device)
+        layout = Layout(batch, hq, hk, t, Q4 in table.formats, frozenset(formats))
+        ops = self.operands(layout, device)
         packed = ops["packed"]
-        self.module.prepare_qk(q, k, ops["q8"], ops["qa"], ops["kp"], ka, ops["partial"], kstat,
-                               ops["q4"], ops["qa4"], ops["k4"], ka4)
-        self.module.pack_v(v, ops["partial"], vstat, packed[F16], packed[I8], packed[I4])
+        self.module.prepare_qk(q, k, ops["q8"], ops["qa"], ops["kp"], ops["ka"], ops["partial"], ops["kstat"],
+                               ops["q4"], ops["qa4"], ops["k4"], ops["ka4"])
+        self.module.pack_v(v, ops["partial"], ops["vstat"], packed[F16], packed[I8], packed[I4])
         exact, nx = self.exact(layer, hq, hk, device)
+        kx = vx = None
         if exact is not None:
             kx, vx = self.exact_records(batch * nx * rows * KX_BYTES, device)
             self.module.pack_exact(k, v, exact, nx, kx, vx)
@@ -191,16 +216,12 @@ class Prefill:
         if attend:
             dtype = self.out_dtype or q.dtype
             out = torch.empty((batch, t, hq, 128), dtype=dtype, device=device).transpose(1, 2)
-            if exact is None:
-                self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4],
-                                      vstat, ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"],
-                                      ka4, out, scale)
-            else:
-                self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4],
-                                      vstat, ops["q8"], ops["kp"], ops["qa"], ka, ops["q4"], ops["k4"], ops["qa4"],
-                                      ka4, out, scale, exact=exact, q=q, kx=kx, vx=vx, nx=nx)
+            extra = {} if exact is None else dict(exact=exact, q=q, kx=kx, vx=vx, nx=nx)
+            self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4],
+                                  ops["vstat"], ops["q8"], ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"],
+                                  ops["qa4"], ops["ka4"], out, scale, **extra)
         if decode is not None:
             exact_kv = sorted(set(int(h) for h in self.bands_fn.bf16(layer))) if exact is not None else []
-            self.decode_cache.store(layer, t, ops["kp"], ka, kstat, vstat, packed, decode[0], table.host,
-                                    ops["k4"], ka4, exact_kv, *(self.records if exact is not None else (None, None)))
+            self.decode_cache.store(layer, t, ops["kp"], ops["ka"], ops["kstat"], ops["vstat"], packed, decode[0],
+                                    table.host, ops["k4"], ops["ka4"], exact_kv, kx, vx)
         return out

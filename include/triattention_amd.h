@@ -105,7 +105,13 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * runs of `per` (the reference's split); otherwise bounds is int32
  * [batch][hk][nsplit + 1] and split s of a head covers entries
  * [bounds[s], bounds[s + 1]) (nondecreasing, bounds[0] = 0, bounds[nsplit] =
- * count, at most 64 entries per split), pm/pl/po then hold splits = nsplit. */
+ * count, at most 64 entries per split), pm/pl/po then hold splits = nsplit.
+ * Task table (extension): tasks NULL, or a table of n_tasks splits that tri_decode_tasks wrote for the
+ * same ka / ka4 / entry / kinfo / count / fmt / slot / per / bounds.  The split kernel then runs only the
+ * listed splits and reads each one's entries, record offsets and K scales from the table (one memory
+ * round trip) instead of gathering them; the partials of splits the table leaves out are not written,
+ * so the caller holds them at the empty partial (pm = -FLT_MAX, pl = 0, po = 0).  Ignored for a cache
+ * with exact heads (xslot set). */
 int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -114,7 +120,7 @@ int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const
                void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
                const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
-               const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
+               const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale,
                void* stream);
 
 /* The two launches of tri_decode separately, same arguments: the split-KV
@@ -130,7 +136,7 @@ int tri_decode_partials(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                         int64_t o_sh, float* pm, float* pl, float* po, const int32_t* prompt, int batch, int hq,
                         int hk, int maxn, int per, int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8,
                         int64_t n_v4, const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
-                        const int32_t* bounds, int nsplit, double scale, void* stream);
+                        const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale, void* stream);
 int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                      const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                      const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -139,7 +145,7 @@ int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c,
                      const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                      float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                      int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
-                     const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
+                     const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale,
                      void* stream);
 
 /* Measurement (no reference counterpart): tri_decode_partials with the split-KV
@@ -156,8 +162,21 @@ int tri_decode_partials_timed(const void* q, int64_t q_sb, int64_t q_sh, const v
                               const int32_t* prompt, int batch, int hq, int hk, int maxn, int per,
                               int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4,
                               const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
-                              const int32_t* bounds, int nsplit, double scale, void* stream, void* ev_start,
+                              const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale, void* stream, void* ev_start,
                               void* ev_stop);
+
+/* No counterpart in the reference: the split kernel's task table for a decode cache's current layout.
+ * Work items are (sequence, KV head, split) of the split tri_decode makes from per / bounds (splits =
+ * nsplit with bounds, else max(1, ceil(maxn / per))), numbered ((sequence * hk) + head) * splits + split.
+ * For the i-th of the n_items items listed in items (int32 on the device; NULL lists every item in
+ * order), 512 int32 at tasks + i * 512: an int4 per lane L (K record byte offset, V record byte
+ * offset, rowmask | INT4-K << 8 | INT8-V << 9 | tile << 10, and the work item in lane 0 / the split's
+ * entry count in the other lanes) for the split's entry L, then a float4 per lane (the tile's K group
+ * scales).  16-byte aligned.  Rebuild it whenever the cache or its split partition changes. */
+int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
+                     const int32_t* count, const int32_t* fmt, const int32_t* slot, int batch, int hk, int maxn,
+                     int per, int tiles_max, const int32_t* bounds, int nsplit, const int32_t* items, int n_items,
+                     int32_t* tasks, void* stream);
 
 /* Replaces the host-side assembly of DecodeCache.store (kernels/decode.py:24-67): one launch appends
  * the decode-cache entries of a Prefill call's batch (batch sequences of t tokens each) as rows row0 ..
@@ -201,7 +220,7 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
                        const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
-                       double scale, void* stream);
+                       const void* tasks, int n_tasks, double scale, void* stream);
 
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */

@@ -54,7 +54,8 @@ def _decode_args(fake, per=8, kcur=None, tst=128):
     kc = kcur if kcur is not None else fake
     return [fake, 24 * 128, 128, fake, None, fake, None, fake, fake, fake, fake, fake, fake, fake, fake, fake,
             fake, fake, 8 * 256 * 128, 256 * tst, tst, 256, kc, kc, 8 * 128, 128, fake, fake, 1, 24 * 128, 128,
-            fake, fake, fake, fake, 1, 24, 8, 64, per, 64, 16, 0, 4, 4, None, None, None, 0, None, 0, 0.088, None]
+            fake, fake, fake, fake, 1, 24, 8, 64, per, 64, 16, 0, 4, 4, None, None, None, 0, None, 0, None, 0,
+            0.088, None]
 
 
 def test_decode_validation_needs_no_gpu():

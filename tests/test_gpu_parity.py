@@ -207,8 +207,9 @@ def test_decode_full_1024_token_tail(module):
 
 
 def test_decode_entries_without_v_format_flags(module):
-    """Entry words without the V-format flags (the reference's plain tile indices) make the kernel
-    read fmt instead; the outputs are bit-identical."""
+    """Without the task table, the split kernel gathers its splits from the metadata rows; entry words
+    without the V-format flags (the reference's plain tile indices) make it read fmt as well.  Both give
+    the task table's outputs bit for bit."""
     from triattention_amd.kernels.decode import ENTRY_TILE
     print("\n[parity] decode with plain tile indices in the entry table", flush=True)
     hq, hk, prompt = 8, 2, 1100
@@ -222,12 +223,20 @@ def test_decode_entries_without_v_format_flags(module):
     dev = torch.device("cuda")
     qd, kd, vd = (S.outlier_tensor(g, 2, hq, 1).to(dev), S.outlier_tensor(g, 2, hk, 1).to(dev),
                   S.outlier_tensor(g, 2, hk, 1).to(dev))
-    flagged = cache(0, qd, kd, vd, 128 ** -0.5).cpu()
+    tasks = cache(0, qd, kd, vd, 128 ** -0.5).cpu()
     e = cache.layers[0]
+    assert "tasks" in e
+    for key in [key for key in e if isinstance(key, tuple) and key[0] == "plan"]:
+        del e[key]
+    cache.tasks = False
+    flagged = cache(0, qd, kd, vd, 128 ** -0.5).cpu()
+    assert torch.equal(tasks.view(torch.int32), flagged.view(torch.int32))
+    for key in [key for key in e if isinstance(key, tuple) and key[0] == "plan"]:
+        del e[key]
     assert bool((e["entry"] != (e["entry"] & ENTRY_TILE)).any())
     e["entry"].bitwise_and_(ENTRY_TILE)
     plain = cache(0, qd, kd, vd, 128 ** -0.5).cpu()
-    assert torch.equal(flagged.view(torch.int32), plain.view(torch.int32))
+    assert torch.equal(tasks.view(torch.int32), plain.view(torch.int32))
 
 
 def test_timed_split_launch_matches_untimed(module):

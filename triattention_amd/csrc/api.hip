@@ -239,8 +239,9 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                        float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
-                       const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, double scale,
-                       void* stream, int phase, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr) {
+                       const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
+                       const void* tasks, int n_tasks, double scale, void* stream, int phase,
+                       hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr) {
   g_error.clear();
   if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
       !ktail || !vtail || !kcur || !vcur || !step || !out || !pm || !pl || !po || !prompt)
@@ -296,6 +297,9 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   d.maxn = maxn;
   d.per = per;
   d.bounds = bounds;
+  // a task table lists the splits to run (exact heads gather their splits themselves)
+  d.tasks = xslot == nullptr ? static_cast<const int32_t*>(tasks) : nullptr;
+  if (d.tasks && (n_tasks < 1 || !aligned(tasks, 16))) return fail("decode: a task table needs n_tasks >= 1, 16-byte aligned");
   d.tiles_max = tiles_max;
   d.splits = splits;
   {
@@ -308,8 +312,10 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
     //   falls with its index, and the affine scatter would load one XCD 2.4x the mean (C3 in runs of
     //   32 tiles: 253 -> 123 us).  An odd launch count L (one padding item), and a multiplier whose
     //   XCD step 8 * scatter mod L is the integer nearest 0.618 L coprime with L.
-    const int64_t items = (int64_t)splits * hk * batch;
-    if (items >= ((int64_t)1 << 31) - 1) return fail("decode: too many splits x heads x sequences");
+    const int64_t all = (int64_t)splits * hk * batch;
+    if (all >= ((int64_t)1 << 31) - 1) return fail("decode: too many splits x heads x sequences");
+    if (d.tasks && n_tasks > all) return fail("decode: the task table lists more splits than exist");
+    const int64_t items = d.tasks ? n_tasks : all;
     const bool pinned = bounds == nullptr && items % 8 == 0 && splits % 2 == 0;
     if (!pinned) {
       const int primes[3] = {1000003, 1000033, 1000037};
@@ -422,7 +428,8 @@ static int noalloc_scratch(float** out) {
 #define TRI_DECODE_ARGS                                                                                      \
   q, q_sb, q_sh, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8c, v4c, vstat, kstat, ktail, vtail, t_sb, t_sh, \
       t_st, max_tail, kcur, vcur, c_sb, c_sh, step, out, out_dtype, o_sb, o_sh, pm, pl, po, prompt, batch, hq, hk,  \
-      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, xslot, kxc, vxc, n_kx, bounds, nsplit, scale, stream
+      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, xslot, kxc, vxc, n_kx, bounds, nsplit, tasks, n_tasks, scale,   \
+      stream
 #define TRI_DECODE_PARAMS                                                                                          \
   const void *q, int64_t q_sb, int64_t q_sh, const void *k8c, const void *k4c, const float *ka, const float *ka4,  \
       const int32_t *entry, const int32_t *kinfo, const int32_t *count, const int32_t *fmt, const int32_t *slot,  \
@@ -431,7 +438,8 @@ static int noalloc_scratch(float** out) {
       int64_t c_sh, const int64_t *step, void *out, int out_dtype, int64_t o_sb, int64_t o_sh, float *pm,          \
       float *pl, float *po, const int32_t *prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,    \
       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t *xslot, const void *kxc,           \
-      const void *vxc, int64_t n_kx, const int32_t *bounds, int nsplit, double scale, void *stream
+      const void *vxc, int64_t n_kx, const int32_t *bounds, int nsplit, const void *tasks, int n_tasks,      \
+      double scale, void *stream
 
 int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
 int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }
@@ -449,7 +457,7 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
                        const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
-                       double scale, void* stream) {
+                       const void* tasks, int n_tasks, double scale, void* stream) {
   g_error.clear();
   if (batch < 1 || hq < 1 || hk < 1 || maxn < 1) return fail("decode_noalloc: empty shape");
   if (!bounds && (per < 1 || per > tri::MAX_PER)) return fail("decode_noalloc: per (tiles per split) must be in [1, 64]");
@@ -471,7 +479,47 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   float* pm = s;
   float* pl = s + pad;
   float* po = s + 2 * pad;
+  if (tasks && xslot == nullptr) {
+    // splits a task table leaves out are never written: the scratch (which holds whatever the last
+    // call left) gets the empty partial in every slot first
+    tri::fill_empty_partials_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        pm, pl, po, n);
+  }
   return decode_impl(TRI_DECODE_ARGS, 3);
+}
+
+int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
+                     const int32_t* count, const int32_t* fmt, const int32_t* slot, int batch, int hk, int maxn,
+                     int per, int tiles_max, const int32_t* bounds, int nsplit, const int32_t* items, int n_items,
+                     int32_t* tasks, void* stream) {
+  g_error.clear();
+  if (!ka || !entry || !kinfo || !count || !fmt || !slot || !tasks) return fail("decode_tasks: null buffer");
+  if (batch < 1 || hk < 1 || maxn < 1 || tiles_max < 1) return fail("decode_tasks: empty shape");
+  if (!bounds && (per < 1 || per > tri::MAX_PER)) return fail("decode_tasks: per (tiles per split) must be in [1, 64]");
+  if (bounds && (nsplit < 1 || nsplit > 65535)) return fail("decode_tasks: nsplit must be in [1, 65535]");
+  if (!aligned(tasks, 16) || !aligned(ka, 16) || (ka4 && !aligned(ka4, 16)))
+    return fail("decode_tasks: the table and the K scales must be 16-byte aligned");
+  const int splits = bounds ? nsplit : std::max(1, (maxn + per - 1) / per);
+  const int64_t all = (int64_t)splits * hk * batch;
+  if (all >= ((int64_t)1 << 31) / tri::TASK_WORDS) return fail("decode_tasks: too many splits x heads x sequences");
+  if (items && (n_items < 1 || n_items > all)) return fail("decode_tasks: n_items must be in [1, splits x hk x batch]");
+  const int64_t listed = items ? n_items : all;
+  tri::DecodeArgs d = {};
+  d.ka = ka;
+  d.ka4 = ka4;
+  d.entry = entry;
+  d.kinfo = kinfo;
+  d.count = count;
+  d.fmt = fmt;
+  d.slot = slot;
+  d.hk = hk;
+  d.maxn = maxn;
+  d.per = per;
+  d.tiles_max = tiles_max;
+  d.bounds = bounds;
+  d.splits = splits;
+  tri::decode_tasks_kernel<<<dim3((unsigned)listed), 64, 0, static_cast<hipStream_t>(stream)>>>(d, items, tasks);
+  return check_launch("decode_tasks");
 }
 
 int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int hq, int hk, int t, int nx,

@@ -55,6 +55,11 @@ struct DecodeArgs {
   // split partition (extension): null for the reference's uniform split of `per` tiles, else
   // [B][Hk][splits + 1] entry bounds, split s of a head covering entries [bounds[s], bounds[s + 1])
   const int32_t* bounds;
+  // task table (extension, may be null): 512 int32 words per listed work item (sequence, KV head,
+  // split): int4 (K record offset, V record offset, flags, w) for lanes 0..63 with w the work item in
+  // lane 0 and the split's entry count in the others, then float4 K group scales for lanes 0..63
+  // (decode_tasks_kernel).  The launch then covers the listed items only (`items` of them).
+  const int32_t* tasks;
 };
 
 constexpr int MAX_TAIL = 1024;
@@ -77,6 +82,52 @@ __device__ __forceinline__ void split_range(const DecodeArgs& a, int64_t hb, int
     first = split * a.per;
     last = min(cnt, first + a.per);
   }
+}
+
+constexpr int OUT_OF_RANGE = (int)0x80000000u;  // a record offset >= any record array size (< 2 GiB)
+constexpr int TASK_WORDS = 512;
+
+// Task table of the split kernel (extension): lane L of work item (sequence, KV head, split) gets
+// entry first + L of the split -- its K and V record byte offsets, rowmask | INT4-K << 8 | INT8-V << 9
+// | tile << 10, the split's entry count, and the tile's four K group scales.  The split kernel then
+// starts streaming a split's records one memory round trip after it starts, instead of three (split
+// bounds, then entry / kinfo / slot, then the records).  Built once per cache layout: the entries and
+// the split partition change only when the cache is stored.
+__global__ __launch_bounds__(64) void decode_tasks_kernel(DecodeArgs a, const int32_t* items, int32_t* tasks) {
+  const int L = threadIdx.x;
+  const int item = items ? items[blockIdx.x] : (int)blockIdx.x;
+  const int split = item % a.splits, kh = (item / a.splits) % a.hk, b = item / (a.splits * a.hk);
+  const int64_t hb = (int64_t)b * a.hk + kh;
+  int first, last;
+  split_range(a, hb, split, first, last);
+  const int n = max(0, last - first);
+  int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, 1 << 9, L == 0 ? item : n);
+  float4 ks = make_float4(1.f, 1.f, 1.f, 1.f);
+  if (L < n) {
+    const int64_t li = hb * a.maxn + min(first + L, a.maxn - 1);
+    const int info = a.kinfo[li], er = a.entry[li], vs = a.slot[li];
+    const int is4 = (info >> 8) & 1;
+    const int j = min(max(er & ENTRY_TILE, 0), a.tiles_max - 1);
+    const int vf = (er & ENTRY_VFMT) ? ((er & ENTRY_V8) ? 1 : 2) : a.fmt[(int64_t)b * a.tiles_max + j];
+    w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
+    w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
+    w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
+    ks = *reinterpret_cast<const float4*>(((is4 && a.ka4) ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
+  }
+  int32_t* t = tasks + (int64_t)blockIdx.x * TASK_WORDS;
+  *reinterpret_cast<int4*>(t + 4 * L) = w;
+  *reinterpret_cast<float4*>(t + 256 + 4 * L) = ks;
+}
+
+// The empty split partial (m = -FLT_MAX, l = 0, o = 0) for n (q-head, split) slots: the partials of the
+// splits a task table leaves out (they hold no kept tile).
+__global__ __launch_bounds__(256) void fill_empty_partials_kernel(float* pm, float* pl, float* po, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    pm[i] = -3.402823466e38f;
+    pl[i] = 0.f;
+  }
+  for (int64_t k = i; k < n * D; k += (int64_t)gridDim.x * 256) po[k] = 0.f;
 }
 
 __device__ __forceinline__ v4i unpack16(v4i w) {
@@ -227,19 +278,31 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   // golden-ratio one with an odd launch count where a plain one would pin split indices to XCDs).
   // Splits share no data but Q, so nothing is lost in L2.
   int split, kh, b;
+  int first, last;
+  int4 task_w = make_int4(0, 0, 0, 0);
+  float4 task_k = make_float4(1.f, 1.f, 1.f, 1.f);
   {
     const int w = (int)(((int64_t)blockIdx.x * a.scatter) % a.launched);
     if (w >= a.items) return;  // the padding item (whole workgroup, before any barrier)
+    int item = w;
+    if (a.tasks != nullptr && !EXACT) {
+      // w-th listed split: its work item, entry count and every entry the prologue needs
+      const int32_t* t = a.tasks + (int64_t)w * TASK_WORDS;
+      task_w = *reinterpret_cast<const int4*>(t + 4 * (threadIdx.x & 63));
+      task_k = *reinterpret_cast<const float4*>(t + 256 + 4 * (threadIdx.x & 63));
+      item = __builtin_amdgcn_readlane(task_w.w, 0);
+      first = 0;
+      last = __builtin_amdgcn_readlane(task_w.w, 1);
+    }
     const int nsplit = a.splits, nkh = a.hk;
-    split = w % nsplit;
-    kh = (w / nsplit) % nkh;
-    b = w / (nsplit * nkh);
+    split = item % nsplit;
+    kh = (item / nsplit) % nkh;
+    b = item / (nsplit * nkh);
   }
   // A split past its head's kept tiles (ragged batches: most splits of the short sequences)
   // writes the empty partial (m = -FLT_MAX, l = 0, o = 0) and leaves.
   const int wv = NW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
-  int first, last;
-  split_range(a, (int64_t)b * a.hk + kh, split, first, last);
+  if (a.tasks == nullptr || EXACT) split_range(a, (int64_t)b * a.hk + kh, split, first, last);
   if (first >= last) {
     if (wv) return;
     const int L = threadIdx.x & 63, g = a.hq / a.hk;
@@ -305,7 +368,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   // zeros without touching memory).  Scalar loads return out of order, so any
   // use of one waits for every outstanding scalar and LDS access; per-tile
   // scalar loads would stall every tile on the metadata of the tiles after it.
-  constexpr int OUT_OF_RANGE = (int)0x80000000u;  // >= any record array size (< 2 GiB)
   struct Meta {
     int info, j, vf, koff, voff;
   };
@@ -367,7 +429,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   Meta mc;  // the split's first tile
   int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);  // koff, voff, info | v8 << 9 | j << 10
   float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
-  {
+  if (a.tasks != nullptr && !EXACT) {
+    // the task table holds this lane's entry ready: the records stream right away
+    w = make_int4(task_w.x, task_w.y, task_w.z, 0);
+    ka = task_k;
+    Meta m0;
+    m0.koff = __builtin_amdgcn_readlane(w.x, wv);
+    m0.info = __builtin_amdgcn_readlane(w.z & 0x1ff, wv);
+    load_k(m0);
+    mc = unpack(int4{__builtin_amdgcn_readlane(w.x, wv), __builtin_amdgcn_readlane(w.y, wv),
+                     __builtin_amdgcn_readlane(w.z, wv), 0});
+    load_v(mc);
+    meta[L] = w;
+    metk[L] = ka;
+    if (L == 0) {
+      meta[MAX_PER] = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);
+      metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+  } else {
     const bool valid = L < last - first;
     // (independent of the split's entry count, so these loads need not wait for it)
     const int64_t li = mbase + min(first + min(L, last - first - 1), a.maxn - 1);

@@ -226,6 +226,9 @@ class DecodeCache:
         self.wave = None
         # None: the balanced split partition; an int: the reference's uniform split of `per` tiles
         self.per = None
+        # the split kernel reads its splits from a task table built once per cache layout (False: it
+        # gathers them from the metadata rows, as the reference's kernel does)
+        self.tasks = True
 
     def codes(self, rows):
         if rows not in self.formats:
@@ -342,9 +345,11 @@ class DecodeCache:
         splits = e["splits"]
         key = ("partials", hq)
         if key not in e:
+            # every slot starts as the empty partial: splits that hold no kept tile are left out of the
+            # launch (the task table lists the others) and keep it
             n = e["batch"] * hq * splits
-            e[key] = (torch.empty(n, device=q.device), torch.empty(n, device=q.device),
-                      torch.empty(n * 128, device=q.device))
+            e[key] = (torch.full((n,), -3.4028234663852886e38, device=q.device), torch.zeros(n, device=q.device),
+                      torch.zeros(n * 128, device=q.device))
         dtype = self.out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=dtype, device=q.device)
         self.plan(layer, q, k, out, scale).run(q, k, v, out)
@@ -356,11 +361,30 @@ class DecodeCache:
         key = ("plan", _geometry(q), _geometry(k), _geometry(out), float(scale))
         if key not in e:
             hq = q.shape[1]
+            if self.tasks and e["xslot"] is None and "tasks" not in e and hasattr(self.module, "decode_tasks"):
+                items = torch.from_numpy(self._task_items(e)).to(q.device)
+                e["tasks"] = self.module.decode_tasks(e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"],
+                                                      e["slot"], e["per"], e["bounds"], items)
             e[key] = self.module.plan_decode(
                 q, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"], e["slot"],
                 e["v"][I8], e["v"][I4], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], k, k, self.step, out,
-                *e[("partials", hq)], e["prompt"], e["per"], scale, e["xslot"], e["kx"], e["vx"], e["bounds"])
+                *e[("partials", hq)], e["prompt"], e["per"], scale, e["xslot"], e["kx"], e["vx"], e["bounds"],
+                e.get("tasks") if self.tasks else None)
         return e[key]
+
+    @staticmethod
+    def _task_items(e):
+        """Work items ((sequence * Hk + head) * splits + split) of the splits that hold kept tiles, from
+        the host metadata: a split of the balanced partition is empty when its bounds coincide, one of
+        the uniform runs when it starts past its head's count."""
+        counts = np.concatenate([np.repeat(g["meta"]["count"].numpy()[None], g["batch"], 0) for g in e["groups"]])
+        if e["bounds_host"] is not None:
+            b = e["bounds_host"]
+            nonempty = b[:, :, 1:] > b[:, :, :-1]
+        else:
+            nonempty = np.arange(e["splits"])[None, None, :] * e["per"] < counts[:, :, None]
+        items = np.flatnonzero(nonempty.reshape(-1)).astype(np.int32)
+        return items if items.size else np.zeros(1, np.int32)
 
     def split_of(self, layer, b):
         """The split argument of the oracle's decode for sequence b of the layer: its bounds

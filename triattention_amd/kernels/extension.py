@@ -37,8 +37,9 @@ K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
            "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_noalloc",
-           "tri_cache_store", "tri_decode_occupancy", "tri_device_cus")
+           "tri_decode_tasks", "tri_cache_store", "tri_decode_occupancy", "tri_device_cus")
 KX_BYTES = 16384
+TASK_WORDS = 512  # int32 words of the decode task table per (sequence, KV head, split)
 
 
 def build(arch: str = "gfx950") -> Path:
@@ -63,12 +64,13 @@ def load_library() -> ctypes.CDLL:
     lib.tri_pack_exact.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I, P, I, P, P, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64,
-                   P, P, P, I64, P, I, D_, P]
+                   P, P, P, I64, P, I, P, I, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
         getattr(lib, name).argtypes = decode_args
     lib.tri_decode_partials_timed.argtypes = decode_args + [P, P]
     # tri_decode without pm / pl / po (arguments 31-33 of tri_decode)
     lib.tri_decode_noalloc.argtypes = decode_args[:31] + decode_args[34:]
+    lib.tri_decode_tasks.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P, I, P, I, P, P]
     lib.tri_cache_store.argtypes = [P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P,
                                     P, P, P, P, P, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, P, I64, I64,
                                     P]
@@ -224,10 +226,12 @@ class Module:
 
     def plan_decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail,
                     kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot=None, kxc=None, vxc=None,
-                    bounds=None):
+                    bounds=None, tasks=None):
         """Validate and marshal every argument of ``decode`` once (extension).  The returned
         plan's ``run(q, kcur, vcur, out, phase)`` launches with new q / k / v / out tensors of the
-        planned shapes and strides and the same cache, at a few microseconds of host time."""
+        planned shapes and strides and the same cache, at a few microseconds of host time.
+        ``tasks``: (table, listed splits) as ``decode_tasks`` returns it for this cache and split, or None;
+        the caller keeps the partials of the splits it leaves out empty."""
         _check(q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(2) == 1 and q.size(3) == D and q.stride(3) == 1,
                "q [B,Hq,1,128]")
         b, hq = q.size(0), q.size(1)
@@ -287,6 +291,11 @@ class Module:
             _check(t is None or (t.is_cuda and t.device == q.device and contiguous),
                    f"decode: {name} must be a{'' if name in ('q', 'k', 'tail', 'out') else ' contiguous'} tensor "
                    f"on q's device")
+        table, n_tasks = tasks if tasks is not None else (None, 0)
+        if table is not None:
+            _check(table.dtype == torch.int32 and table.is_cuda and table.is_contiguous() and
+                   1 <= n_tasks <= b * hk * splits and table.numel() == n_tasks * TASK_WORDS,
+                   "decode: task table int32 [n_tasks*512], at most one task per split")
         kc = kcur.view(b, hk, -1, D) if kcur.dim() == 4 else kcur
         args = [0, q.stride(0), q.stride(1), _ptr(k8c), _ptr(k4c), _ptr(ka),
                 _ptr(ka4), _ptr(entry), _ptr(kinfo), _ptr(count), _ptr(fmt), _ptr(slot), _ptr(v8), _ptr(v4),
@@ -296,10 +305,31 @@ class Module:
                 _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, k8c.size(0),
                 0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), _ptr(xslot), _ptr(kxc),
                 _ptr(vxc), 0 if kxc is None else kxc.numel() * kxc.element_size() // KX_BYTES, _ptr(bounds),
-                splits if bounds is not None else 0, float(scale), 0]
+                splits if bounds is not None else 0, _ptr(table), int(n_tasks), float(scale), 0]
         keep = (k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, step, pm, pl,
-                po, prompt_t, xslot, kxc, vxc, bounds)
+                po, prompt_t, xslot, kxc, vxc, bounds, table)
         return DecodePlan(self, args, q, kcur, out, keep)
+
+    def decode_tasks(self, ka, ka4, entry, kinfo, count, fmt, slot, per, bounds=None, items=None):
+        """The split kernel's task table for a decode cache and its split (extension): (int32
+        [n*512], n) for the work items ``items`` (int32 on the device; None: every split)."""
+        b, hk, maxn = entry.shape
+        tiles_max = fmt.numel() // b
+        splits = bounds.size(2) - 1 if bounds is not None else max(1, -(-maxn // int(per)))
+        _check(entry.dtype == kinfo.dtype == slot.dtype == count.dtype == fmt.dtype == torch.int32 and
+               kinfo.shape == entry.shape and slot.shape == entry.shape and count.numel() == b * hk and
+               ka.numel() == b * hk * tiles_max * 4 and (ka4 is None or ka4.numel() == ka.numel()),
+               "decode_tasks: cache metadata")
+        n = b * hk * splits if items is None else items.numel()
+        _check(items is None or (items.dtype == torch.int32 and items.is_cuda and 1 <= n <= b * hk * splits),
+               "decode_tasks: items int32 on the device, at most one per split")
+        table = torch.empty(n * TASK_WORDS, dtype=torch.int32, device=entry.device)
+        with torch.cuda.device(entry.device):
+            self._call(self.lib.tri_decode_tasks, _ptr(ka), _ptr(ka4), _ptr(entry), _ptr(kinfo), _ptr(count),
+                       _ptr(fmt), _ptr(slot), b, hk, maxn, int(per), tiles_max, _ptr(bounds),
+                       splits if bounds is not None else 0, _ptr(items), n if items is not None else 0, _ptr(table),
+                       self._stream(entry.device))
+        return table, n
 
     def cache_store(self, bands, exact, t, kp, k4p, ka, ka4, kstat, vstat, v8p, v4p, kx, vx, nx, row0, dst, used,
                     cap):
@@ -371,7 +401,7 @@ def _geometry(t):
 class DecodePlan:
     """A validated, marshalled ``decode`` call; ``run`` swaps in the per-step tensors."""
 
-    Q, QSB, QSH, KC, VC, KSB, KSH, OUT, STREAM = 0, 1, 2, 22, 23, 24, 25, 27, 52
+    Q, QSB, QSH, KC, VC, KSB, KSH, OUT, STREAM = 0, 1, 2, 22, 23, 24, 25, 27, 54
 
     def __init__(self, module, args, q, kcur, out, keep):
         self.module, self.args, self.keep = module, args, keep

@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 K8, K4, V8, V4 = 8192, 4096, 8192, 4096
 
 
@@ -333,6 +334,95 @@ def calibration_sweep(args):
                    "shared_scratch_bytes": r["shared_scratch_bytes"], "parallelism": "single GPU"}}))
 
 
+def prefill_only(args):
+    """--only prefill / c2: the prefill figures alone (C0 and C2, or the C2 attention launch repeated),
+    so that a profiler's trace or counters cover nothing else."""
+    import torch
+
+    from triattention_amd import synthetic as S
+    from triattention_amd.kernels.extension import load_extension
+    from triattention_amd.kernels.prefill import Prefill
+    from triattention_amd.maps import from_bands
+
+    module = load_extension()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    cases = [("C0", S.config0, 20)] if args.only == "prefill" else []
+    cases.append(("C2", S.config2, 5 if args.only == "prefill" else args.steps))
+    out = {}
+    for name, make, reps in cases:
+        cfg = make()
+        if name == "C0":
+            cfg["kinds"] = []
+        out[name] = prefill_case(module, dev, stream, name, cfg, reps, Prefill, from_bands, full_call=args.only == "prefill")
+    print(json.dumps({"prefill": out}))
+
+
+def prefill_case(module, dev, stream, name, cfg, reps, Prefill, from_bands, full_call=True):
+    """Attention-kernel time (HIP events over ``reps`` launches) and the full Prefill call of one config."""
+    import torch
+    q0, k0, v0 = cfg["q"].to(dev), cfg["k"].to(dev), cfg["v"].to(dev)
+    b, hq0, t, _ = q0.shape
+    hk0 = k0.shape[1]
+    bf16_kv = [h for h, kind in enumerate(cfg["kinds"]) if kind == "bf16"]
+    fn = from_bands({"0": cfg["bands"].tolist()}, bf16={"0": bf16_kv} if bf16_kv else None)
+    pre0 = Prefill(module, fn)
+    pre0(0, q0, k0, v0, cfg["scale"])
+    ops = next(iter(pre0.views.values()))
+    table = next(iter(pre0.tables.values()))
+    exact, nx = pre0.exact(0, hq0, hk0, dev)
+    kx, vx = pre0.records if exact is not None else (None, None)
+    outp = torch.empty((b, t, hq0, 128), dtype=torch.bfloat16, device=dev).transpose(1, 2)
+    pk = ops["packed"]
+
+    def attn():
+        module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
+                         ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], outp,
+                         cfg["scale"], exact=exact, q=q0, kx=kx, vx=vx, nx=nx)
+
+    # untimed calls until ~0.5 s of this workload has run: the clocks rise under sustained
+    # load (C2's first calls are ~17% slower than its tenth)
+    t_warm = time.perf_counter()
+    n_warm = 0
+    while n_warm < 2 or time.perf_counter() - t_warm < 0.5:
+        attn()
+        torch.cuda.synchronize()
+        n_warm += 1
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a0.record(stream)
+    for _ in range(reps):
+        attn()
+    a1.record(stream)
+    torch.cuda.synchronize()
+    att_ms = a0.elapsed_time(a1) / reps
+    full_ms = float("nan")
+    if full_call:
+        w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0.record(stream)
+        for _ in range(reps):
+            pre0(0, q0, k0, v0, cfg["scale"])
+        w1.record(stream)
+        torch.cuda.synchronize()
+        full_ms = w0.elapsed_time(w1) / reps
+    # every head keeps all causal pairs here (INT8 / INT4 / bf16 bands skip no tiles)
+    ops_alg = b * hq0 * 4 * 128 * (t * (t + 1) // 2)
+    tops = ops_alg / (att_ms * 1e-3) / 1e12
+    # mixed bound: QK of the quantized heads at the int8 peak, their PV and every exact head's QK and PV
+    # at the bf16 / fp16 peak (the quantized PV runs on int8 MFMA, but its semantics are a u8 x s8 product
+    # that the bf16 peak also prices)
+    nq = sum(1 for kind in cfg["kinds"] for _ in range(hq0 // hk0) if kind != "bf16") if cfg["kinds"] else hq0
+    per_head = ops_alg / hq0
+    mixed_us = (nq * per_head / 2 / (INT8_PEAK_TOPS * 1e12) + nq * per_head / 2 / (BF16_PEAK_TFLOPS * 1e12) +
+                (hq0 - nq) * per_head / (BF16_PEAK_TFLOPS * 1e12)) * 1e6
+    log(f"prefill {name}: attention {att_ms * 1e3:.1f} us = {tops:.1f} int8-TOPS, full call {full_ms * 1e3:.1f} us")
+    return {"attention_us": round(att_ms * 1e3, 2), "prefill_call_us": round(full_ms * 1e3, 2),
+            "algorithmic_ops": ops_alg, "int8_tops": round(tops, 2),
+            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+            "mixed_bound_us": round(mixed_us, 2), "frac_mixed_bound": round(mixed_us / (att_ms * 1e3), 4),
+            "tokens_per_s": round(b * t / (full_ms * 1e-3), 1) if full_call else None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -344,6 +434,9 @@ def main():
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="leave out the C4 generation from the default run")
     ap.add_argument("--no-calibrate", action="store_true", help="leave out the calibration sweep from the default run")
+    ap.add_argument("--only", choices=("prefill", "c2"),
+                    help="run one workload alone and print its figures (for profilers): 'prefill' = C0 and C2, "
+                         "'c2' = the C2 attention launch")
     ap.add_argument("--c4", action="store_true", help="run the C4 end-to-end generation instead")
     ap.add_argument("--calibrate", action="store_true", help="time the calibration sweep's Prefill executors instead")
     args = ap.parse_args()
@@ -360,6 +453,9 @@ def main():
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
+    if args.only:
+        prefill_only(args)
+        return
 
     import numpy as np
     import torch
@@ -526,62 +622,10 @@ def main():
 
     # ----------------------------------------------------------------- prefill
     if not args.no_prefill:
-        def prefill_case(name, cfg, reps):
-            q0, k0, v0 = cfg["q"].to(dev), cfg["k"].to(dev), cfg["v"].to(dev)
-            b, hq0, t, _ = q0.shape
-            hk0 = k0.shape[1]
-            bf16_kv = [h for h, kind in enumerate(cfg["kinds"]) if kind == "bf16"]
-            fn = from_bands({"0": cfg["bands"].tolist()}, bf16={"0": bf16_kv} if bf16_kv else None)
-            pre0 = Prefill(module, fn)
-            pre0(0, q0, k0, v0, cfg["scale"])
-            ops = next(iter(pre0.views.values()))
-            table = next(iter(pre0.tables.values()))
-            exact, nx = pre0.exact(0, hq0, hk0, dev)
-            kx, vx = pre0.records if exact is not None else (None, None)
-            outp = torch.empty((b, t, hq0, 128), dtype=torch.bfloat16, device=dev).transpose(1, 2)
-            pk = ops["packed"]
-
-            def attn():
-                module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
-                                 ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], outp,
-                                 cfg["scale"], exact=exact, q=q0, kx=kx, vx=vx, nx=nx)
-
-            # untimed calls until ~0.5 s of this workload has run: the clocks rise under sustained
-            # load (C2's first calls are ~17% slower than its tenth)
-            t_warm = time.perf_counter()
-            n_warm = 0
-            while n_warm < 2 or time.perf_counter() - t_warm < 0.5:
-                attn()
-                torch.cuda.synchronize()
-                n_warm += 1
-            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            a0.record(stream)
-            for _ in range(reps):
-                attn()
-            a1.record(stream)
-            torch.cuda.synchronize()
-            att_ms = a0.elapsed_time(a1) / reps
-            w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            w0.record(stream)
-            for _ in range(reps):
-                pre0(0, q0, k0, v0, cfg["scale"])
-            w1.record(stream)
-            torch.cuda.synchronize()
-            full_ms = w0.elapsed_time(w1) / reps
-            # every head keeps all causal pairs here (INT8 / INT4 / bf16 bands skip no tiles)
-            ops_alg = b * hq0 * 4 * 128 * (t * (t + 1) // 2)
-            tops = ops_alg / (att_ms * 1e-3) / 1e12
-            log(f"prefill {name}: attention {att_ms * 1e3:.1f} us = {tops:.1f} int8-TOPS, full call {full_ms * 1e3:.1f} us")
-            return {"attention_us": round(att_ms * 1e3, 2), "prefill_call_us": round(full_ms * 1e3, 2),
-                    "algorithmic_ops": ops_alg, "int8_tops": round(tops, 2),
-                    "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                    "tokens_per_s": round(b * t / (full_ms * 1e-3), 1)}
-
         log("prefill C0")
         c0 = S.config0()
         c0["kinds"] = []
-        r0 = prefill_case("C0", c0, 20)
+        r0 = prefill_case(module, dev, stream, "C0", c0, 20, Prefill, from_bands)
         r0["workload"] = "C0 prefill: batch 1, Hq 24 / Hk 8, T 1024, 50/50 INT8/INT4 KV heads"
         if not args.no_cpu:
             import oracle as O
@@ -601,7 +645,7 @@ def main():
             log(f"CPU oracle C0 prefill: {cpu_ms:.1f} ms per call ({threads} threads)")
         log("prefill C2 (generating 4 x 8192 tokens)")
         c2 = S.config2()
-        r2 = prefill_case("C2", c2, 5)
+        r2 = prefill_case(module, dev, stream, "C2", c2, 5, Prefill, from_bands)
         r2["workload"] = (f"C2 prefill: batch 4, Hq 28 / Hk 4, T 8192, log-uniform channel scales, KV heads "
                           f"{c2['kinds']}")
         result["prefill"] = {"C0": r0, "C2": r2}

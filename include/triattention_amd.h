@@ -111,7 +111,12 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * listed splits and reads each one's entries, record offsets and K scales from the table (one memory
  * round trip) instead of gathering them; the partials of splits the table leaves out are not written,
  * so the caller holds them at the empty partial (pm = -FLT_MAX, pl = 0, po = 0).  Ignored for a cache
- * with exact heads (xslot set). */
+ * with exact heads (xslot set).
+ * Tail growth (extension): tail_base NULL keeps the reference's tail (it holds step tokens before the
+ * new one, and past max_tail - 1 the new token overwrites the last slot, common_device.cuh:384);
+ * otherwise int64 on the device, the tokens tri_tail_spill has moved from the tail into the cache since
+ * the store, and the tail holds step - *tail_base tokens.  Tiles past a sequence's prompt tiles
+ * (ceil(prompt / 64)) hold 64 valid keys each. */
 int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -120,7 +125,7 @@ int tri_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const
                void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl, float* po,
                const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
-               const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale,
+               const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, const int64_t* tail_base, double scale,
                void* stream);
 
 /* The two launches of tri_decode separately, same arguments: the split-KV
@@ -136,7 +141,7 @@ int tri_decode_partials(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                         int64_t o_sh, float* pm, float* pl, float* po, const int32_t* prompt, int batch, int hq,
                         int hk, int maxn, int per, int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8,
                         int64_t n_v4, const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
-                        const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale, void* stream);
+                        const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, const int64_t* tail_base, double scale, void* stream);
 int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                      const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                      const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,
@@ -145,7 +150,7 @@ int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c,
                      const int64_t* step, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, float* pm, float* pl,
                      float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                      int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot, const void* kxc,
-                     const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale,
+                     const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, const int64_t* tail_base, double scale,
                      void* stream);
 
 /* Measurement (no reference counterpart): tri_decode_partials with the split-KV
@@ -162,7 +167,7 @@ int tri_decode_partials_timed(const void* q, int64_t q_sb, int64_t q_sh, const v
                               const int32_t* prompt, int batch, int hq, int hk, int maxn, int per,
                               int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4,
                               const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
-                              const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, double scale, void* stream, void* ev_start,
+                              const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, const int64_t* tail_base, double scale, void* stream, void* ev_start,
                               void* ev_stop);
 
 /* No counterpart in the reference: the split kernel's task table for a decode cache's current layout.
@@ -185,7 +190,9 @@ int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, co
  * Sources (the Prefill outputs): kp / k4p K8 / K4 records, v8p / v4p V8 / V4 records [batch][hk][tiles],
  * ka / ka4 f32 [batch][hk][tiles][4], kstat / vstat f32 [batch][hk][3][128]; k4p / ka4 / v4p may be NULL
  * when no tile needs them.  exact: NULL, or int32 [hk] on the device, -1 for a quantized KV head and
- * otherwise the head's slot (< nx) in kx / vx [batch][nx][tiles] (16 KiB bf16 records, tri_pack_exact).
+ * otherwise the head's slot (< nx) in kx / vx [batch][nx][tiles] (16 KiB bf16 records, tri_pack_exact);
+ * in kxc / vxc each (sequence, exact head) takes xstride >= tiles records (room for tiles that
+ * tri_tail_spill appends).
  * Destinations, as tri_decode reads them: entry / kinfo / slot [rows][hk][maxn] (entries past a head's
  * count zero), count [rows][hk], fmt [rows][tiles_max] (1 = INT8 V, 2 = INT4 V, 1 past the prompt),
  * prompt [rows], xslot [rows][hk] (may be NULL without exact heads), ka_c / ka4_c [rows][hk][tiles_max][4]
@@ -195,7 +202,7 @@ int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, co
  * k4c / v4c NULL with capacity 0 when absent).  Within a sequence, records are numbered in (KV head,
  * entry) order and each sequence takes as many as its metadata selects, after the previous sequence's. */
 int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int hq, int hk, int t, int nx,
-                    const void* kp, const void* k4p, const float* ka, const float* ka4, const float* kstat,
+                    int xstride, const void* kp, const void* k4p, const float* ka, const float* ka4, const float* kstat,
                     const float* vstat, const void* v8p, const void* v4p, const void* kx, const void* vx, int row0,
                     int rows, int maxn, int tiles_max, int32_t* entry, int32_t* kinfo, int32_t* slot, int32_t* count,
                     int32_t* fmt, int32_t* prompt, int32_t* xslot, float* ka_c, float* ka4_c, float* kstat_c,
@@ -220,7 +227,30 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
                        const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
-                       const void* tasks, int n_tasks, double scale, void* stream);
+                       const void* tasks, int n_tasks, const int64_t* tail_base, double scale, void* stream);
+
+/* No counterpart in the reference, which overwrites the tail's last slot once max_tail tokens are
+ * generated (common_device.cuh:384): tail growth for one layer's decode cache, launched before each of
+ * the layer's tri_decode calls.  When the tail holds max_tail tokens (*step - tail_base[0] >= max_tail,
+ * max_tail >= 64), the oldest 64 tail tokens of every (sequence, KV head) become a new tile of the cache
+ * and the tail moves up by 64 slots; tail_base[0] then grows by 64 (int64 [2] on the device, zero at the
+ * store; tail_base[1] is the kernel's own counter and must stay zero between launches).  Otherwise
+ * nothing is written.  The new tile is tile ceil(prompt / 64) + tail_base[0] / 64 of its sequence,
+ * quantized with the prompt's statistics (INT8 or INT4 K with four group scales, INT8 V) and classified
+ * as the newest tile of the cache; an exact head (xslot >= 0) stores KX / VX records at xslot + tile.
+ * grow int32 [rows][hk][4] per (sequence, KV head): the new tile's kinfo bits (rowmask | INT4 K << 8,
+ * or -1 when no q-head keeps it), the K and V record slots of its first spilled tile (spill n uses
+ * slot + n), and the task-table row of its first growth split (-1: none; growth split i holds spilled
+ * tiles 64 i .. 64 i + 63 as entries count0 + 64 i ...).  cap: spilled tiles per head that the arrays
+ * have room for (when full, nothing moves and the tail clamps as the reference's does).  The metadata
+ * arrays, K scales and records are the cache's, as tri_decode reads them; tasks (may be NULL) is its
+ * task table. */
+int tri_tail_spill(const int64_t* step, int64_t* tail_base, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh,
+                   int64_t t_st, int max_tail, int rows, int hk, int maxn, int tiles_max, const int32_t* grow, int cap,
+                   const int32_t* prompt, const int32_t* xslot, int32_t* entry, int32_t* kinfo, int32_t* slot,
+                   int32_t* count, int32_t* fmt, float* ka, float* ka4, const float* kstat, const float* vstat,
+                   void* k8c, int64_t n_k8, void* k4c, int64_t n_k4, void* v8c, int64_t n_v8, void* kxc, void* vxc,
+                   int64_t n_kx, int32_t* tasks, int n_tasks, void* stream);
 
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */

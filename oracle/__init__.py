@@ -64,14 +64,14 @@ def lib():
         L.ora_decode_state.argtypes = [I, I, I, I]
         L.ora_decode_vfmt.restype = I
         L.ora_decode_vfmt.argtypes = [I, I]
-        L.ora_decode.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I, P]
+        L.ora_decode.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I, I, P]
         L.ora_num_threads.restype = I
         L.ora_set_mutation.argtypes = [I]
         L.ora_prefill_rows.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, P, I64, P, I]
         L.ora_prefill_trace.restype = I
         L.ora_prefill_trace.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, I, I, I, P, P, P, P, P, P, P]
         L.ora_decode_trace.restype = I
-        L.ora_decode_trace.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I,
+        L.ora_decode_trace.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I, I,
                                        I, I, P, P, P, P, P, P, P, P, P, P, P]
         _lib = L
     return _lib
@@ -275,7 +275,7 @@ def set_mutation(value: int) -> None:
 
 
 MUTATIONS = dict(no_margin=1, no_half=2, dither_byte=3, no_rel_margin=4, bq_levels=5, v4_restore=6, no_dither=7,
-                 slope_group=8)
+                 slope_group=8, grown_mask=9, grown_state=10)
 
 
 def prefill(q_bits, k_bits, v_bits, bands, scale: float, decode_cache: bool = False, threads: int = 0):
@@ -291,13 +291,38 @@ def decode_state(w8, w4, tiles, j):
     return lib().ora_decode_state(int(w8), int(w4), int(tiles), int(j))
 
 
-def decode(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vtail, kcur, vcur, step: int):
+def _operands(codes, grown):
+    """The decode's code arrays: the prompt's, followed per KV head by the tiles taken from the tail
+    (``grown``: tail_tile dicts, oldest first), and the tiles per head in them."""
+    hk = codes["kstat"].shape[0]
+    tiles = codes["k8"].shape[1] // BN
+    grown = list(grown or [])
+    if not grown:
+        ops = {n: codes[n] for n in ("k8", "ka", "k4", "ka4", "v8", "v4")}
+        return ops, tiles
+    n = len(grown)
+    cat = lambda name, prompt_part: np.ascontiguousarray(
+        np.concatenate([prompt_part] + [t[name] for t in grown], axis=1))
+    zeros = lambda: np.zeros((hk, tiles * BN, D), np.int8)
+    ones = lambda: np.ones((hk, tiles, 4), np.float32)
+    ops = dict(k8=cat("k8", codes["k8"]), ka=cat("ka", codes["ka"]),
+               k4=cat("k4", codes["k4"] if codes["k4"] is not None else zeros()),
+               ka4=cat("ka4", codes["ka4"] if codes["ka4"] is not None else ones()),
+               v8=cat("v8", codes["v8"] if codes["v8"] is not None else zeros()),
+               v4=np.concatenate([codes["v4"] if codes["v4"] is not None else zeros(),
+                                  np.zeros((hk, n * BN, D), np.int8)], axis=1))
+    return ops, tiles + n
+
+
+def decode(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vtail, kcur, vcur, step: int, grown=None):
     """fp32 output [Hq, 128] of one decode step of one sequence.
 
     ``codes`` holds the prompt's prefill operands (k8/ka/k4/ka4/v8/v4/kstat/vstat);
     q_bits [Hq,128], ktail/vtail [Hk,max_tail,128], kcur/vcur [Hk,128] are uint16 bf16 bits.
     ``per`` is the uniform split size (common_host.cuh:55), or an int [Hk, splits+1] array of
-    per-head split bounds (the product's balanced partition, an extension).
+    per-head split bounds (the product's balanced partition, an extension).  ``step`` is the number
+    of tokens the tail holds before this one.  ``grown`` (extension): the tiles taken from a full tail
+    so far (tail_tile results, oldest first), which follow the prompt's tiles.
     """
     if np.ndim(per) == 0:
         bounds, nsplit, per = None, 0, int(per)
@@ -310,19 +335,20 @@ def decode(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vtail, k
     out = np.empty((hq, D), np.float32)
     ktail = _c(ktail, np.uint16)
     vtail = _c(vtail, np.uint16)
+    ops, ctiles = _operands(codes, grown)
     dummy = np.zeros((1,), np.int8)
-    v4 = codes["v4"] if codes["v4"] is not None else dummy
-    v8 = codes["v8"] if codes["v8"] is not None else dummy
+    v4 = ops["v4"] if ops["v4"] is not None else dummy
+    v8 = ops["v8"] if ops["v8"] is not None else dummy
     lib().ora_decode(hq, hk, int(prompt), _p(b), int(per), sm_log2(scale), _p(_c(q_bits, np.uint16)),
-                     _p(codes["k8"]), _p(codes["ka"]), _p(codes["k4"]), _p(codes["ka4"]), _p(v8), _p(v4),
+                     _p(ops["k8"]), _p(ops["ka"]), _p(ops["k4"]), _p(ops["ka4"]), _p(v8), _p(v4),
                      _p(codes["vstat"]), _p(codes["kstat"]), _p(ktail), _p(vtail), int(ktail.shape[1]),
                      _p(_c(kcur, np.uint16)), _p(_c(vcur, np.uint16)), int(step),
-                     None if bounds is None else _p(bounds), int(nsplit), _p(out))
+                     None if bounds is None else _p(bounds), int(nsplit), int(ctiles), _p(out))
     return out
 
 
 def decode_trace(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vtail, kcur, vcur, step: int,
-                 qh: int):
+                 qh: int, grown=None):
     """``decode`` for q-head ``qh`` with its record: per kept tile (split order) col, kind (K width 8/4 |
     V format << 4), split, m, base, bq, p [tiles, 64]; the split partials pm, pl, po [splits, 128]; out."""
     if np.ndim(per) == 0:
@@ -334,10 +360,10 @@ def decode_trace(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vt
         splits = nsplit
     hq = q_bits.shape[0]
     b = _c(bands, np.int32).reshape(hq, 2)
-    tiles = (int(prompt) + BN - 1) // BN
-    cap = max(1, tiles)
+    ops, ctiles = _operands(codes, grown)
+    cap = max(1, ctiles)
     if splits is None:
-        splits = max(1, -(-tiles // per))
+        splits = max(1, -(-ctiles // per))
     col, kind, split = np.zeros(cap, np.int32), np.zeros(cap, np.int32), np.zeros(cap, np.int32)
     m, base, bq = np.zeros(cap, np.float32), np.zeros(cap, np.float32), np.zeros(cap, np.float32)
     p = np.zeros((cap, BN), np.int32)
@@ -345,18 +371,61 @@ def decode_trace(codes, bands, q_bits, prompt: int, per, scale: float, ktail, vt
     out = np.zeros(D, np.float32)
     ktail, vtail = _c(ktail, np.uint16), _c(vtail, np.uint16)
     dummy = np.zeros((1,), np.int8)
-    v4 = codes["v4"] if codes["v4"] is not None else dummy
-    v8 = codes["v8"] if codes["v8"] is not None else dummy
+    v4 = ops["v4"] if ops["v4"] is not None else dummy
+    v8 = ops["v8"] if ops["v8"] is not None else dummy
     q = _c(q_bits, np.uint16)
     kc, vc = _c(kcur, np.uint16), _c(vcur, np.uint16)
     n = lib().ora_decode_trace(hq, codes["kstat"].shape[0], int(prompt), _p(b), int(per), sm_log2(scale), _p(q),
-                               _p(codes["k8"]), _p(codes["ka"]), _p(codes["k4"]), _p(codes["ka4"]), _p(v8), _p(v4),
+                               _p(ops["k8"]), _p(ops["ka"]), _p(ops["k4"]), _p(ops["ka4"]), _p(v8), _p(v4),
                                _p(codes["vstat"]), _p(codes["kstat"]), _p(ktail), _p(vtail), int(ktail.shape[1]),
                                _p(kc), _p(vc), int(step), None if bounds is None else _p(bounds), int(nsplit),
-                               int(qh), cap, _p(col), _p(kind), _p(split), _p(m), _p(base), _p(bq), _p(p), _p(pm),
-                               _p(pl), _p(po), _p(out))
+                               int(ctiles), int(qh), cap, _p(col), _p(kind), _p(split), _p(m), _p(base), _p(bq),
+                               _p(p), _p(pm), _p(pl), _p(po), _p(out))
     return dict(col=col[:n], kind=kind[:n], split=split[:n], m=m[:n], base=base[:n], bq=bq[:n], p=p[:n], pm=pm,
                 pl=pl, po=po, out=out)
+
+
+# ------------------------------------------------------------- tail growth
+def tail_tile(k_bits, v_bits, kstat, vstat):
+    """Codes of one tile taken from a full tail (extension): the 64 oldest tail rows k_bits / v_bits
+    [Hk, 64, 128] (uint16 bf16 bits) quantized with the prompt's statistics, as the prompt's tiles
+    are (INT8 and INT4 K with group scales, INT8 V)."""
+    k8, ka, k4, ka4 = quantize_k(k_bits, kstat, True)
+    _, v8, _ = pack_v(v_bits, vstat, want16=False, want8=True, want4=False)
+    return dict(k8=k8, ka=ka, k4=k4, ka4=ka4, v8=v8)
+
+
+class GrowingTail:
+    """Decode of one sequence with tail growth (extension; the reference overwrites the tail's last
+    slot once it holds max_tail tokens, common_device.cuh:384).  Before a step whose tail is full,
+    its 64 oldest rows become a tile of the cache (tail_tile) and the rest move up by 64 slots; the
+    step then attends over the prompt's tiles, the tiles taken so far and the tail, and appends its
+    own k / v to the tail."""
+
+    def __init__(self, codes, bands, prompt: int, max_tail: int):
+        hk = codes["kstat"].shape[0]
+        self.codes, self.bands, self.prompt, self.max_tail = codes, bands, int(prompt), int(max_tail)
+        self.ktail = np.zeros((hk, max_tail, D), np.uint16)
+        self.vtail = np.zeros((hk, max_tail, D), np.uint16)
+        self.held = 0
+        self.grown = []
+
+    def step(self, q_bits, kcur, vcur, per, scale: float, compute: bool = True):
+        """The fp32 output [Hq, 128] of one step (q_bits [Hq,128], kcur / vcur [Hk,128] bf16 bits); with
+        ``compute`` False only the state moves on (None is returned)."""
+        if self.max_tail >= BN and self.held >= self.max_tail:
+            self.grown.append(tail_tile(self.ktail[:, :BN], self.vtail[:, :BN], self.codes["kstat"],
+                                        self.codes["vstat"]))
+            self.ktail[:, :self.max_tail - BN] = self.ktail[:, BN:].copy()
+            self.vtail[:, :self.max_tail - BN] = self.vtail[:, BN:].copy()
+            self.held -= BN
+        out = decode(self.codes, self.bands, q_bits, self.prompt, per, scale, self.ktail, self.vtail, kcur, vcur,
+                     self.held, grown=self.grown) if compute else None
+        slot = min(self.held, self.max_tail - 1)
+        self.ktail[:, slot] = _c(kcur, np.uint16)
+        self.vtail[:, slot] = _c(vcur, np.uint16)
+        self.held = slot + 1
+        return out
 
 
 def num_threads() -> int:

@@ -15,6 +15,8 @@
  *   ora_prefill       cuda/prefill_sm80.cu:244-488      (scaled_row_max, tile_base_margin, run_task)
  *   ora_decode        cuda/common_device.cuh:178-469    (decode_tile, decode_kernel, decode_merge_kernel)
  *                     kernels/decode.py:17-67           (tile states, kept-tile lists, V recency rule)
+ *   grown_state/vfmt  extension, no reference counterpart: tiles taken from a full tail after the
+ *                     prompt's (the reference overwrites the tail's last slot, common_device.cuh:384)
  *
  * Arithmetic conventions (the defined semantics that the HIP kernels match):
  *  - IEEE-754 binary32 with round-to-nearest-even and denormals kept.  The
@@ -332,6 +334,8 @@ enum {
   MUT_V4_RESTORE = 6,    /* INT4-V tiles weighted by bq, without the 127/7 restore */
   MUT_NO_DITHER = 7,     /* decode P levels without the dither (plain truncation) */
   MUT_SLOPE_GROUP = 8,   /* P-level arguments all use the first 16-key group's slope */
+  MUT_GROWN_MASK = 9,    /* tiles taken from the tail masked like prompt tiles (keys past the prompt invalid) */
+  MUT_GROWN_STATE = 10,  /* tiles taken from the tail classified against the prompt's tile count */
 };
 static int g_mutation = MUT_NONE;
 void ora_set_mutation(int m) { g_mutation = m; }
@@ -553,6 +557,16 @@ int ora_decode_state(int w8, int w4, int tiles, int j) {
 /* V format of tile j (decode.py:17-22): 1 = INT8 V, 2 = INT4 V. */
 int ora_decode_vfmt(int tiles, int j) { return (tiles - 1 - j < NEAR_V8 || j == 0) ? 1 : 2; }
 
+/* Tail growth (extension, no reference counterpart): a tile j taken from the tail after the prompt's
+ * `tiles` tiles is classified as the newest tile of a cache of j + 1 tiles when it enters, and keeps
+ * that classification; the prompt's tiles keep theirs (the reference never reclassifies a stored
+ * tile).  Every key of such a tile is valid. */
+static int grown_state(int w8, int w4, int tiles, int j) {
+  if (g_mutation == MUT_GROWN_STATE) return ora_decode_state(w8, w4, tiles, j);
+  return j < tiles ? ora_decode_state(w8, w4, tiles, j) : ora_decode_state(w8, w4, j + 1, j);
+}
+static int grown_vfmt(int tiles, int j) { return j < tiles ? ora_decode_vfmt(tiles, j) : ora_decode_vfmt(j + 1, j); }
+
 /* Exact restatement of the 32-lane butterfly sum used by decode_merge_kernel
  * (common_device.cuh:397-415): lane l holds an fma chain over channels 4l..4l+3. */
 static float tail_score(const uint16_t* qv, const uint16_t* kv, const float* kmean, float sm_log2) {
@@ -575,6 +589,7 @@ static float tail_score(const uint16_t* qv, const uint16_t* kv, const float* kme
 
 typedef struct {
   int hq, hk, prompt, per, max_tail;
+  int ctiles; /* tiles per KV head in the code arrays: the prompt's, then those taken from the tail */
   const int32_t* bounds; /* NULL: uniform split of `per`; else [hk][nsplit + 1] entry bounds */
   int nsplit;
   const int32_t* bands;
@@ -589,22 +604,22 @@ typedef struct {
 /* One query head of decode_kernel + decode_merge_kernel. */
 static void decode_head(const decode_args* a, int qh, float* out_row, ora_trace* tr, float* tpm, float* tpl,
                         float* tpo) {
-  const int g = a->hq / a->hk, kh = qh / g, tiles = (a->prompt + BN - 1) / BN;
+  const int g = a->hq / a->hk, kh = qh / g, tiles = (a->prompt + BN - 1) / BN, ct = a->ctiles;
   /* kept-tile list of this KV head: ascending tiles whose group state > 0 */
-  int* entry = (int*)malloc(sizeof(int) * (tiles > 0 ? tiles : 1));
-  int* kprec = (int*)malloc(sizeof(int) * (tiles > 0 ? tiles : 1));
-  int* own = (int*)malloc(sizeof(int) * (tiles > 0 ? tiles : 1));
+  int* entry = (int*)malloc(sizeof(int) * (ct > 0 ? ct : 1));
+  int* kprec = (int*)malloc(sizeof(int) * (ct > 0 ? ct : 1));
+  int* own = (int*)malloc(sizeof(int) * (ct > 0 ? ct : 1));
   int count = 0;
-  for (int j = 0; j < tiles; ++j) {
+  for (int j = 0; j < ct; ++j) {
     int kv = 0;
     for (int h = 0; h < g; ++h) {
-      const int s = ora_decode_state(a->bands[2 * (kh * g + h)], a->bands[2 * (kh * g + h) + 1], tiles, j);
+      const int s = grown_state(a->bands[2 * (kh * g + h)], a->bands[2 * (kh * g + h) + 1], tiles, j);
       if (s > kv) kv = s;
     }
     if (kv > 0) {
       entry[count] = j;
       kprec[count] = kv;
-      own[count] = ora_decode_state(a->bands[2 * qh], a->bands[2 * qh + 1], tiles, j) > 0;
+      own[count] = grown_state(a->bands[2 * qh], a->bands[2 * qh + 1], tiles, j) > 0;
       ++count;
     }
   }
@@ -612,10 +627,10 @@ static void decode_head(const decode_args* a, int qh, float* out_row, ora_trace*
   int maxn = 1;
   for (int h2 = 0; h2 < a->hk; ++h2) {
     int c2 = 0;
-    for (int j = 0; j < tiles; ++j) {
+    for (int j = 0; j < ct; ++j) {
       int kv = 0;
       for (int h = 0; h < g; ++h) {
-        const int s = ora_decode_state(a->bands[2 * (h2 * g + h)], a->bands[2 * (h2 * g + h) + 1], tiles, j);
+        const int s = grown_state(a->bands[2 * (h2 * g + h)], a->bands[2 * (h2 * g + h) + 1], tiles, j);
         if (s > kv) kv = s;
       }
       c2 += kv > 0;
@@ -656,11 +671,11 @@ static void decode_head(const decode_args* a, int qh, float* out_row, ora_trace*
     float m = -FLT_MAX, dw[4] = {0.f, 0.f, 0.f, 0.f}, out[D];
     for (int c = 0; c < D; ++c) out[c] = 0.f;
     for (int e = first; e < last; ++e) {
-      const int j = entry[e], four = kprec[e] == 4, fmt = ora_decode_vfmt(tiles, j);
-      const float* kt = (four ? a->ka4 : a->ka) + ((int64_t)kh * tiles + j) * 4;
+      const int j = entry[e], four = kprec[e] == 4, fmt = grown_vfmt(tiles, j);
+      const float* kt = (four ? a->ka4 : a->ka) + ((int64_t)kh * ct + j) * 4;
       const float qs = four ? qscale4 : qscale;
       const int8_t* qc = four ? q4 : q8;
-      const int8_t* kc = (four ? a->k4 : a->k8) + ((int64_t)kh * tiles + j) * BN * D;
+      const int8_t* kc = (four ? a->k4 : a->k8) + ((int64_t)kh * ct + j) * BN * D;
       float slope[4];
       for (int w = 0; w < 4; ++w) slope[w] = qs * kt[w];
       const float slope1 = qs * fmaxf(fmaxf(kt[0], kt[1]), fmaxf(kt[2], kt[3]));
@@ -669,7 +684,7 @@ static void decode_head(const decode_args* a, int qh, float* out_row, ora_trace*
         int sdot = 0;
         for (int c = 0; c < D; ++c) sdot += (int)qc[c] * (int)kc[(int64_t)k * D + c];
         dot[k] = sdot;
-        valid[k] = own[e] && (j * BN + k < a->prompt);
+        valid[k] = own[e] && ((j >= tiles && g_mutation != MUT_GROWN_MASK) || j * BN + k < a->prompt);
       }
       float tile = -INFINITY;
       for (int w = 0; w < 4; ++w) {
@@ -717,7 +732,7 @@ static void decode_head(const decode_args* a, int qh, float* out_row, ora_trace*
         const float tot = (part[0] + part[1]) + (part[2] + part[3]);
         dw[w] = fmaf(dw[w], alpha, tot);
       }
-      const int8_t* vt = (fmt == 1 ? a->v8 : a->v4) + ((int64_t)kh * tiles + j) * BN * D;
+      const int8_t* vt = (fmt == 1 ? a->v8 : a->v4) + ((int64_t)kh * ct + j) * BN * D;
       int32_t pv[D];
       for (int c = 0; c < D; ++c) pv[c] = 0;
       for (int k = 0; k < BN; ++k) {
@@ -779,9 +794,9 @@ void ora_decode(int hq, int hk, int prompt, const int32_t* bands, int per, float
                 const int8_t* k8, const float* ka, const int8_t* k4, const float* ka4, const int8_t* v8,
                 const int8_t* v4, const float* vstat, const float* kstat, const uint16_t* ktail,
                 const uint16_t* vtail, int max_tail, const uint16_t* kcur, const uint16_t* vcur, int64_t step,
-                const int32_t* bounds, int nsplit, float* out) {
-  decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, bounds, nsplit < 1 ? 1 : nsplit, bands, sm_log2,
-                   q, k8, k4, v8, v4, ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
+                const int32_t* bounds, int nsplit, int ctiles, float* out) {
+  decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, ctiles, bounds, nsplit < 1 ? 1 : nsplit, bands,
+                   sm_log2, q, k8, k4, v8, v4, ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
   for (int qh = 0; qh < hq; ++qh) decode_head(&a, qh, out + (int64_t)qh * D, NULL, NULL, NULL, NULL);
 }
 
@@ -792,10 +807,11 @@ int ora_decode_trace(int hq, int hk, int prompt, const int32_t* bands, int per, 
                      const int8_t* k8, const float* ka, const int8_t* k4, const float* ka4, const int8_t* v8,
                      const int8_t* v4, const float* vstat, const float* kstat, const uint16_t* ktail,
                      const uint16_t* vtail, int max_tail, const uint16_t* kcur, const uint16_t* vcur, int64_t step,
-                     const int32_t* bounds, int nsplit, int qh, int cap, int32_t* col, int32_t* kind, int32_t* split,
-                     float* m, float* base, float* bq, int32_t* p, float* pm, float* pl, float* po, float* out_row) {
-  decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, bounds, nsplit < 1 ? 1 : nsplit, bands, sm_log2,
-                   q, k8, k4, v8, v4, ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
+                     const int32_t* bounds, int nsplit, int ctiles, int qh, int cap, int32_t* col, int32_t* kind,
+                     int32_t* split, float* m, float* base, float* bq, int32_t* p, float* pm, float* pl, float* po,
+                     float* out_row) {
+  decode_args a = {hq, hk, prompt, per < 1 ? 1 : per, max_tail, ctiles, bounds, nsplit < 1 ? 1 : nsplit, bands,
+                   sm_log2, q, k8, k4, v8, v4, ka, ka4, vstat, kstat, ktail, vtail, kcur, vcur, step};
   ora_trace tr = {cap, 0, col, kind, split, m, base, bq, p};
   decode_head(&a, qh, out_row, &tr, pm, pl, po);
   return tr.n;

@@ -55,7 +55,7 @@ def _decode_args(fake, per=8, kcur=None, tst=128):
     return [fake, 24 * 128, 128, fake, None, fake, None, fake, fake, fake, fake, fake, fake, fake, fake, fake,
             fake, fake, 8 * 256 * 128, 256 * tst, tst, 256, kc, kc, 8 * 128, 128, fake, fake, 1, 24 * 128, 128,
             fake, fake, fake, fake, 1, 24, 8, 64, per, 64, 16, 0, 4, 4, None, None, None, 0, None, 0, None, 0,
-            0.088, None]
+            None, 0.088, None]
 
 
 def test_decode_validation_needs_no_gpu():
@@ -90,3 +90,21 @@ def test_noalloc_decode_rejects_partials_beyond_its_scratch():
     args[32], args[33], args[34], args[35], args[36] = 64, 32, 8, 64, 1
     assert lib.tri_decode_noalloc(*args) != 0
     assert b"exceed" in lib.tri_last_error() and b"48395" in lib.tri_last_error()
+
+
+def test_tail_spill_validation_needs_no_gpu():
+    """tri_tail_spill refuses tails shorter than one tile, misaligned tails and missing buffers before
+    any device work."""
+    lib = load_library()
+    fake = ctypes.c_void_p(4096)
+
+    def args(max_tail=256, tst=128, grow=fake):
+        return [fake, fake, fake, fake, 8 * max_tail * tst, max_tail * tst, tst, max_tail, 2, 8, 64, 64, grow, 4,
+                fake, None, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, 16, None, 0, fake, 16, None,
+                None, 0, None, 0, None]
+    assert lib.tri_tail_spill(*args(max_tail=32)) != 0
+    assert b"max_tail must be in [64, 1024]" in lib.tri_last_error()
+    assert lib.tri_tail_spill(*args(tst=100)) != 0
+    assert b"16-byte aligned rows" in lib.tri_last_error()
+    assert lib.tri_tail_spill(*args(grow=None)) != 0
+    assert b"null buffer" in lib.tri_last_error()

@@ -17,6 +17,7 @@
 #include "decode.hip"
 #include "prefill.hip"
 #include "quantize.hip"
+#include "tail.hip"
 
 namespace {
 
@@ -240,7 +241,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        float* po, const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
                        const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
-                       const void* tasks, int n_tasks, double scale, void* stream, int phase,
+                       const void* tasks, int n_tasks, const int64_t* tail_base, double scale, void* stream, int phase,
                        hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr) {
   g_error.clear();
   if (!q || !k8c || !ka || !entry || !kinfo || !count || !fmt || !slot || !v8c || !v4c || !vstat || !kstat ||
@@ -354,6 +355,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   mg.kcur = static_cast<const uint16_t*>(kcur);
   mg.vcur = static_cast<const uint16_t*>(vcur);
   mg.step = step;
+  mg.tail_base = tail_base;
   mg.out = out;
   mg.out_dtype = out_dtype;
   mg.qsb = q_sb;
@@ -428,8 +430,8 @@ static int noalloc_scratch(float** out) {
 #define TRI_DECODE_ARGS                                                                                      \
   q, q_sb, q_sh, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8c, v4c, vstat, kstat, ktail, vtail, t_sb, t_sh, \
       t_st, max_tail, kcur, vcur, c_sb, c_sh, step, out, out_dtype, o_sb, o_sh, pm, pl, po, prompt, batch, hq, hk,  \
-      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, xslot, kxc, vxc, n_kx, bounds, nsplit, tasks, n_tasks, scale,   \
-      stream
+      maxn, per, tiles_max, n_k8, n_k4, n_v8, n_v4, xslot, kxc, vxc, n_kx, bounds, nsplit, tasks, n_tasks,          \
+      tail_base, scale, stream
 #define TRI_DECODE_PARAMS                                                                                          \
   const void *q, int64_t q_sb, int64_t q_sh, const void *k8c, const void *k4c, const float *ka, const float *ka4,  \
       const int32_t *entry, const int32_t *kinfo, const int32_t *count, const int32_t *fmt, const int32_t *slot,  \
@@ -439,7 +441,7 @@ static int noalloc_scratch(float** out) {
       float *pl, float *po, const int32_t *prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,    \
       int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t *xslot, const void *kxc,           \
       const void *vxc, int64_t n_kx, const int32_t *bounds, int nsplit, const void *tasks, int n_tasks,      \
-      double scale, void *stream
+      const int64_t *tail_base, double scale, void *stream
 
 int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
 int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }
@@ -457,7 +459,7 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                        const int32_t* prompt, int batch, int hq, int hk, int maxn, int per, int tiles_max,
                        int64_t n_k8, int64_t n_k4, int64_t n_v8, int64_t n_v4, const int32_t* xslot,
                        const void* kxc, const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit,
-                       const void* tasks, int n_tasks, double scale, void* stream) {
+                       const void* tasks, int n_tasks, const int64_t* tail_base, double scale, void* stream) {
   g_error.clear();
   if (batch < 1 || hq < 1 || hk < 1 || maxn < 1) return fail("decode_noalloc: empty shape");
   if (!bounds && (per < 1 || per > tri::MAX_PER)) return fail("decode_noalloc: per (tiles per split) must be in [1, 64]");
@@ -523,7 +525,7 @@ int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, co
 }
 
 int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int hq, int hk, int t, int nx,
-                    const void* kp, const void* k4p, const float* ka, const float* ka4, const float* kstat,
+                    int xstride, const void* kp, const void* k4p, const float* ka, const float* ka4, const float* kstat,
                     const float* vstat, const void* v8p, const void* v4p, const void* kx, const void* vx, int row0,
                     int rows, int maxn, int tiles_max, int32_t* entry, int32_t* kinfo, int32_t* slot, int32_t* count,
                     int32_t* fmt, int32_t* prompt, int32_t* xslot, float* ka_c, float* ka4_c, float* kstat_c,
@@ -544,6 +546,7 @@ int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int h
   if (maxn < 1 || tiles_max < tiles) return fail("cache_store: maxn >= 1 and tiles_max >= the prompt's tiles");
   if (exact && (nx < 1 || nx > hk || !kx || !vx || !kxc || !vxc || !xslot))
     return fail("cache_store: exact heads need nx in [1, hk], KX/VX sources, destinations and xslot");
+  if (exact && xstride < tiles) return fail("cache_store: xstride (records per exact head) below the prompt's tiles");
   if (o8 < 0 || o4 < 0 || ov8 < 0 || ov4 < 0 || ox < 0) return fail("cache_store: negative record offset");
   if ((k4c == nullptr) != (cap4 == 0) || (v4c == nullptr) != (capv4 == 0))
     return fail("cache_store: INT4 K / V destinations and capacities (both or neither)");
@@ -562,6 +565,7 @@ int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int h
   a.t = t;
   a.tiles = tiles;
   a.nx = exact ? nx : 0;
+  a.xstride = exact ? xstride : 0;
   a.batch = batch;
   a.kp = static_cast<const uint8_t*>(kp);
   a.k4p = static_cast<const uint8_t*>(k4p);
@@ -607,6 +611,73 @@ int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int h
   const dim3 grid((tiles + tri::STORE_CHUNK - 1) / tri::STORE_CHUNK, hk, batch);
   tri::cache_store_kernel<<<grid, tri::STORE_THREADS, 0, static_cast<hipStream_t>(stream)>>>(a);
   return check_launch("cache_store");
+}
+
+int tri_tail_spill(const int64_t* step, int64_t* tail_base, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh,
+                   int64_t t_st, int max_tail, int rows, int hk, int maxn, int tiles_max, const int32_t* grow, int cap,
+                   const int32_t* prompt, const int32_t* xslot, int32_t* entry, int32_t* kinfo, int32_t* slot,
+                   int32_t* count, int32_t* fmt, float* ka, float* ka4, const float* kstat, const float* vstat,
+                   void* k8c, int64_t n_k8, void* k4c, int64_t n_k4, void* v8c, int64_t n_v8, void* kxc, void* vxc,
+                   int64_t n_kx, int32_t* tasks, int n_tasks, void* stream) {
+  g_error.clear();
+  if (!step || !tail_base || !ktail || !vtail || !grow || !prompt || !entry || !kinfo || !slot || !count || !fmt ||
+      !ka || !kstat || !vstat || !k8c || !v8c)
+    return fail("tail_spill: null buffer");
+  if (rows < 1 || hk < 1 || maxn < 1 || tiles_max < 1 || cap < 0) return fail("tail_spill: empty shape");
+  if (max_tail < tri::BN || max_tail > tri::MAX_TAIL)
+    return fail("tail_spill: tail growth moves 64 tokens at a time: max_tail must be in [64, 1024]");
+  if (!aligned(ktail, 16) || !aligned(vtail, 16) || (t_sb % 8) || (t_sh % 8) || (t_st % 8))
+    return fail("tail_spill: tail buffers must be 16-byte aligned rows");
+  if (!aligned(grow, 16) || !aligned(ka, 16) || (ka4 && !aligned(ka4, 16)) || (tasks && !aligned(tasks, 16)))
+    return fail("tail_spill: grow, the K scales and the task table must be 16-byte aligned");
+  if ((k4c == nullptr) != (ka4 == nullptr)) return fail("tail_spill: INT4 K records and scales (both or neither)");
+  if (xslot && (!kxc || !vxc)) return fail("tail_spill: exact heads need KX/VX record arrays");
+  if (tasks && n_tasks < 1) return fail("tail_spill: a task table needs n_tasks >= 1");
+  const int64_t lim = (int64_t)1 << 31;
+  if (n_k8 < 1 || n_v8 < 1 || n_k8 * tri::K8_BYTES >= lim || n_k4 * tri::K4_BYTES >= lim ||
+      n_v8 * tri::V8_BYTES >= lim || n_kx * tri::KX_BYTES >= lim)
+    return fail("tail_spill: compacted record arrays must be non-empty and below 2 GiB each");
+  for (const void* p : {(const void*)k8c, (const void*)k4c, (const void*)v8c, (const void*)kxc, (const void*)vxc})
+    if (p && !aligned(p, 16)) return fail("tail_spill: record arrays must be 16-byte aligned");
+  tri::SpillArgs a;
+  a.step = step;
+  a.tail_base = tail_base;
+  a.ktail = static_cast<uint16_t*>(ktail);
+  a.vtail = static_cast<uint16_t*>(vtail);
+  a.tsb = t_sb;
+  a.tsh = t_sh;
+  a.tst = t_st;
+  a.max_tail = max_tail;
+  a.rows = rows;
+  a.hk = hk;
+  a.maxn = maxn;
+  a.tiles_max = tiles_max;
+  a.cap = cap;
+  a.grow = grow;
+  a.prompt = prompt;
+  a.xslot = xslot;
+  a.entry = entry;
+  a.kinfo = kinfo;
+  a.slot = slot;
+  a.count = count;
+  a.fmt = fmt;
+  a.ka = ka;
+  a.ka4 = ka4;
+  a.kstat = kstat;
+  a.vstat = vstat;
+  a.k8c = static_cast<uint8_t*>(k8c);
+  a.k4c = static_cast<uint8_t*>(k4c);
+  a.v8c = static_cast<uint8_t*>(v8c);
+  a.kxc = static_cast<uint8_t*>(kxc);
+  a.vxc = static_cast<uint8_t*>(vxc);
+  a.n_k8 = n_k8;
+  a.n_k4 = k4c ? n_k4 : 0;
+  a.n_v8 = n_v8;
+  a.n_kx = xslot ? n_kx : 0;
+  a.tasks = tasks;
+  a.n_tasks = tasks ? n_tasks : 0;
+  tri::tail_spill_kernel<<<dim3(hk, rows), tri::SPILL_THREADS, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return check_launch("tail_spill");
 }
 
 int tri_decode_occupancy(int* blocks) {

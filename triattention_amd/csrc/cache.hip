@@ -31,6 +31,7 @@ struct CacheStoreArgs {
   const int32_t* bands;  // [hq][2] (w8, w4)
   const int32_t* exact;  // [hk]: -1 for a quantized KV head, else its slot among the exact heads; may be null
   int hq, hk, t, tiles, nx, batch;
+  int xstride;  // records per (sequence, exact head) in the destination (>= tiles: room for tail tiles)
   // sources: the Prefill call's outputs, [batch][hk][tiles] records and scales
   const uint8_t* kp;   // K8
   const uint8_t* k4p;  // K4 (may be null when no tile is INT4)
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(STORE_THREADS) void cache_store_kernel(CacheStoreAr
         CopyDesc dsc;
         if (ex) {
           const int64_t src = ((int64_t)s * a.nx + xs) * tiles + j;
-          const int64_t dst = a.ox + ((int64_t)s * a.nx + xs) * tiles + j;
+          const int64_t dst = a.ox + ((int64_t)s * a.nx + xs) * a.xstride + j;
           dsc.kind = 1;
           dsc.ksrc = dsc.vsrc = src;
           dsc.kdst = dsc.vdst = dst;
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(STORE_THREADS) void cache_store_kernel(CacheStoreAr
     }
     if (tid == 0) {
       a.count[hb] = cnt;
-      if (a.xslot) a.xslot[hb] = ex ? (int)(a.ox + ((int64_t)s * a.nx + xs) * tiles) : -1;
+      if (a.xslot) a.xslot[hb] = ex ? (int)(a.ox + ((int64_t)s * a.nx + xs) * a.xstride) : -1;
     }
     for (int i = tid; i < a.tiles_max * 4; i += STORE_THREADS) {
       a.ka_c[hb * a.tiles_max * 4 + i] = i < tiles * 4 ? a.ka[hb_src * tiles * 4 + i] : 1.f;

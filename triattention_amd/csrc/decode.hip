@@ -145,7 +145,7 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
   // Q as the B operand, kept in LDS: column lq = q-head kh*g + lq, features ks*16 + 8*half + e
   __shared__ __align__(16) uint16_t qx[32][D];
   const int L = threadIdx.x, lq = L & 31, half = L >> 5;
-  const int g = a.hq / a.hk, prompt = a.prompt[b];
+  const int g = a.hq / a.hk, prompt = a.prompt[b], ptiles = (prompt + BN - 1) / BN;
   const int64_t hb = (int64_t)b * a.hk + kh;
   int first, last;
   split_range(a, hb, split, first, last);
@@ -197,11 +197,13 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
                      sc);
     if (hs + 1 < steps) load_k(hs + 1);
     const int key0 = (first + (hs >> 1)) * BN + (hs & 1) * 32;
+    // keys past the prompt exist only in its last tile; tiles after it (spilled from the tail) are full
+    const int lim = first + (hs >> 1) < ptiles ? prompt : INT_MAX;
     float mx = -__builtin_inff();
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
-      sc[r] = key < prompt ? (sc[r] - cq) * a.sm_log2 : -__builtin_inff();
+      sc[r] = key < lim ? (sc[r] - cq) * a.sm_log2 : -__builtin_inff();
       mx = fmaxf(mx, sc[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   }
   const int L = threadIdx.x & 63, lq = L & 31, half = L >> 5;
   const int g = a.hq / a.hk;
-  const int prompt = a.prompt[b];
+  const int prompt = a.prompt[b], ptiles = (prompt + BN - 1) / BN;
   uint8_t (&pls)[MAX_GROUP][BN] = pls_all[wv];
   const int64_t hb = (int64_t)b * a.hk + kh;
 
@@ -637,6 +639,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     else { kavc[0] = kv0; kavc[NK - 1] = kv1; }
     bool ok[R][NK];
     float slope[R][NK], trow[R];
+    // keys past the prompt exist only in its last tile; tiles after it (spilled from the tail) are full
+    const int lim = j < ptiles ? prompt : INT_MAX;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int q = qrow(r);
@@ -647,7 +651,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
 #pragma unroll
       for (int t = 0; t < NK; ++t) {
         const int kb = DUP ? half : t;
-        ok[r][t] = on && (j * BN + kb * 32 + lq < prompt);
+        ok[r][t] = on && (j * BN + kb * 32 + lq < lim);
         slope[r][t] = qs * kavc[t];
         // The 16 lanes of a DPP row hold keys of one 16-key group, so one slope (>= 0): the row's
         // largest scaled score is the slope times its largest integer dot product.
@@ -832,6 +836,7 @@ struct MergeArgs {
   const uint16_t* kcur;  // [B][Hk][1][128], strides csb, csh
   const uint16_t* vcur;
   const int64_t* step;
+  const int64_t* tail_base;  // tokens moved from the tail into the cache since the store (may be null: 0)
   void* out;             // [B][Hq][1][128], strides osb, osh
   int out_dtype;         // 0 = fp32, 1 = bf16
   int64_t qsb, qsh, tsb, tsh, tst, csb, csh, osb, osh;
@@ -863,7 +868,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   }
   const int g = a.hq / a.hk, kh = hq / g;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int prior = (int)min((int64_t)a.max_tail - 1, *a.step), tail = prior + 1;
+  // the tail holds step - tail_base tokens before this one (the reference: step, clamped to max_tail - 1)
+  const int64_t held = *a.step - (a.tail_base != nullptr ? *a.tail_base : 0);
+  const int prior = (int)max((int64_t)0, min((int64_t)a.max_tail - 1, held)), tail = prior + 1;
   const int64_t hb = (int64_t)b * a.hk + kh;
   const float* vmean = a.vstat + hb * 3 * D;
   const float* vscale = vmean + D;

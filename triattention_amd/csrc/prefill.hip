@@ -414,31 +414,24 @@ struct ExactPackArgs {
   int hq, hk, t, nx;
 };
 
-__global__ __launch_bounds__(256) void pack_exact_kernel(ExactPackArgs a) {
-  const int tile = blockIdx.x, kh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-  const int slot = a.exact[kh * (a.hq / a.hk)] - 1;
-  if (slot < 0) return;
-  const int tiles = gridDim.x;
-  const int64_t rec = ((int64_t)b * a.nx + slot) * tiles + tile;
-  uint8_t* kd = a.kx + rec * KX_BYTES;
-  uint8_t* vd = a.vx + rec * KX_BYTES;
-  const uint16_t* kbase = a.k + b * a.ksb + kh * a.ksh;
-  const uint16_t* vbase = a.v + b * a.vsb + kh * a.vsh;
-  constexpr int VP = D + 8;  // padded LDS row (bf16 elements)
-  __shared__ __align__(16) uint16_t vt[BN * VP];
+// One tile of pack_exact: keys r < rows of ksrc / vsrc (row strides kst / vst) into the KX and VX
+// records kd / vd; vt is the workgroup's LDS staging of V.  256 threads.
+constexpr int EXACT_VP = D + 8;  // padded LDS row of the V staging (bf16 elements)
+__device__ __forceinline__ void pack_exact_tile(const uint16_t* ksrc, int64_t kst, const uint16_t* vsrc, int64_t vst,
+                                                int rows, uint8_t* kd, uint8_t* vd, uint16_t* vt) {
+  const int tid = threadIdx.x;
   // K: 1024 16-byte pieces in source order (key, 8-feature piece)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int c = tid + 256 * i, key = c >> 4, f0 = (c & 15) * 8;
-    const int tok = tile * BN + key;
     uint4 w = make_uint4(0, 0, 0, 0), u = w;
-    if (tok < a.t) {
-      w = *reinterpret_cast<const uint4*>(kbase + (int64_t)tok * a.kst + f0);
-      u = *reinterpret_cast<const uint4*>(vbase + (int64_t)tok * a.vst + f0);
+    if (key < rows) {
+      w = *reinterpret_cast<const uint4*>(ksrc + (int64_t)key * kst + f0);
+      u = *reinterpret_cast<const uint4*>(vsrc + (int64_t)key * vst + f0);
     }
     const int kb = key >> 5, lk = key & 31, ks = f0 >> 4, h = (f0 >> 3) & 1;
     *reinterpret_cast<uint4*>(kd + kb * (KX_BYTES / 2) + ks * 1024 + (h * 32 + lk) * 16) = w;
-    *reinterpret_cast<uint4*>(vt + key * VP + f0) = u;
+    *reinterpret_cast<uint4*>(vt + key * EXACT_VP + f0) = u;
   }
   __syncthreads();
   // V: 1024 output pieces in destination order
@@ -452,10 +445,22 @@ __global__ __launch_bounds__(256) void pack_exact_kernel(ExactPackArgs a) {
       const int e0 = 2 * j, e1 = 2 * j + 1;
       const int k0 = kb * 32 + 16 * khalf + 8 * (e0 >> 2) + 4 * h + (e0 & 3);
       const int k1 = kb * 32 + 16 * khalf + 8 * (e1 >> 2) + 4 * h + (e1 & 3);
-      w[j] = (uint32_t)vt[k0 * VP + ch] | ((uint32_t)vt[k1 * VP + ch] << 16);
+      w[j] = (uint32_t)vt[k0 * EXACT_VP + ch] | ((uint32_t)vt[k1 * EXACT_VP + ch] << 16);
     }
     *reinterpret_cast<uint4*>(vd + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
   }
+}
+
+__global__ __launch_bounds__(256) void pack_exact_kernel(ExactPackArgs a) {
+  const int tile = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int slot = a.exact[kh * (a.hq / a.hk)] - 1;
+  if (slot < 0) return;
+  const int tiles = gridDim.x;
+  const int64_t rec = ((int64_t)b * a.nx + slot) * tiles + tile;
+  __shared__ __align__(16) uint16_t vt[BN * EXACT_VP];
+  pack_exact_tile(a.k + b * a.ksb + kh * a.ksh + (int64_t)tile * BN * a.kst, a.kst,
+                  a.v + b * a.vsb + kh * a.vsh + (int64_t)tile * BN * a.vst, a.vst, a.t - tile * BN,
+                  a.kx + rec * KX_BYTES, a.vx + rec * KX_BYTES, vt);
 }
 
 template <int V>

@@ -106,36 +106,32 @@ __global__ __launch_bounds__(128) void finalize_kernel(const float* __restrict__
   stat[hb * 3 * D + 2 * D + c] = 1.f / scale;
 }
 
-// y = R(k - mean) for one 64-key tile; wave w owns the 16-key group w, one key
-// per 8 lanes (16 features per lane, DPP rotation), two passes of 8 keys.
-// INT8 record + group scale ka, optional INT4 record + ka4.
+// y = R(k - mean) of one 64-key tile: rows src + r * st for r < rows (zeros past); the INT8 record rec8
+// with its four group scales ka, and the INT4 record rec4 with ka4 (either pair may be null).  Wave w
+// owns the 16-key group w, one key per 8 lanes (16 features per lane, DPP rotation), two passes of 8
+// keys; c8 / c4 are the workgroup's LDS staging.  256 threads.
 // common_device.cuh:58-131 (quantize_k_kernel).
-__global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restrict__ k, int64_t sb, int64_t sh,
-                                                         int64_t st, const float* __restrict__ kstat, int hk, int t,
-                                                         uint8_t* __restrict__ k8, float* __restrict__ ka,
-                                                         uint8_t* __restrict__ k4, float* __restrict__ ka4) {
-  __shared__ __align__(16) uint8_t c8[BN][D];
-  __shared__ __align__(16) uint8_t c4[BN][D];
-  const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN;
+__device__ __forceinline__ void quantize_k_tile(const uint16_t* __restrict__ src, int64_t st, int rows,
+                                                const float* __restrict__ mean, uint8_t* __restrict__ rec8,
+                                                float* __restrict__ ka, uint8_t* __restrict__ rec4,
+                                                float* __restrict__ ka4, uint8_t (*c8)[D], uint8_t (*c4)[D]) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, sub = lane & 7;
-  const int64_t hb = (int64_t)b * hk + hd;
-  const float* mean = kstat + hb * 3 * D + sub * 16;
   float mc[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) mc[i] = mean[i];
+  for (int i = 0; i < 16; ++i) mc[i] = mean[sub * 16 + i];
   float y[2][16];
   float cm = 0.f;
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
-    const int r = wave * 16 + it * 8 + (lane >> 3), tk = tile * BN + r;
+    const int r = wave * 16 + it * 8 + (lane >> 3);
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = 0.f;
-    if (tk < t) {
-      const uint16_t* src = k + b * sb + hd * sh + (int64_t)tk * st + sub * 16;
+    if (r < rows) {
+      const uint16_t* row = src + (int64_t)r * st + sub * 16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(src + 4 * i);
+        const uint2 raw = *reinterpret_cast<const uint2*>(row + 4 * i);
         x[4 * i] = bf16f(raw.x & 0xffffu) - mc[4 * i];
         x[4 * i + 1] = bf16f(raw.x >> 16) - mc[4 * i + 1];
         x[4 * i + 2] = bf16f(raw.y & 0xffffu) - mc[4 * i + 2];
@@ -151,10 +147,9 @@ __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restr
   }
   cm = wave_max(cm);
   const float inv = cm > 0.f ? 127.f / cm : 0.f, inv4 = cm > 0.f ? 7.f / cm : 0.f;
-  const int64_t si = (hb * tiles + tile) * 4 + wave;
   if (lane == 0) {
-    ka[si] = cm > 0.f ? cm / 127.f : 1.f;
-    if (k4 != nullptr) ka4[si] = cm > 0.f ? cm / 7.f : 1.f;
+    if (rec8 != nullptr) ka[wave] = cm > 0.f ? cm / 127.f : 1.f;
+    if (rec4 != nullptr) ka4[wave] = cm > 0.f ? cm / 7.f : 1.f;
   }
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
@@ -174,15 +169,15 @@ __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restr
     *reinterpret_cast<uint4*>(&c4[r][sub * 16]) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
   }
   __syncthreads();
-  uint8_t* rec8 = k8 + (hb * tiles + tile) * K8_BYTES;
+  if (rec8 != nullptr) {
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int s = tid + it * 256, F = s >> 6, L = s & 63, kb = F >> 2, ks = F & 3;
-    const int key = kb * 32 + (L & 31), f0 = ks * 32 + 16 * (L >> 5);
-    *reinterpret_cast<uint4*>(rec8 + F * 1024 + L * 16) = *reinterpret_cast<const uint4*>(&c8[key][f0]);
+    for (int it = 0; it < 2; ++it) {
+      const int s = tid + it * 256, F = s >> 6, L = s & 63, kb = F >> 2, ks = F & 3;
+      const int key = kb * 32 + (L & 31), f0 = ks * 32 + 16 * (L >> 5);
+      *reinterpret_cast<uint4*>(rec8 + F * 1024 + L * 16) = *reinterpret_cast<const uint4*>(&c8[key][f0]);
+    }
   }
-  if (k4 == nullptr) return;
-  uint8_t* rec4 = k4 + (hb * tiles + tile) * K4_BYTES;
+  if (rec4 == nullptr) return;
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int s = tid + it * 256, F = s >> 6, L = s & 63, kb = F >> 2, ks = F & 3;
@@ -193,22 +188,33 @@ __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restr
   }
 }
 
-// v' = (v - mean) * inv (zero for padded keys) into V16 (fp16), V8 and V4 records.
+// quantize_k_tile for every (tile, KV head, sequence): K [B][Hk][T][128] into [B][Hk][tiles] records.
+__global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restrict__ k, int64_t sb, int64_t sh,
+                                                         int64_t st, const float* __restrict__ kstat, int hk, int t,
+                                                         uint8_t* __restrict__ k8, float* __restrict__ ka,
+                                                         uint8_t* __restrict__ k4, float* __restrict__ ka4) {
+  __shared__ __align__(16) uint8_t c8[BN][D];
+  __shared__ __align__(16) uint8_t c4[BN][D];
+  const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN;
+  const int64_t hb = (int64_t)b * hk + hd, rec = hb * tiles + tile;
+  quantize_k_tile(k + b * sb + hd * sh + (int64_t)tile * BN * st, st, t - tile * BN, kstat + hb * 3 * D,
+                  k8 + rec * K8_BYTES, ka + rec * 4, k4 != nullptr ? k4 + rec * K4_BYTES : nullptr,
+                  k4 != nullptr ? ka4 + rec * 4 : nullptr, c8, c4);
+}
+
+// v' = (v - mean) * inv of one 64-key tile (rows src + r * st for r < rows, zeros past) into the V16
+// (fp16), V8 and V4 records (any may be null); vn is the workgroup's LDS staging.  256 threads.
 // common_device.cuh:132-172 (vnorm, pack_v_kernel).
-__global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict__ v, int64_t sb, int64_t sh,
-                                                     int64_t st, const float* __restrict__ vstat, int hk, int t,
-                                                     uint8_t* __restrict__ v16, uint8_t* __restrict__ v8,
-                                                     uint8_t* __restrict__ v4) {
-  __shared__ float vn[BN][D + 1];
-  const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN, tid = threadIdx.x;
-  const int64_t hb = (int64_t)b * hk + hd;
-  const float* mean = vstat + hb * 3 * D;
-  const float* inv = mean + 2 * D;
+__device__ __forceinline__ void pack_v_tile(const uint16_t* __restrict__ src, int64_t st, int rows,
+                                            const float* __restrict__ mean, const float* __restrict__ inv,
+                                            uint8_t* __restrict__ v16, uint8_t* __restrict__ v8,
+                                            uint8_t* __restrict__ v4, float (*vn)[D + 1]) {
+  const int tid = threadIdx.x;
   for (int i = tid; i < BN * D / 4; i += 256) {
-    const int r = i / (D / 4), c0 = (i % (D / 4)) * 4, tk = tile * BN + r;
+    const int r = i / (D / 4), c0 = (i % (D / 4)) * 4;
     float x[4] = {0.f, 0.f, 0.f, 0.f};
-    if (tk < t) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(v + b * sb + hd * sh + (int64_t)tk * st + c0);
+    if (r < rows) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(src + (int64_t)r * st + c0);
       x[0] = (bf16f(raw.x & 0xffffu) - mean[c0]) * inv[c0];
       x[1] = (bf16f(raw.x >> 16) - mean[c0 + 1]) * inv[c0 + 1];
       x[2] = (bf16f(raw.y & 0xffffu) - mean[c0 + 2]) * inv[c0 + 2];
@@ -218,9 +224,7 @@ __global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict_
     for (int j = 0; j < 4; ++j) vn[r][c0 + j] = x[j];
   }
   __syncthreads();
-  const int64_t rec = hb * tiles + tile;
   if (v16 != nullptr) {
-    uint8_t* out = v16 + rec * V16_BYTES;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int s = tid + it * 256, F = s >> 6, L = s & 63, kh = F & 1, kb = (F >> 1) & 1, cb = F >> 2;
@@ -231,7 +235,7 @@ __global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict_
         const int k0 = kb * 32 + 8 * (2 * kh + e / 4) + 4 * g + e % 4;
         w[e / 2] = (uint32_t)f32_to_f16_bits(vn[k0][ch]) | ((uint32_t)f32_to_f16_bits(vn[k0 + 1][ch]) << 16);
       }
-      *reinterpret_cast<uint4*>(out + F * 1024 + L * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      *reinterpret_cast<uint4*>(v16 + F * 1024 + L * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
   if (v8 == nullptr && v4 == nullptr) return;
@@ -248,11 +252,25 @@ __global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict_
       b8[p / 4] |= ((uint32_t)q8 & 0xffu) << (8 * (p % 4));
       b4[p / 4] |= ((uint32_t)q4 & 0xfu) << (8 * (p % 4));
     }
-    if (v8 != nullptr) *reinterpret_cast<uint4*>(v8 + rec * V8_BYTES + F * 1024 + L * 16) = make_uint4(b8[0], b8[1], b8[2], b8[3]);
+    if (v8 != nullptr) *reinterpret_cast<uint4*>(v8 + F * 1024 + L * 16) = make_uint4(b8[0], b8[1], b8[2], b8[3]);
     if (v4 != nullptr)
-      *reinterpret_cast<uint2*>(v4 + rec * V4_BYTES + (F >> 1) * 1024 + L * 16 + (F & 1) * 8) =
+      *reinterpret_cast<uint2*>(v4 + (F >> 1) * 1024 + L * 16 + (F & 1) * 8) =
           make_uint2(b4[0] | (b4[1] << 4), b4[2] | (b4[3] << 4));
   }
+}
+
+// pack_v_tile for every (tile, KV head, sequence): V [B][Hk][T][128] into [B][Hk][tiles] records.
+__global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict__ v, int64_t sb, int64_t sh,
+                                                     int64_t st, const float* __restrict__ vstat, int hk, int t,
+                                                     uint8_t* __restrict__ v16, uint8_t* __restrict__ v8,
+                                                     uint8_t* __restrict__ v4) {
+  __shared__ float vn[BN][D + 1];
+  const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN;
+  const int64_t hb = (int64_t)b * hk + hd, rec = hb * tiles + tile;
+  const float* mean = vstat + hb * 3 * D;
+  pack_v_tile(v + b * sb + hd * sh + (int64_t)tile * BN * st, st, t - tile * BN, mean, mean + 2 * D,
+              v16 != nullptr ? v16 + rec * V16_BYTES : nullptr, v8 != nullptr ? v8 + rec * V8_BYTES : nullptr,
+              v4 != nullptr ? v4 + rec * V4_BYTES : nullptr, vn);
 }
 
 }  // namespace tri

@@ -16,6 +16,17 @@ Extension: batches.  One ``store`` holds the B sequences of one Prefill call;
 with ``ragged = True`` successive ``store`` calls for a layer append their
 sequences (e.g. one Prefill per prompt of a different length), and the decode
 op then serves the whole ragged batch in one launch.
+
+Extension: tail growth (``grow_tail`` > 0).  The reference's tail holds
+max_tail generated tokens and then overwrites its last slot
+(common_device.cuh:384).  Here each layer's decode step first launches
+``tail_spill``: when the tail is full, its oldest 64 tokens become a new tile
+of the cache (quantized with the prompt's statistics, classified as the newest
+tile) and the tail moves up by 64 slots.  The store reserves room for
+``grow_tail`` tokens of such tiles per (sequence, KV head); the decode's
+partition gets growth splits that fill as tiles arrive, so every launch's
+arguments stay the same until the room runs out (a captured step replays
+unchanged), and the cache then doubles the room.
 """
 from __future__ import annotations
 
@@ -40,6 +51,7 @@ BALANCE_TILES = 16  # kept tiles per slot up to which the split partition is bal
 # entry words: bits 0-28 the tile index (decode.py:36); extension: bit 30 marks that bit 29 holds
 # the tile's V format (1 = INT8 V), which spares the decode kernel a dependent load of fmt
 ENTRY_TILE, ENTRY_V8, ENTRY_VFMT = (1 << 29) - 1, 1 << 29, 1 << 30
+BN = 64  # tokens per tile (and per move of a full tail into the cache)
 
 
 def tile_states(bands: torch.Tensor, tiles: int) -> torch.Tensor:
@@ -85,6 +97,22 @@ def sequence_metadata(bands, tiles: int, hk: int, vcodes: torch.Tensor, exact_kv
         vsel[code] = select
     return dict(count=count, maxn=maxn, order=order, valid=valid, is4=is4, is8=is8, rows=rows, kslot=kslot,
                 kbase=kbase, vslot=vslot, vcode=vcode, vsel=vsel, exact=exact)
+
+
+def growth_kinds(bands, hk: int, exact_kv=()):
+    """Per KV head, how a tile taken from a full tail is kept (extension): kind 8 / 4 (K precision),
+    1 (exact head) or 0 (no q-head keeps it), and its kinfo bits (rowmask | INT4 K << 8).  The tile is
+    classified as the newest tile of the cache, d = 0 in decode.py:27-33: state 8 for a q-head with
+    w8 > 0, else 4 with w4 > 0, else 0."""
+    b = torch.as_tensor(bands, dtype=torch.int64).cpu().view(-1, 2).numpy()
+    g = b.shape[0] // hk
+    state = np.where(b[:, 0] > 0, 8, np.where(b[:, 1] > 0, 4, 0)).reshape(hk, g)
+    kind = state.max(1)
+    mask = ((state > 0).astype(np.int64) << np.arange(g)[None, :]).sum(1)
+    info = np.where(kind > 0, (mask & 0xFF) | ((kind == 4).astype(np.int64) << 8), -1)
+    for h in exact_kv:
+        kind[h], info[h] = 1, (1 << g) - 1
+    return kind.astype(np.int64), info.astype(np.int32)
 
 
 def entry_costs(meta) -> np.ndarray:
@@ -160,8 +188,13 @@ class _LayerStore:
         self.cap = dict(rows=0, k8=0, k4=0, v8=0, v4=0, x=0)
         self.arrays = {name: None for name in ("entry", "kinfo", "slot", "count", "fmt", "prompt", "xslot", "ka",
                                                "ka4", "kstat", "vstat", "tail_k", "tail_v", "k8", "k4", "v8", "v4",
-                                               "kx", "vx")}
+                                               "kx", "vx", "grow", "count0")}
         self.groups = []
+        # tail growth: tiles of room per (sequence, KV head), and the host's mirror of the device's
+        # tail base (tokens moved from the tail into the cache since the store)
+        self.grow_tiles = 0
+        self.tb = 0
+        self.arrays["tail_base"] = torch.zeros(2, dtype=torch.int64, device=device)
 
     def _regrow(self, name, shape, fill, dtype):
         """Array ``name`` at ``shape``, filled with ``fill`` and holding the old contents in its corner."""
@@ -195,6 +228,8 @@ class _LayerStore:
             self._regrow("vstat", (cap_rows, hk, 3, 128), 0.0, f32)
             for name in ("tail_k", "tail_v"):
                 self._regrow(name, (cap_rows, hk, self.max_tail, 128), 0.0, torch.bfloat16)
+            self._regrow("grow", (cap_rows, hk, 4), -1, i32)
+            self._regrow("count0", (cap_rows, hk), 0, i32)
         if (int4 or self.arrays["ka4"] is not None) and (relayout or self.arrays["ka4"] is None):
             self._regrow("ka4", (cap_rows, hk, tiles_max, 4), 1.0, f32)
         if (exact or self.arrays["xslot"] is not None) and (relayout or self.arrays["xslot"] is None):
@@ -217,7 +252,7 @@ class _LayerStore:
 
 
 class DecodeCache:
-    def __init__(self, module, max_tail=256):
+    def __init__(self, module, max_tail=256, grow_tail=0):
         self.module, self.max_tail = module, max_tail
         self.layers, self.formats, self.step = {}, {}, None
         self.ragged = False
@@ -229,6 +264,17 @@ class DecodeCache:
         # the split kernel reads its splits from a task table built once per cache layout (False: it
         # gathers them from the metadata rows, as the reference's kernel does)
         self.tasks = True
+        # tail growth (extension): tokens of room per (sequence, KV head) for tiles taken from a full
+        # tail (0: the reference's clamped tail)
+        if grow_tail and max_tail < BN:
+            raise ValueError(f"tail growth moves {BN} tokens at a time: max_tail must be at least {BN}")
+        self.grow_tail = int(grow_tail)
+        # host mirror of the device step (the tail base of each layer is mirrored in its store), the
+        # layers called since the last advance, and graph capture bookkeeping
+        self.host_step = 0
+        self._called = set()
+        self.capturing = False
+        self._capture_set = set()
 
     def codes(self, rows):
         if rows not in self.formats:
@@ -254,27 +300,60 @@ class DecodeCache:
         exact_kv = sorted(set(int(h) for h in exact_kv))
         meta, dev = self._metadata(bands, tiles, hk, codes, exact_kv, device)
         hq = dev["bands"].shape[0]
-        seq = dict(k8=int(meta["is8"].sum()), k4=int(meta["is4"].sum()), v8=int(meta["vsel"][I8].sum()),
-                   v4=int(meta["vsel"][I4].sum()), x=len(exact_kv) * tiles)
         entry = self.layers.get(layer)
         st = entry["store"] if (self.ragged and entry is not None) else _LayerStore(hk, self.max_tail, device)
         if st.hk != hk:
             raise ValueError(f"decode cache layer {layer}: {hk} KV heads after {st.hk}")
+        if self.grow_tail and not st.grow_tiles:
+            st.grow_tiles = -(-self.grow_tail // BN)
+        G = st.grow_tiles
+        kind, info = growth_kinds(bands, hk, exact_kv) if G else (np.zeros(hk, np.int64), np.full(hk, -1, np.int32))
+        nx = len(exact_kv)
+        xstride = tiles + G
+        seq = dict(k8=int(meta["is8"].sum()), k4=int(meta["is4"].sum()), v8=int(meta["vsel"][I8].sum()),
+                   v4=int(meta["vsel"][I4].sum()), x=nx * xstride)
+        # growth room per sequence: G records per KV head of each kind (V always INT8)
+        room = dict(k8=int((kind == 8).sum()) * G, k4=int((kind == 4).sum()) * G,
+                    v8=int(((kind == 8) | (kind == 4)).sum()) * G, v4=0, x=0)
         row0 = st.rows
-        st.reserve(row0 + batch, max(st.maxn, meta["maxn"]), max(st.tiles_max, tiles),
-                   {k: st.n[k] + batch * seq[k] for k in seq}, k4 is not None or ka4 is not None, bool(exact_kv),
-                   ragged=self.ragged)
+        int4 = k4 is not None or ka4 is not None or bool(room["k4"])
+        st.reserve(row0 + batch, max(st.maxn, meta["maxn"] + G), max(st.tiles_max, tiles + G),
+                   {k: st.n[k] + batch * (seq[k] + room[k]) for k in seq}, int4, bool(exact_kv), ragged=self.ragged)
+        used = dict(st.n)
         self.module.cache_store(dev["bands"], dev["exact"], prompt, kp, k4, ka, ka4, kstat, vstat, packed[I8],
-                                packed.get(I4), kx, vx, len(exact_kv), row0, st.arrays, st.n, st.cap)
+                                packed.get(I4), kx, vx, nx, row0, st.arrays, used, st.cap, xstride=xstride)
+        a = st.arrays
+        if G:
+            # growth regions after the batch's prompt records: sequence s, head h of kind K takes G records
+            # from base_K + (s * heads_K + rank of h among them) * G
+            grow = np.full((batch, hk, 4), -1, np.int32)
+            grow[:, :, 0] = info[None, :]
+            for rec, sel in (("k8", kind == 8), ("k4", kind == 4)):
+                heads = np.flatnonzero(sel)
+                base = st.n[rec] + batch * seq[rec]
+                for r, h in enumerate(heads):
+                    grow[:, h, 1] = base + (np.arange(batch) * len(heads) + r) * G
+            vheads = np.flatnonzero((kind == 8) | (kind == 4))
+            vbase = st.n["v8"] + batch * seq["v8"]
+            for r, h in enumerate(vheads):
+                grow[:, h, 2] = vbase + (np.arange(batch) * len(vheads) + r) * G
+            a["grow"][row0:row0 + batch].copy_(torch.from_numpy(grow))
+        a["count0"][row0:row0 + batch].copy_(a["count"][row0:row0 + batch])
+        if self.ragged and row0:
+            a["count"][:row0].copy_(a["count0"][:row0])  # the earlier rows' tiles taken from their tails go
         st.rows += batch
         for k in seq:
-            st.n[k] += batch * seq[k]
-        st.groups.append(dict(prompt=prompt, batch=batch, hk=hk, tiles=tiles, meta=meta, exact=exact_kv))
+            st.n[k] += batch * (seq[k] + room[k])
+        st.groups.append(dict(prompt=prompt, batch=batch, hk=hk, tiles=tiles, meta=meta, exact=exact_kv, row0=row0,
+                              kind=kind, xstride=xstride, ox=used["x"]))
         if self.step is None:
             self.step = torch.zeros(1, dtype=torch.int64, device=device)
         self.step.zero_()
-        st.arrays["tail_k"][:st.rows].zero_()
-        st.arrays["tail_v"][:st.rows].zero_()
+        self.host_step = 0
+        st.tb = 0
+        a["tail_base"].zero_()
+        a["tail_k"][:st.rows].zero_()
+        a["tail_v"][:st.rows].zero_()
         self.layers[layer] = self._assemble(st)
 
     def _metadata(self, bands, tiles, hk, codes, exact_kv, device):
@@ -325,6 +404,21 @@ class DecodeCache:
             per = self.per or min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 3))))
             bounds_host = bounds = None
             splits = max(1, -(-st.maxn // per))
+        if st.grow_tiles:
+            # tail growth: growth splits of 64 entries after each head's prompt entries (split_range
+            # clamps them to the head's count, which grows as tiles arrive)
+            counts = torch.from_numpy(np.concatenate(
+                [np.repeat(g["meta"]["count"].numpy()[None], g["batch"], 0) for g in groups]).astype(np.int32))
+            if bounds_host is None:
+                runs = -(-int(counts.max()) // per)
+                bounds_host = torch.minimum(torch.arange(runs + 1, dtype=torch.int32)[None, None, :] * per,
+                                            counts[:, :, None])
+            extra = torch.minimum(torch.arange(1, -(-st.grow_tiles // 64) + 1, dtype=torch.int32) * 64,
+                                  torch.tensor(st.grow_tiles, dtype=torch.int32))
+            bounds_host = torch.cat([bounds_host, counts[:, :, None] + extra[None, None, :]], 2).contiguous()
+            splits = bounds_host.shape[2] - 1
+            per = int(bounds_host.diff(dim=2).max())
+            bounds = bounds_host.to(device)
         some = lambda name, n: a[name][:max(1, n)]
         has_x = any(g["exact"] for g in groups)
         return dict(groups=groups, store=st, prompt=a["prompt"][:rows], maxn=st.maxn, per=per, splits=splits,
@@ -337,10 +431,27 @@ class DecodeCache:
                     tail_k=a["tail_k"][:rows], tail_v=a["tail_v"][:rows], batch=rows, tiles_max=st.tiles_max,
                     xslot=a["xslot"][:rows] if has_x else None,
                     kx=a["kx"][:st.n["x"] * KX_BYTES] if has_x else None,
-                    vx=a["vx"][:st.n["x"] * KX_BYTES] if has_x else None)
+                    vx=a["vx"][:st.n["x"] * KX_BYTES] if has_x else None,
+                    grow_splits=-(-st.grow_tiles // 64) if st.grow_tiles else 0)
+
+    def _grow_step(self, layer):
+        """Tail growth bookkeeping before a decode step of ``layer``: when the tail is full and the room
+        for tiles taken from it is used up, the room doubles (a new layer entry).  Returns the entry."""
+        e = self.layers[layer]
+        st = e["store"]
+        if st.grow_tiles:
+            if self.capturing:
+                self._capture_set.add(layer)
+            else:
+                if self.host_step - st.tb >= self.max_tail and st.tb // BN >= st.grow_tiles:
+                    self._extend(st)
+                    e = self.layers[layer] = self._assemble(st)
+                self._called.add(layer)
+        return e
 
     def __call__(self, layer, q, k, v, scale):
-        e = self.layers[layer]
+        e = self._grow_step(layer)
+        st = e["store"]
         hq = q.shape[1]
         splits = e["splits"]
         key = ("partials", hq)
@@ -352,7 +463,10 @@ class DecodeCache:
                       torch.zeros(n * 128, device=q.device))
         dtype = self.out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=dtype, device=q.device)
-        self.plan(layer, q, k, out, scale).run(q, k, v, out)
+        plan = self.plan(layer, q, k, out, scale)
+        if st.grow_tiles:
+            self._spill_plan(e).run()
+        plan.run(q, k, v, out)
         return out
 
     def plan(self, layer, q, k, out, scale):
@@ -362,15 +476,112 @@ class DecodeCache:
         if key not in e:
             hq = q.shape[1]
             if self.tasks and e["xslot"] is None and "tasks" not in e and hasattr(self.module, "decode_tasks"):
-                items = torch.from_numpy(self._task_items(e)).to(q.device)
+                items_host = self._task_items(e)
+                items = torch.from_numpy(items_host).to(q.device)
                 e["tasks"] = self.module.decode_tasks(e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"],
                                                       e["slot"], e["per"], e["bounds"], items)
+                if e["grow_splits"]:
+                    # task row of each head's first growth split (they are listed, in order)
+                    first = np.arange(e["batch"] * e["store"].hk, dtype=np.int64) * e["splits"] + \
+                        (e["splits"] - e["grow_splits"])
+                    rows = np.searchsorted(items_host, first).astype(np.int32)
+                    e["store"].arrays["grow"][:e["batch"], :, 3].copy_(
+                        torch.from_numpy(rows.reshape(e["batch"], e["store"].hk)))
             e[key] = self.module.plan_decode(
                 q, e["k8"], e["k4"], e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"], e["slot"],
                 e["v"][I8], e["v"][I4], e["vstat"], e["kstat"], e["tail_k"], e["tail_v"], k, k, self.step, out,
                 *e[("partials", hq)], e["prompt"], e["per"], scale, e["xslot"], e["kx"], e["vx"], e["bounds"],
-                e.get("tasks") if self.tasks else None)
+                e.get("tasks") if self.tasks else None,
+                tail_base=e["store"].arrays["tail_base"] if e["grow_splits"] else None)
         return e[key]
+
+    def _spill_plan(self, e):
+        """The layer's tail_spill launch (tail growth), built once per cache layout."""
+        if "spill" not in e:
+            st, a, rows = e["store"], e["store"].arrays, e["batch"]
+            if "tasks" not in e or not self.tasks:
+                a["grow"][:rows, :, 3].fill_(-1)
+            dst = dict(entry=e["entry"], kinfo=e["kinfo"], slot=e["slot"], count=e["count"], fmt=e["fmt"],
+                       xslot=e["xslot"], ka=e["ka"], ka4=e["ka4"], kstat=e["kstat"], vstat=e["vstat"], k8=e["k8"],
+                       k4=e["k4"], v8=e["v"][I8], kx=e["kx"], vx=e["vx"])
+            e["spill"] = self.module.plan_tail_spill(self.step, a["tail_base"], e["tail_k"], e["tail_v"],
+                                                     a["grow"][:rows], st.grow_tiles, e["prompt"], dst,
+                                                     e.get("tasks") if self.tasks else None)
+        return e["spill"]
+
+    def _extend(self, st):
+        """Double the room for tiles taken from the tail (when a full tail finds it used up): each
+        (sequence, KV head) gets a new run of records twice as long, the tiles already taken move to its
+        start (records and metadata), and the metadata rows, scales and exact-head records grow to fit."""
+        g0, g1 = st.grow_tiles, 2 * st.grow_tiles
+        n = st.tb // BN  # tiles taken so far (all sequences alike)
+        a = st.arrays
+        rows, hk = st.rows, st.hk
+        room = dict(k8=0, k4=0, v8=0, v4=0, x=0)
+        for g in st.groups:
+            room["k8"] += g["batch"] * int((g["kind"] == 8).sum()) * g1
+            room["k4"] += g["batch"] * int((g["kind"] == 4).sum()) * g1
+            room["v8"] += g["batch"] * int(((g["kind"] == 8) | (g["kind"] == 4)).sum()) * g1
+        st.reserve(rows, st.maxn + g1 - g0, st.tiles_max + g1 - g0, {k: st.n[k] + room[k] for k in room},
+                   a["k4"] is not None, a["kx"] is not None, ragged=self.ragged)
+        grow = a["grow"][:rows].cpu().numpy()
+        count0 = a["count0"][:rows].cpu().numpy()
+        new = grow.copy()
+        moves = {"k8": ([], []), "k4": ([], []), "v8": ([], [])}
+        meta_idx, kinfo_val, slot_val = [], [], []
+        base = dict(st.n)
+        for r in range(rows):
+            for h in range(hk):
+                info, gk, gv = int(grow[r, h, 0]), int(grow[r, h, 1]), int(grow[r, h, 2])
+                if info < 0 or gk < 0:
+                    continue
+                rec = "k4" if (info >> 8) & 1 else "k8"
+                new[r, h, 1], new[r, h, 2] = base[rec], base["v8"]
+                moves[rec][0].extend(range(gk, gk + n))
+                moves[rec][1].extend(range(base[rec], base[rec] + n))
+                moves["v8"][0].extend(range(gv, gv + n))
+                moves["v8"][1].extend(range(base["v8"], base["v8"] + n))
+                for i in range(n):
+                    meta_idx.append((r, h, int(count0[r, h]) + i))
+                    kinfo_val.append((info & 0x1FF) | ((base[rec] + i) << 9))
+                    slot_val.append(base["v8"] + i)
+                base[rec] += g1
+                base["v8"] += g1
+        for rec, (src, dst) in moves.items():
+            if src:
+                arr = a[rec].view(torch.int32)  # (no indexed copies on uint32 tensors)
+                arr[torch.tensor(dst, device=arr.device)] = arr[torch.tensor(src, device=arr.device)]
+        if meta_idx:
+            idx = torch.tensor(meta_idx, dtype=torch.int64).T.to(a["kinfo"].device)
+            a["kinfo"][idx[0], idx[1], idx[2]] = torch.tensor(kinfo_val, dtype=torch.int32, device=idx.device)
+            a["slot"][idx[0], idx[1], idx[2]] = torch.tensor(slot_val, dtype=torch.int32, device=idx.device)
+        a["grow"][:rows].copy_(torch.from_numpy(new))
+        for k in room:
+            st.n[k] += room[k]
+        if a["kx"] is not None and any(g["exact"] for g in st.groups):
+            # exact heads address tile j at xslot + j: give each (sequence, exact head) a longer run
+            kx, vx = a["kx"].view(-1, KX_BYTES), a["vx"].view(-1, KX_BYTES)
+            total = sum(g["batch"] * len(g["exact"]) * (g["xstride"] + g1 - g0) for g in st.groups)
+            nkx = torch.zeros((max(1, total), KX_BYTES), dtype=torch.uint8, device=kx.device)
+            nvx = torch.zeros_like(nkx)
+            xslot = a["xslot"][:rows].cpu().numpy()
+            off = 0
+            for g in st.groups:
+                nx, xs0 = len(g["exact"]), g["xstride"]
+                xs1 = xs0 + g1 - g0
+                for s in range(g["batch"]):
+                    for i, h in enumerate(g["exact"]):
+                        old = g["ox"] + (s * nx + i) * xs0
+                        dst = off + (s * nx + i) * xs1
+                        nkx[dst:dst + xs0] = kx[old:old + xs0]
+                        nvx[dst:dst + xs0] = vx[old:old + xs0]
+                        xslot[g["row0"] + s, h] = dst
+                g["ox"], g["xstride"] = off, xs1
+                off += g["batch"] * nx * xs1
+            a["kx"], a["vx"] = nkx.view(-1), nvx.view(-1)
+            a["xslot"][:rows].copy_(torch.from_numpy(xslot))
+            st.n["x"] = st.cap["x"] = max(1, total)
+        st.grow_tiles = g1
 
     @staticmethod
     def _task_items(e):
@@ -394,6 +605,40 @@ class DecodeCache:
 
     def advance(self):
         self.step.add_(1)
+        if not self.capturing:
+            self._mirror(self._called)
+            self._called = set()
+
+    def _mirror(self, layers):
+        """Host mirror of one step: the device's tail base of each layer in ``layers`` moves by 64 when
+        that step found its tail full with room left (tail_spill's rule), and the step counter by one."""
+        for layer in layers:
+            st = self.layers[layer]["store"]
+            if st.grow_tiles and self.host_step - st.tb >= self.max_tail and st.tb // BN < st.grow_tiles:
+                st.tb += BN
+        self.host_step += 1
+
+    # ---- graph capture of decode steps (extension): the launches of a step stay the same while no
+    # layer has to grow its room for tiles taken from the tail
+    def begin_capture(self):
+        self.capturing = True
+        self._capture_set = set()
+
+    def end_capture(self):
+        self.capturing = False
+
+    def graph_ready(self) -> bool:
+        """Whether a captured step can replay now: no captured layer finds its tail full with its room
+        used up (that step must run eagerly, which grows the room, and the step be captured again)."""
+        for layer in self._capture_set:
+            st = self.layers[layer]["store"]
+            if st.grow_tiles and self.host_step - st.tb >= self.max_tail and st.tb // BN >= st.grow_tiles:
+                return False
+        return True
+
+    def replayed(self):
+        """Record one replay of a captured step (the host mirror of its spills and step advance)."""
+        self._mirror(self._capture_set)
 
     def stored(self, layer):
         return layer in self.layers

@@ -37,7 +37,7 @@ K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
            "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_noalloc",
-           "tri_decode_tasks", "tri_cache_store", "tri_decode_occupancy", "tri_device_cus")
+           "tri_decode_tasks", "tri_cache_store", "tri_tail_spill", "tri_decode_occupancy", "tri_device_cus")
 KX_BYTES = 16384
 TASK_WORDS = 512  # int32 words of the decode task table per (sequence, KV head, split)
 
@@ -64,16 +64,18 @@ def load_library() -> ctypes.CDLL:
     lib.tri_pack_exact.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I, P, I, P, P, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64,
-                   P, P, P, I64, P, I, P, I, D_, P]
+                   P, P, P, I64, P, I, P, I, P, D_, P]
     for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
         getattr(lib, name).argtypes = decode_args
     lib.tri_decode_partials_timed.argtypes = decode_args + [P, P]
     # tri_decode without pm / pl / po (arguments 31-33 of tri_decode)
     lib.tri_decode_noalloc.argtypes = decode_args[:31] + decode_args[34:]
     lib.tri_decode_tasks.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P, I, P, I, P, P]
-    lib.tri_cache_store.argtypes = [P, P, I, I, I, I, I, P, P, P, P, P, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P,
+    lib.tri_cache_store.argtypes = [P, P, I, I, I, I, I, I, P, P, P, P, P, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P,
                                     P, P, P, P, P, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, P, I64, I64,
                                     P]
+    lib.tri_tail_spill.argtypes = [P, P, P, P, I64, I64, I64, I, I, I, I, I, P, I, P, P, P, P, P, P, P, P, P, P, P,
+                                   P, I64, P, I64, P, I64, P, P, I64, P, I, P]
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:
@@ -226,12 +228,14 @@ class Module:
 
     def plan_decode(self, q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail,
                     kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot=None, kxc=None, vxc=None,
-                    bounds=None, tasks=None):
+                    bounds=None, tasks=None, tail_base=None):
         """Validate and marshal every argument of ``decode`` once (extension).  The returned
         plan's ``run(q, kcur, vcur, out, phase)`` launches with new q / k / v / out tensors of the
         planned shapes and strides and the same cache, at a few microseconds of host time.
         ``tasks``: (table, listed splits) as ``decode_tasks`` returns it for this cache and split, or None;
-        the caller keeps the partials of the splits it leaves out empty."""
+        the caller keeps the partials of the splits it leaves out empty.  ``tail_base``: the int64
+        tokens ``tail_spill`` has moved from the tail into the cache (the tail then holds step - tail_base
+        tokens), or None for the reference's tail."""
         _check(q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(2) == 1 and q.size(3) == D and q.stride(3) == 1,
                "q [B,Hq,1,128]")
         b, hq = q.size(0), q.size(1)
@@ -291,6 +295,9 @@ class Module:
             _check(t is None or (t.is_cuda and t.device == q.device and contiguous),
                    f"decode: {name} must be a{'' if name in ('q', 'k', 'tail', 'out') else ' contiguous'} tensor "
                    f"on q's device")
+        _check(tail_base is None or (tail_base.dtype == torch.int64 and tail_base.is_cuda and
+                                     tail_base.device == q.device and tail_base.numel() >= 1),
+               "decode: tail_base int64 on q's device")
         table, n_tasks = tasks if tasks is not None else (None, 0)
         if table is not None:
             _check(table.dtype == torch.int32 and table.is_cuda and table.is_contiguous() and
@@ -305,9 +312,9 @@ class Module:
                 _ptr(pl), _ptr(po), _ptr(prompt_t), b, hq, hk, maxn, int(per), tiles_max, k8c.size(0),
                 0 if k4c is None else k4c.size(0), v8.size(0), v4.size(0), _ptr(xslot), _ptr(kxc),
                 _ptr(vxc), 0 if kxc is None else kxc.numel() * kxc.element_size() // KX_BYTES, _ptr(bounds),
-                splits if bounds is not None else 0, _ptr(table), int(n_tasks), float(scale), 0]
+                splits if bounds is not None else 0, _ptr(table), int(n_tasks), _ptr(tail_base), float(scale), 0]
         keep = (k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, step, pm, pl,
-                po, prompt_t, xslot, kxc, vxc, bounds, table)
+                po, prompt_t, xslot, kxc, vxc, bounds, table, tail_base)
         return DecodePlan(self, args, q, kcur, out, keep)
 
     def decode_tasks(self, ka, ka4, entry, kinfo, count, fmt, slot, per, bounds=None, items=None):
@@ -332,17 +339,20 @@ class Module:
         return table, n
 
     def cache_store(self, bands, exact, t, kp, k4p, ka, ka4, kstat, vstat, v8p, v4p, kx, vx, nx, row0, dst, used,
-                    cap):
+                    cap, xstride=None):
         """Append one Prefill call's batch to a decode cache on the device (extension; the reference
         assembles its cache on the host, kernels/decode.py:24-67).  Sources as ``store`` receives them;
         ``dst`` the cache's arrays (entry / kinfo / slot [rows][hk][maxn], count, fmt, prompt, xslot, ka,
         ka4, kstat, vstat, compacted k8 / k4 / v8 / v4 records and kx / vx bytes), ``used`` / ``cap`` the
-        records in use and held per kind (k8, k4, v8, v4, x), sequence rows from ``row0``."""
+        records in use and held per kind (k8, k4, v8, v4, x), sequence rows from ``row0``.  ``xstride``:
+        KX / VX records per (sequence, exact head) in the cache (default: the prompt's tiles)."""
         b, hk = vstat.shape[0], vstat.shape[1]
         hq = bands.shape[0]
         rows, maxn = dst["entry"].shape[0], dst["entry"].shape[2]
         tiles_max = dst["fmt"].shape[1]
         tiles = (t + 63) // 64
+        xstride = tiles if xstride is None else int(xstride)
+        _check(xstride >= tiles, "cache_store: xstride below the prompt's tiles")
         _check(bands.dtype == torch.int32 and bands.is_cuda and bands.is_contiguous() and bands.dim() == 2 and
                bands.size(1) == 2, "cache_store: bands int32 [Hq,2] on the device")
         _check(exact is None or (exact.dtype == torch.int32 and exact.is_cuda and exact.numel() == hk),
@@ -372,13 +382,54 @@ class Module:
         _check(dst["kx"] is None or dst["kx"].numel() >= cap["x"] * KX_BYTES, "cache_store: KX/VX record arrays")
         p = _ptr
         with torch.cuda.device(vstat.device):
-            self._call(self.lib.tri_cache_store, p(bands), p(exact), b, hq, hk, int(t), int(nx), p(kp), p(k4p), p(ka),
+            self._call(self.lib.tri_cache_store, p(bands), p(exact), b, hq, hk, int(t), int(nx), xstride, p(kp), p(k4p),
+                       p(ka),
                        p(ka4), p(kstat), p(vstat), p(v8p), p(v4p), p(kx), p(vx), int(row0), rows, maxn, tiles_max,
                        p(dst["entry"]), p(dst["kinfo"]), p(dst["slot"]), p(dst["count"]), p(dst["fmt"]),
                        p(dst["prompt"]), p(dst["xslot"]), p(dst["ka"]), p(dst["ka4"]), p(dst["kstat"]),
                        p(dst["vstat"]), p(dst["k8"]), used["k8"], cap["k8"], p(dst["k4"]), used["k4"], cap["k4"],
                        p(dst["v8"]), used["v8"], cap["v8"], p(dst["v4"]), used["v4"], cap["v4"], p(dst["kx"]),
                        p(dst["vx"]), used["x"], cap["x"], self._stream(vstat.device))
+
+    def plan_tail_spill(self, step, tail_base, ktail, vtail, grow, cap, prompt, dst, tasks=None):
+        """Validate and marshal one layer's ``tail_spill`` launch (extension; the reference clamps its
+        tail, common_device.cuh:384).  ``dst``: the cache arrays as ``cache_store`` takes them (entry /
+        kinfo / slot, count, fmt, xslot, ka, ka4, kstat, vstat, k8 / k4 / v8 records, kx / vx bytes);
+        ``grow`` int32 [rows, hk, 4]; ``cap`` spilled tiles per head the arrays hold; ``tasks`` the
+        decode's (table, n) or None.  The plan's ``run()`` launches on the current stream."""
+        rows, hk, maxn = dst["entry"].shape
+        tiles_max = dst["fmt"].shape[1]
+        max_tail = ktail.size(2)
+        _check(step.dtype == tail_base.dtype == torch.int64 and tail_base.numel() == 2 and step.is_cuda and
+               tail_base.is_cuda, "tail_spill: step int64 and tail_base int64 [2] on the device")
+        _check(ktail.dtype == torch.bfloat16 and ktail.dim() == 4 and tuple(ktail.shape[:2]) == (rows, hk) and
+               ktail.size(3) == D and ktail.stride(3) == 1 and _geometry(vtail) == _geometry(ktail),
+               "tail_spill: tails bf16 [rows,Hk,max_tail,128], K and V alike")
+        _check(64 <= max_tail <= 1024, "tail_spill: max_tail must be in [64, 1024]")
+        _check(grow.dtype == torch.int32 and grow.is_contiguous() and tuple(grow.shape) == (rows, hk, 4),
+               "tail_spill: grow int32 [rows,Hk,4]")
+        _check(prompt.dtype == torch.int32 and prompt.numel() == rows and int(cap) >= 0, "tail_spill: prompt / cap")
+        for name in ("kinfo", "slot"):
+            _check(tuple(dst[name].shape) == (rows, hk, maxn), f"tail_spill: {name}")
+        _check(tuple(dst["ka"].shape) == (rows, hk, tiles_max, 4) and tuple(dst["count"].shape) == (rows, hk) and
+               (dst["ka4"] is None or tuple(dst["ka4"].shape) == (rows, hk, tiles_max, 4)) and
+               tuple(dst["kstat"].shape) == (rows, hk, 3, D) and tuple(dst["vstat"].shape) == (rows, hk, 3, D) and
+               (dst["xslot"] is None or tuple(dst["xslot"].shape) == (rows, hk)), "tail_spill: cache rows")
+        for kind, words in (("k8", K8_WORDS), ("k4", K4_WORDS), ("v8", V8_WORDS)):
+            x = dst[kind]
+            _check(x is None or (x.dim() == 2 and x.shape[1] == words), f"tail_spill: {kind} record array")
+        table, n_tasks = tasks if tasks is not None else (None, 0)
+        xb = lambda x: 0 if x is None else x.numel() * x.element_size() // KX_BYTES
+        p = _ptr
+        args = [p(step), p(tail_base), p(ktail), p(vtail), ktail.stride(0), ktail.stride(1), ktail.stride(2),
+                max_tail, rows, hk, maxn, tiles_max, p(grow), int(cap), p(prompt), p(dst["xslot"]), p(dst["entry"]),
+                p(dst["kinfo"]), p(dst["slot"]), p(dst["count"]), p(dst["fmt"]), p(dst["ka"]), p(dst["ka4"]),
+                p(dst["kstat"]), p(dst["vstat"]), p(dst["k8"]), dst["k8"].shape[0], p(dst["k4"]),
+                0 if dst["k4"] is None else dst["k4"].shape[0], p(dst["v8"]), dst["v8"].shape[0],
+                p(dst["kx"] if dst["xslot"] is not None else None), p(dst["vx"] if dst["xslot"] is not None else None),
+                xb(dst["kx"]) if dst["xslot"] is not None else 0, p(table), int(n_tasks), 0]
+        keep = (step, tail_base, ktail, vtail, grow, prompt, table, dict(dst))
+        return SpillPlan(self, args, ktail.device, keep)
 
     def decode_occupancy(self) -> int:
         """Resident decode workgroups per compute unit."""
@@ -401,7 +452,7 @@ def _geometry(t):
 class DecodePlan:
     """A validated, marshalled ``decode`` call; ``run`` swaps in the per-step tensors."""
 
-    Q, QSB, QSH, KC, VC, KSB, KSH, OUT, STREAM = 0, 1, 2, 22, 23, 24, 25, 27, 54
+    Q, QSB, QSH, KC, VC, KSB, KSH, OUT, STREAM = 0, 1, 2, 22, 23, 24, 25, 27, 55
 
     def __init__(self, module, args, q, kcur, out, keep):
         self.module, self.args, self.keep = module, args, keep
@@ -431,6 +482,24 @@ class DecodePlan:
         else:
             self.module._call(fn, *a, *extra)
         return out
+
+
+class SpillPlan:
+    """A validated, marshalled ``tail_spill`` launch for one layer's decode cache."""
+
+    STREAM = 36
+
+    def __init__(self, module, args, device, keep):
+        self.module, self.args, self.device, self.keep = module, args, device, keep
+
+    def run(self):
+        index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        self.args[self.STREAM] = torch.cuda.current_stream(index).cuda_stream
+        if torch.cuda.current_device() != index:
+            with torch.cuda.device(index):
+                self.module._call(self.module.lib.tri_tail_spill, *self.args)
+        else:
+            self.module._call(self.module.lib.tri_tail_spill, *self.args)
 
 
 def _only_f16(bands, tiles: int) -> bool:

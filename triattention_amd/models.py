@@ -17,7 +17,11 @@ bf16, so each q-head attends causally over the unquantized bf16 operands with
 fp32 accumulation.
 
 Extensions: ``TriAttention`` accepts a map path or a ``bands_fn`` (as built by
-``triattention_amd.maps``), and an optional ``module`` (the loaded extension).
+``triattention_amd.maps``), an optional ``module`` (the loaded extension) and
+an optional ``max_tail``: with more new tokens than the tail holds (the
+reference's tail is max_new_tokens long, and its kernels cap it at 1024), the
+decode cache grows, taking the oldest 64 tail tokens into a new quantized tile
+whenever the tail is full.
 
 Loading checkpoints and tokenizers, chat templates and end-of-sequence ids
 (models.py:16-42) are the caller's: any HF causal LM whose attention modules
@@ -79,10 +83,14 @@ class TriAttention:
     """Quantized attention for a HF model: prompt through ``Prefill``, generated tokens through
     ``DecodeCache`` (models.py:58-85)."""
 
-    def __init__(self, model, qk_map=None, max_new_tokens=256, module=None):
+    def __init__(self, model, qk_map=None, max_new_tokens=256, module=None, max_tail=None):
         self.model = model
         module = module if module is not None else load_extension()
-        self.decode_cache = DecodeCache(module, max_tail=max_new_tokens)
+        # the reference sizes the tail for every new token (max_tail = max_new_tokens); past the tail's
+        # 1024-token cap, or with a shorter max_tail, the cache grows instead
+        max_tail = min(max_new_tokens, 1024) if max_tail is None else int(max_tail)
+        grow = max_new_tokens - max_tail + 64 if max_new_tokens > max_tail else 0
+        self.decode_cache = DecodeCache(module, max_tail=max_tail, grow_tail=grow)
         bands_fn = qk_map if callable(qk_map) else load_map(qk_map or preset(model), model)
         self.prefill = Prefill(module, bands_fn, self.decode_cache)
 
@@ -105,15 +113,19 @@ class TriAttention:
         out = self.model(input_ids=ids, use_cache=False, logits_to_keep=1)
         tokens = []
         step = None
+        cache = self.decode_cache
         for i in range(max_new_tokens):
             token = int(out.logits[0, -1].argmax())
             if token in eos:
                 break
             tokens.append(token)
-            if step is not None:
+            # (a step at which a layer's tail is full and its room for tiles taken from the tail used
+            # up runs eagerly, which grows the room, and the step is captured again)
+            if step is not None and cache.graph_ready():
                 step.ids.fill_(token)
                 step.position.fill_(ids.shape[1] + i)
                 out = step.replay()
+                cache.replayed()
                 continue
             position = torch.tensor([[ids.shape[1] + i]], device=ids.device)
             out = self.model(input_ids=torch.tensor([[token]], device=ids.device), position_ids=position,
@@ -139,9 +151,13 @@ class _GraphStep:
             model(input_ids=self.ids, position_ids=self.position, use_cache=False)
         torch.cuda.current_stream(device).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.out = model(input_ids=self.ids, position_ids=self.position, use_cache=False)
-            cache.advance()
+        cache.begin_capture()
+        try:
+            with torch.cuda.graph(self.graph):
+                self.out = model(input_ids=self.ids, position_ids=self.position, use_cache=False)
+                cache.advance()
+        finally:
+            cache.end_capture()
 
     def replay(self):
         self.graph.replay()

@@ -91,7 +91,8 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
  * out [batch][hq][1][128] (strides o_sb, o_sh), out_dtype 0 = fp32, 1 = bf16;
  * pm/pl f32 [batch][hq][splits], po f32 [batch][hq][splits][128] with
  * splits = max(1, ceil(maxn / per)) with 1 <= per <= 64; n_k8/n_k4/n_v8/n_v4 are the record
- * counts of the compacted arrays (each array below 2 GiB).
+ * counts of the compacted arrays (K arrays at most 2^23 records, the kinfo slot field; every record is
+ * addressed through its own 64-bit base, so no 32-bit byte-offset limit applies).
  * Exact (bf16) KV heads (extension): xslot NULL, or int32 [batch][hk] with -1
  * for a quantized head and otherwise the index of the head's first KX/VX
  * record in kxc/vxc (tri_pack_exact layout, n_kx records of 16 KiB each); such
@@ -174,8 +175,8 @@ int tri_decode_partials_timed(const void* q, int64_t q_sb, int64_t q_sh, const v
  * Work items are (sequence, KV head, split) of the split tri_decode makes from per / bounds (splits =
  * nsplit with bounds, else max(1, ceil(maxn / per))), numbered ((sequence * hk) + head) * splits + split.
  * For the i-th of the n_items items listed in items (int32 on the device; NULL lists every item in
- * order), 512 int32 at tasks + i * 512: an int4 per lane L (K record byte offset, V record byte
- * offset, rowmask | INT4-K << 8 | INT8-V << 9 | tile << 10, and the work item in lane 0 / the split's
+ * order), 512 int32 at tasks + i * 512: an int4 per lane L (K record slot, V record
+ * slot, rowmask | INT4-K << 8 | INT8-V << 9 | tile << 10, and the work item in lane 0 / the split's
  * entry count in the other lanes) for the split's entry L, then a float4 per lane (the tile's K group
  * scales).  16-byte aligned.  Rebuild it whenever the cache or its split partition changes. */
 int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,

@@ -185,8 +185,8 @@ class HostSpill:
                     if row_t < n:
                         lane = k % 64
                         w = table[row_t * 512:(row_t + 1) * 512]
-                        w[4 * lane] = ks * (4096 if is4 else 8192)
-                        w[4 * lane + 1] = vs * 8192
+                        w[4 * lane] = ks
+                        w[4 * lane + 1] = vs
                         w[4 * lane + 2] = (info & 0x1FF) | (1 << 9) | (j << 10)
                         if lane > 0:
                             w[4 * lane + 3] = lane + 1

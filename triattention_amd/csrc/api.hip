@@ -261,18 +261,18 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
     return fail("decode: tail buffers must be 16-byte aligned rows");
   if (!aligned(po, 16)) return fail("decode: po must be 16-byte aligned");
   const int splits = bounds ? nsplit : std::max(1, (maxn + per - 1) / per);
-  const int64_t lim = (int64_t)1 << 31;
-  if (n_k8 < 1 || n_v8 < 1 || n_v4 < 1 || n_k8 * tri::K8_BYTES >= lim || n_k4 * tri::K4_BYTES >= lim ||
-      n_v8 * tri::V8_BYTES >= lim || n_v4 * tri::V4_BYTES >= lim || (k4c != nullptr && n_k4 < 1))
-    return fail("decode: compacted record arrays must be non-empty and below 2 GiB each");
-  if (xslot != nullptr && (!kxc || !vxc || n_kx < 1 || n_kx * tri::KX_BYTES >= lim || !aligned(kxc, 16) ||
-                           !aligned(vxc, 16)))
-    return fail("decode: exact heads need 16-byte aligned KX/VX record arrays, non-empty and below 2 GiB");
+  // record slots: K slots in the 23-bit kinfo field, V and exact-record slots in int32
+  const int64_t kslots = (int64_t)1 << 23, slots = ((int64_t)1 << 31) - 1;
+  if (n_k8 < 1 || n_v8 < 1 || n_v4 < 1 || n_k8 > kslots || n_k4 > kslots || n_v8 > slots || n_v4 > slots ||
+      (k4c != nullptr && n_k4 < 1))
+    return fail("decode: compacted record arrays must be non-empty, K arrays of at most 2^23 records");
+  if (xslot != nullptr && (!kxc || !vxc || n_kx < 1 || n_kx > slots || !aligned(kxc, 16) || !aligned(vxc, 16)))
+    return fail("decode: exact heads need 16-byte aligned KX/VX record arrays, non-empty");
   tri::DecodeArgs d;
   d.xslot = xslot;
   d.kxc = static_cast<const uint8_t*>(kxc);
   d.vxc = static_cast<const uint8_t*>(vxc);
-  d.kx_bytes = xslot ? (int)(n_kx * tri::KX_BYTES) : 0;
+  d.n_kx = xslot ? n_kx : 0;
   d.kstat = kstat;
   d.vstat = vstat;
   d.q = static_cast<const uint16_t*>(q);
@@ -339,10 +339,10 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
     d.items = (int)items;
   }
   d.sm_log2 = (float)(scale * 1.4426950408889634);
-  d.k8_bytes = (int)(n_k8 * tri::K8_BYTES);
-  d.k4_bytes = k4c ? (int)(n_k4 * tri::K4_BYTES) : 0;
-  d.v8_bytes = (int)(n_v8 * tri::V8_BYTES);
-  d.v4_bytes = (int)(n_v4 * tri::V4_BYTES);
+  d.n_k8 = n_k8;
+  d.n_k4 = k4c ? n_k4 : 0;
+  d.n_v8 = n_v8;
+  d.n_v4 = n_v4;
   tri::MergeArgs mg;
   mg.pm = pm;
   mg.pl = pl;
@@ -550,10 +550,10 @@ int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int h
   if (o8 < 0 || o4 < 0 || ov8 < 0 || ov4 < 0 || ox < 0) return fail("cache_store: negative record offset");
   if ((k4c == nullptr) != (cap4 == 0) || (v4c == nullptr) != (capv4 == 0))
     return fail("cache_store: INT4 K / V destinations and capacities (both or neither)");
-  if (cap8 * tri::K8_BYTES >= ((int64_t)1 << 31) || cap4 * tri::K4_BYTES >= ((int64_t)1 << 31) ||
-      capv8 * tri::V8_BYTES >= ((int64_t)1 << 31) || capv4 * tri::V4_BYTES >= ((int64_t)1 << 31) ||
-      capx * tri::KX_BYTES >= ((int64_t)1 << 31))
-    return fail("cache_store: compacted record arrays must stay below 2 GiB each");
+  // record slots: K slots in the 23-bit kinfo field, V and exact-record slots in int32
+  if (cap8 > ((int64_t)1 << 23) || cap4 > ((int64_t)1 << 23) || capv8 >= ((int64_t)1 << 31) ||
+      capv4 >= ((int64_t)1 << 31) || capx >= ((int64_t)1 << 31))
+    return fail("cache_store: K record arrays hold at most 2^23 records, V and KX/VX arrays fewer than 2^31");
   for (const void* p : {kp, k4p, v8p, v4p, kx, vx, (const void*)k8c, (const void*)k4c, (const void*)v8c,
                         (const void*)v4c, (const void*)kxc, (const void*)vxc})
     if (p && !aligned(p, 16)) return fail("cache_store: record arrays must be 16-byte aligned");
@@ -633,10 +633,9 @@ int tri_tail_spill(const int64_t* step, int64_t* tail_base, void* ktail, void* v
   if ((k4c == nullptr) != (ka4 == nullptr)) return fail("tail_spill: INT4 K records and scales (both or neither)");
   if (xslot && (!kxc || !vxc)) return fail("tail_spill: exact heads need KX/VX record arrays");
   if (tasks && n_tasks < 1) return fail("tail_spill: a task table needs n_tasks >= 1");
-  const int64_t lim = (int64_t)1 << 31;
-  if (n_k8 < 1 || n_v8 < 1 || n_k8 * tri::K8_BYTES >= lim || n_k4 * tri::K4_BYTES >= lim ||
-      n_v8 * tri::V8_BYTES >= lim || n_kx * tri::KX_BYTES >= lim)
-    return fail("tail_spill: compacted record arrays must be non-empty and below 2 GiB each");
+  if (n_k8 < 1 || n_v8 < 1 || n_k8 > ((int64_t)1 << 23) || n_k4 > ((int64_t)1 << 23) || n_v8 >= ((int64_t)1 << 31) ||
+      n_kx >= ((int64_t)1 << 31))
+    return fail("tail_spill: record arrays must be non-empty, K arrays of at most 2^23 records");
   for (const void* p : {(const void*)k8c, (const void*)k4c, (const void*)v8c, (const void*)kxc, (const void*)vxc})
     if (p && !aligned(p, 16)) return fail("tail_spill: record arrays must be 16-byte aligned");
   tri::SpillArgs a;

@@ -38,7 +38,7 @@ struct DecodeArgs {
   int64_t qsb, qsh;
   int hq, hk, maxn, per, tiles_max, splits;
   float sm_log2;
-  int k8_bytes, k4_bytes, v8_bytes, v4_bytes;  // sizes of the compacted record arrays (< 2^31)
+  int64_t n_k8, n_k4, n_v8, n_v4;  // records in the compacted arrays
   // exact (bf16) KV heads: xslot[B][Hk] = first KX/VX record of the (sequence,
   // KV head) whose tiles are all kept (record of tile j at xslot + j), or -1
   // for a quantized head; xslot may be null when no head is exact
@@ -47,7 +47,7 @@ struct DecodeArgs {
   const uint8_t* vxc;
   const float* kstat;   // [B][Hk][3][128]: K mean (the frame of the merge's tail scores)
   const float* vstat;   // [B][Hk][3][128]: V mean, scale, 1/scale
-  int kx_bytes;
+  int64_t n_kx;
   // work scatter: the grid is 1-D with `launched` = items | 1 workgroups (odd); workgroup lin takes work
   // item lin * scatter mod launched (a permutation), and the one padding item (>= items) exits
   int64_t scatter;
@@ -84,11 +84,21 @@ __device__ __forceinline__ void split_range(const DecodeArgs& a, int64_t hb, int
   }
 }
 
-constexpr int OUT_OF_RANGE = (int)0x80000000u;  // a record offset >= any record array size (< 2 GiB)
+constexpr int NO_RECORD = -1;  // the record slot of an entry past a split's end (its loads read zeros)
+
+// Buffer descriptor of record `slot` (`bytes` long) of an array of n records: loads through it at
+// offsets past the record, or through the descriptor of a slot outside the array (num_records 0),
+// return zeros without touching memory.  Each record gets its own 64-bit base, so the arrays may
+// exceed the 32-bit offsets of a single descriptor.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_rsrc(const uint8_t* base, int slot, int64_t n, int bytes) {
+  const bool ok = slot >= 0 && slot < n;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)(ok ? slot : 0) * bytes), (short)0,
+                                           ok ? bytes : 0, 0x00020000);
+}
 constexpr int TASK_WORDS = 512;
 
 // Task table of the split kernel (extension): lane L of work item (sequence, KV head, split) gets
-// entry first + L of the split -- its K and V record byte offsets, rowmask | INT4-K << 8 | INT8-V << 9
+// entry first + L of the split -- its K and V record slots, rowmask | INT4-K << 8 | INT8-V << 9
 // | tile << 10, the split's entry count, and the tile's four K group scales.  The split kernel then
 // starts streaming a split's records one memory round trip after it starts, instead of three (split
 // bounds, then entry / kinfo / slot, then the records).  Built once per cache layout: the entries and
@@ -101,7 +111,7 @@ __global__ __launch_bounds__(64) void decode_tasks_kernel(DecodeArgs a, const in
   int first, last;
   split_range(a, hb, split, first, last);
   const int n = max(0, last - first);
-  int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, 1 << 9, L == 0 ? item : n);
+  int4 w = make_int4(NO_RECORD, NO_RECORD, 1 << 9, L == 0 ? item : n);
   float4 ks = make_float4(1.f, 1.f, 1.f, 1.f);
   if (L < n) {
     const int64_t li = hb * a.maxn + min(first + L, a.maxn - 1);
@@ -109,8 +119,8 @@ __global__ __launch_bounds__(64) void decode_tasks_kernel(DecodeArgs a, const in
     const int is4 = (info >> 8) & 1;
     const int j = min(max(er & ENTRY_TILE, 0), a.tiles_max - 1);
     const int vf = (er & ENTRY_VFMT) ? ((er & ENTRY_V8) ? 1 : 2) : a.fmt[(int64_t)b * a.tiles_max + j];
-    w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
-    w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
+    w.x = (int)((unsigned)info >> 9);
+    w.y = vs;
     w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
     ks = *reinterpret_cast<const float4*>(((is4 && a.ka4) ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
   }
@@ -164,8 +174,6 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
   }
   cq += __shfl_xor(cq, 32, 64);
   __syncthreads();
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)a.kxc, (short)0, a.kx_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)a.vxc, (short)0, a.kx_bytes, 0x00020000);
   v16f acc[4];
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb)
@@ -173,16 +181,19 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
     for (int r = 0; r < 16; ++r) acc[cb][r] = 0.f;
   float m = -3.402823466e38f, den = 0.f;
   v4i kf[8], vf[8];
-  // half step hs covers keys 32*(hs & 1) .. +31 of tile first + hs / 2; the
+  // half step hs covers keys 32*(hs & 1) .. +31 of tile first + hs / 2 (record x0 + tile); the
   // next half's K streams in after the QK MFMAs, its V after the PV MFMAs
-  auto off_of = [&](int hs) { return (x0 + first + (hs >> 1)) * KX_BYTES + (hs & 1) * (KX_BYTES / 2); };
   auto load_k = [&](int hs) {
+    const __amdgpu_buffer_rsrc_t rk = record_rsrc(a.kxc, x0 + first + (hs >> 1), a.n_kx, KX_BYTES);
 #pragma unroll
-    for (int F = 0; F < 8; ++F) kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, L * 16 + F * 1024, off_of(hs), 0);
+    for (int F = 0; F < 8; ++F)
+      kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, L * 16 + F * 1024, (hs & 1) * (KX_BYTES / 2), 0);
   };
   auto load_v = [&](int hs) {
+    const __amdgpu_buffer_rsrc_t rv = record_rsrc(a.vxc, x0 + first + (hs >> 1), a.n_kx, KX_BYTES);
 #pragma unroll
-    for (int F = 0; F < 8; ++F) vf[F] = __builtin_amdgcn_raw_buffer_load_b128(rv, L * 16 + F * 1024, off_of(hs), 0);
+    for (int F = 0; F < 8; ++F)
+      vf[F] = __builtin_amdgcn_raw_buffer_load_b128(rv, L * 16 + F * 1024, (hs & 1) * (KX_BYTES / 2), 0);
   };
   const int steps = 2 * max(0, last - first);
   if (steps > 0) {
@@ -356,12 +367,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     for (int cb = 0; cb < 4; ++cb) acc[cb][r] = 0.f;
   }
   const int64_t mbase = hb * a.maxn;
-  // Record streams are read through buffer descriptors (uniform base, 32-bit
-  // lane offsets); an out-of-range offset reads zeros instead of faulting.
-  const __amdgpu_buffer_rsrc_t rk8 = __builtin_amdgcn_make_buffer_rsrc((void*)a.k8c, (short)0, a.k8_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rk4 = __builtin_amdgcn_make_buffer_rsrc((void*)a.k4c, (short)0, a.k4_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv8 = __builtin_amdgcn_make_buffer_rsrc((void*)a.v8c, (short)0, a.v8_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv4 = __builtin_amdgcn_make_buffer_rsrc((void*)a.v4c, (short)0, a.v4_bytes, 0x00020000);
+  // Record streams are read through one buffer descriptor per record (record_rsrc: uniform 64-bit
+  // base, 32-bit lane offsets); a slot outside its array, or an offset past its record, reads zeros.
   v4i kf[8], vf8[8];
   float kav[2], kmax = 0.f;
   // Per-tile metadata of this split in LDS: lane L loads entry first + L with
@@ -371,12 +378,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   // use of one waits for every outstanding scalar and LDS access; per-tile
   // scalar loads would stall every tile on the metadata of the tiles after it.
   struct Meta {
-    int info, j, vf, koff, voff;
+    int info, j, vf, kslot, vslot;
   };
   auto unpack = [](const int4& v) {
     Meta m;
-    m.koff = __builtin_amdgcn_readfirstlane(v.x);
-    m.voff = __builtin_amdgcn_readfirstlane(v.y);
+    m.kslot = __builtin_amdgcn_readfirstlane(v.x);
+    m.vslot = __builtin_amdgcn_readfirstlane(v.y);
     const int z = __builtin_amdgcn_readfirstlane(v.z);
     m.info = z & 0x1ff;
     m.vf = ((z >> 9) & 1) ? 1 : 2;
@@ -402,21 +409,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     // would make the compiler wait for every outstanding load at each tile): a
     // K8 record is fragments 0..7; a K4 record takes four loads (its fragment
     // pairs, or with DUP the lane's own key), and the upper four loads are past
-    // the end of the range (zeros, no memory access).
-    const __amdgpu_buffer_rsrc_t rk = is4 ? rk4 : rk8;
-    const int hi = is4 ? OUT_OF_RANGE : m.koff;
+    // the end of its 4 KiB record (zeros, no memory access).
+    const __amdgpu_buffer_rsrc_t rk =
+        is4 ? record_rsrc(a.k4c, m.kslot, a.n_k4, K4_BYTES) : record_rsrc(a.k8c, m.kslot, a.n_k8, K8_BYTES);
 #pragma unroll
     for (int F = 0; F < 8; ++F) {
       const int vo = (DUP && F < 4 && is4) ? k4off[F] : L * 16 + F * 1024;
-      kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo, F < 4 ? m.koff : hi, 0);
+      kf[F] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, 0);
     }
   };
   auto load_v = [&](const Meta& m) {
     const bool v4 = m.vf != 1;
-    const __amdgpu_buffer_rsrc_t rv = v4 ? rv4 : rv8;
-    const int hi = v4 ? OUT_OF_RANGE : m.voff;
+    const __amdgpu_buffer_rsrc_t rv =
+        v4 ? record_rsrc(a.v4c, m.vslot, a.n_v4, V4_BYTES) : record_rsrc(a.v8c, m.vslot, a.n_v8, V8_BYTES);
 #pragma unroll
-    for (int F = 0; F < 8; ++F) vf8[F] = __builtin_amdgcn_raw_buffer_load_b128(rv, L * 16 + F * 1024, F < 4 ? m.voff : hi, 0);
+    for (int F = 0; F < 8; ++F) vf8[F] = __builtin_amdgcn_raw_buffer_load_b128(rv, L * 16 + F * 1024, 0, 0);
   };
   // fragment f of a 4-bit record: half (f & 1) of load f >> 1, expanded to 16*code bytes
   auto frag4 = [](const v4i (&w)[8], int f) {
@@ -429,14 +436,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   // loads; the tile index is clamped too, as entries past the count are not
   // tiles); lanes past the split's end get the out-of-range offsets.
   Meta mc;  // the split's first tile
-  int4 w = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);  // koff, voff, info | v8 << 9 | j << 10
+  int4 w = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);  // kslot, vslot, info | v8 << 9 | j << 10
   float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
   if (a.tasks != nullptr && !EXACT) {
     // the task table holds this lane's entry ready: the records stream right away
     w = make_int4(task_w.x, task_w.y, task_w.z, 0);
     ka = task_k;
     Meta m0;
-    m0.koff = __builtin_amdgcn_readlane(w.x, wv);
+    m0.kslot = __builtin_amdgcn_readlane(w.x, wv);
     m0.info = __builtin_amdgcn_readlane(w.z & 0x1ff, wv);
     load_k(m0);
     mc = unpack(int4{__builtin_amdgcn_readlane(w.x, wv), __builtin_amdgcn_readlane(w.y, wv),
@@ -445,7 +452,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     meta[L] = w;
     metk[L] = ka;
     if (L == 0) {
-      meta[MAX_PER] = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);
+      meta[MAX_PER] = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);
       metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
     }
   } else {
@@ -462,11 +469,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     // LDS writes below) then holds no record load
     const float4 kl = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
     __builtin_amdgcn_sched_barrier(0);
-    if (valid) w.x = (int)((unsigned)info >> 9) * (is4 ? K4_BYTES : K8_BYTES);
+    if (valid) w.x = (int)((unsigned)info >> 9);
     {
       // the wave's first tile's K streams (lane wv holds entry first + wv)
       Meta m0;
-      m0.koff = __builtin_amdgcn_readlane(w.x, wv);
+      m0.kslot = __builtin_amdgcn_readlane(w.x, wv);
       m0.info = __builtin_amdgcn_readlane(info & 0x1ff, wv);
       load_k(m0);
     }
@@ -479,7 +486,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
       asm volatile("" ::"v"(vf));  // wait for it here, so that no wait follows the join
     }
     if (valid) {
-      w.y = vs * (vf == 1 ? V8_BYTES : V4_BYTES);
+      w.y = vs;
       w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
     }
     mc = unpack(int4{__builtin_amdgcn_readlane(w.x, wv), __builtin_amdgcn_readlane(w.y, wv),
@@ -489,7 +496,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     meta[L] = w;
     metk[L] = ka;
     if (L == 0) {
-      meta[MAX_PER] = make_int4(OUT_OF_RANGE, OUT_OF_RANGE, (1 << 9), 0);
+      meta[MAX_PER] = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);
       metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
     }
   }

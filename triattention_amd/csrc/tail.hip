@@ -111,8 +111,8 @@ __global__ __launch_bounds__(SPILL_THREADS) void tail_spill_kernel(SpillArgs a) 
         if (a.tasks != nullptr && tr >= 0 && tr < a.n_tasks) {
           int32_t* t = a.tasks + (int64_t)tr * TASK_WORDS;
           if (tid == 0) {
-            t[4 * lane] = (int)(ks * (is4 ? K4_BYTES : K8_BYTES));
-            t[4 * lane + 1] = (int)(vs * V8_BYTES);
+            t[4 * lane] = (int)ks;
+            t[4 * lane + 1] = (int)vs;
             t[4 * lane + 2] = (gr.x & 0x1ff) | (1 << 9) | (j << 10);
             if (lane > 0) t[4 * lane + 3] = lane + 1;
             t[4 * 1 + 3] = lane + 1;  // the split's entry count (lane 1's word; lane 0's holds the item)

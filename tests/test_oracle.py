@@ -7,6 +7,8 @@ fp32 rounding, and invariants.
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -33,6 +35,32 @@ def test_texp2_faithful_over_domain():
     y = O.texp2(x)
     ref = np.exp2(x.astype(np.float64))
     assert ulp_err(y, ref).max() <= 1.0
+
+
+# exp2f of S. L. Moshier's Cephes Math Library (single precision): 2^x = 1 + x P(x) on [-0.5, 0.5],
+# P's coefficients from the highest degree down, as published (decimal)
+CEPHES_EXP2F_P = (1.535336188319500e-4, 1.339887440266574e-3, 9.618437357674640e-3, 5.550332471162809e-2,
+                  2.402264791363012e-1, 6.931472028550421e-1)
+
+
+def test_texp2_is_the_cephes_polynomial():
+    """texp2's 2^f is the Cephes exp2f polynomial with its coefficients rounded to binary32, evaluated by
+    fma in Horner order: the oracle's values equal that evaluation (fma emulated in float64, exact
+    products; a double rounding may move a result by one ulp) on a dense sample of f in [-0.5, 0.5]."""
+    f = np.linspace(-0.5, 0.5, 200_001).astype(np.float32)
+    c = [np.float32(x) for x in CEPHES_EXP2F_P] + [np.float32(1.0)]
+    p = np.full_like(f, c[0])
+    for k in c[1:]:
+        p = (p.astype(np.float64) * f.astype(np.float64) + np.float64(k)).astype(np.float32)
+    y = O.texp2(f)
+    diff = np.abs(y.view(np.int32).astype(np.int64) - p.view(np.int32).astype(np.int64))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.999
+    # a different polynomial of the same degree (the Taylor coefficients ln2^k / k!) is told apart
+    t = [np.float32(np.log(2) ** k / math.factorial(k)) for k in range(6, -1, -1)]
+    q = np.full_like(f, t[0])
+    for k in t[1:]:
+        q = (q.astype(np.float64) * f.astype(np.float64) + np.float64(k)).astype(np.float32)
+    assert (q != y).mean() > 0.1
 
 
 def test_texp2_special_values():

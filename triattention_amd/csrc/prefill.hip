@@ -133,7 +133,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   // and |PV| < 2^21 per tile, so acc stays below 2^(64 + 21 + 11) over 2048
   // tiles, far inside fp32.
   const float n = KIND == KF16 ? fmaxf(st.m, tile) : (tile > st.m + 64.f ? tile : st.m);
-  const float alpha = texp2(st.m - n);
+  // (quantized tiles rarely move the max: the factor and the rescale only when some row's does)
+  float alpha = 1.f;
+  if (KIND == KF16 || __any(n != st.m)) alpha = texp2(st.m - n);
   st.m = n;
   if (__any(alpha != 1.f)) {
 #pragma unroll
@@ -179,7 +181,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
     const float ksmax = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
     float base = tile > -__builtin_inff() ? tile : st.m;
     base += __builtin_fmaf(qs * ksmax, 0.75f, fabsf(base) * 2.4e-7f);
-    const float bq = texp2(base - st.m) / 255.f;
+    // the reference divides by the level count under fast math; here: times its rounded reciprocal
+    const float bq = texp2(base - st.m) * (1.f / 255.f);
     float c[4];
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi)

@@ -24,6 +24,7 @@ from __future__ import annotations
 import ctypes
 import functools
 import subprocess
+import weakref
 from pathlib import Path
 
 import torch
@@ -105,8 +106,11 @@ def _ptr(t):
 class Module:
     """The op set of the reference's extension module, on the gfx950 kernels."""
 
+    PLAN_CACHE = 256  # decode plans kept for callers of the reference-shaped ``decode`` (one per layer)
+
     def __init__(self, lib: ctypes.CDLL):
         self.lib = lib
+        self._plans = {}
 
     def _call(self, fn, *args):
         if fn(*args) != 0:
@@ -221,8 +225,28 @@ class Module:
         makes the listed KV heads attend exactly over their bf16 prompt.  ``bounds``
         (extension, int32 [B,Hk,splits+1]) replaces the uniform split of ``per`` tiles
         by the given partition of each head's kept tiles."""
-        plan = self.plan_decode(q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail,
-                                vtail, kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot, kxc, vxc, bounds)
+        # A caller of the reference's op (decode.py:76-79) passes the same cache tensors at every step, with
+        # new q / k / v / out: the validated plan is kept per cache (tensor identities, shapes and strides,
+        # prompt, per, scale), so a step costs one launch call, not a re-validation and a prompt tensor.
+        cache_args = (k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat, ktail, vtail, step,
+                      pm, pl, po, xslot, kxc, vxc, bounds)
+        key = (tuple(None if t is None else (t.data_ptr(), _geometry(t)) for t in cache_args),
+               prompt.data_ptr() if isinstance(prompt, torch.Tensor) else int(prompt), int(per), float(scale),
+               _geometry(q), _geometry(kcur), _geometry(vcur), _geometry(out))
+        plan = self._plans.pop(key, None)
+        if plan is not None and any(ref() is None for ref in plan.weak):
+            plan = None  # a tensor of that cache was freed (its address may be reused)
+        if plan is None:
+            plan = self.plan_decode(q, k8c, k4c, ka, ka4, entry, kinfo, count, fmt, slot, v8, v4, vstat, kstat,
+                                    ktail, vtail, kcur, vcur, step, out, pm, pl, po, prompt, per, scale, xslot, kxc,
+                                    vxc, bounds)
+            # the caller owns the cache: the kept plan holds it weakly (and its own prompt tensor strongly),
+            # so dropping a cache frees it
+            plan.weak = tuple(weakref.ref(t) for t in cache_args if t is not None)
+            plan.keep = tuple(t for t in plan.keep if t is not None and not any(t is c for c in cache_args))
+        self._plans[key] = plan  # most recently used last
+        while len(self._plans) > self.PLAN_CACHE:
+            self._plans.pop(next(iter(self._plans)))
         plan.run(q, kcur, vcur, out, phase)
         return out
 

@@ -1,7 +1,7 @@
 """GPU parity at the full shapes of the benchmark configurations.
 
 The bench runs exactly these paths (C1: a batch-32 Prefill into the cache and the cost-balanced split;
-C3: 64 ragged prompts drawn on the device, stored by Prefill.store_only, uniform runs of 32 tiles
+C3: 64 ragged prompts drawn on the device, stored by Prefill.store_only, uniform runs of 28 tiles
 with two waves per workgroup and the golden-ratio scatter; C2: the 4 x 8192-token attention launch with
 an exact head; C4: the 28-layer Qwen2-7B architecture through TriAttention).  Each test holds the GPU
 to the oracle on the same bits: the sequences or rows it checks are copied to the host.
@@ -99,7 +99,7 @@ def test_config1_full_decode(module):
 
 def test_config3_full_ragged_decode(module):
     """C3 (64 ragged prompts, log-uniform in [512, 32768], Hq 32 / Hk 8): the bench's device draw and
-    store_only path, uniform runs of 32 tiles, two waves per workgroup; the shortest, the longest and three
+    store_only path, uniform runs of 28 tiles, two waves per workgroup; the shortest, the longest and three
     middle sequences match the oracle at steps 0 and 1."""
     lengths = S.config3_lengths()
     kinds, bands = S.config3_map()
@@ -122,7 +122,7 @@ def test_config3_full_ragged_decode(module):
             host[b] = (k[0].cpu(), v[0].cpu())
     torch.cuda.synchronize()
     e = cache.layers[0]
-    assert e["bounds"] is None and e["per"] == 32, (e["per"], "C3 runs uniform splits of 32 tiles")
+    assert e["bounds"] is None and e["per"] == 28, (e["per"], "C3 runs uniform splits of 28 tiles")
     assert e["splits"] * hk * batch > 4 * module.device_cus(), "C3 takes the two-wave launch"
     codes = {b: O.prefill_codes(None, bits(host[b][0]), bits(host[b][1]), bands.numpy(), decode_cache=True)
              for b in check}

@@ -387,11 +387,12 @@ class DecodeCache:
         #   C1: 16384 tiles on 1024 slots): every SIMD runs one split, so the kernel lasts as
         #   long as its costliest split, and balanced_partition cuts the heads by cost (C1:
         #   36.9 us vs 39.6 us for runs of 16 tiles).
-        # - Above that (C3: 48.8k tiles), runs of `per` tiles, as the reference splits
-        #   (decode.py:54-55), over one wave of slots with every average head in at least 3
+        # - Above that (C3: 49.1k tiles), runs of `per` tiles, as the reference splits
+        #   (decode.py:54-55), over one wave of slots with every average head in about 3.5
         #   splits: the dispatcher then balances the waves itself, and no partition tried did
-        #   better (C3, two waves per workgroup: 121.5 us at 32 tiles per split, 127-128 at 24 or
-        #   36, 129 at 16, 134 at 64; balanced over 4096-8192 slots 138-168 us).
+        #   better (C3, two waves per workgroup, listed splits, median of 3 rounds on one box:
+        #   102.1 us at 28 tiles per split, 103.2 at 30, 104.4 at 32, 105.2 at 26, 106.7 at 24,
+        #   108.2 at 36; balanced over 4096-8192 slots 138-168 us in an earlier build).
         # - self.per set: always runs of that many tiles.  At most 64 tiles per split.
         kept = sum(g["batch"] * int(g["meta"]["count"].sum()) for g in groups)
         if self.per is None and kept <= BALANCE_TILES * self.wave:
@@ -401,7 +402,7 @@ class DecodeCache:
             bounds = bounds_host.to(device)
         else:
             mean = kept / max(1, rows * st.hk)
-            per = self.per or min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 3))))
+            per = self.per or min(64, max(1, min(-(-kept // self.wave), math.ceil(mean / 3.5))))
             bounds_host = bounds = None
             splits = max(1, -(-st.maxn // per))
         if st.grow_tiles:

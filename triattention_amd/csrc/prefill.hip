@@ -479,7 +479,16 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   __shared__ __align__(16) uint8_t v_lds0[V8_BYTES], v_lds1[V8_BYTES];
   __shared__ __align__(16) float ks_lds0[4], ks_lds1[4];  // the tile's 4 K group scales
   const int rows = (a.t + BN - 1) / BN;
-  const int task = __builtin_amdgcn_readfirstlane(a.order[blockIdx.x]), b = blockIdx.y;
+  // Launch sequence: BandTable's order is KV-head-major (prefill.py:24-25), so the workgroups running at
+  // any one time would all belong to one KV head.  Workgroup j takes entry (kv * rows + qd) * g + r of it
+  // for j = (qd * hk + kv) * g + r: the same entries, longest query tiles still first, but the KV heads
+  // interleaved, so exact heads (MFMA-heavy) run beside quantized ones (VALU-heavy) on the same CUs.
+  int j = blockIdx.x;
+  if ((int)gridDim.x == a.hq * rows) {
+    const int g0 = a.hq / a.hk, r = j % g0, t = j / g0;
+    j = ((t % a.hk) * rows + t / a.hk) * g0 + r;
+  }
+  const int task = __builtin_amdgcn_readfirstlane(a.order[j]), b = blockIdx.y;
   const int qh = task / rows, qb = task % rows, g = a.hq / a.hk, kh = qh / g;
   if (a.exact != nullptr && a.exact[qh] > 0) {
     prefill_exact(a, b, qh, qb, k_lds0, k_lds1, v_lds0, v_lds1);

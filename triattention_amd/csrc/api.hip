@@ -318,7 +318,12 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
     if (d.tasks && n_tasks > all) return fail("decode: the task table lists more splits than exist");
     const int64_t items = d.tasks ? n_tasks : all;
     const bool pinned = bounds == nullptr && items % 8 == 0 && splits % 2 == 0;
-    if (!pinned) {
+    if (d.tasks) {
+      // a task table lists its splits in the order to run them (costliest first): workgroup lin takes
+      // row lin, and the XCDs receive the rows round-robin
+      d.scatter = 1;
+      d.launched = (int)items;
+    } else if (!pinned) {
       const int primes[3] = {1000003, 1000033, 1000037};
       d.scatter = primes[0];
       for (int p : primes)

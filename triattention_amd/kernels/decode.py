@@ -482,10 +482,13 @@ class DecodeCache:
                 e["tasks"] = self.module.decode_tasks(e["ka"], e["ka4"], e["entry"], e["kinfo"], e["count"], e["fmt"],
                                                       e["slot"], e["per"], e["bounds"], items)
                 if e["grow_splits"]:
-                    # task row of each head's first growth split (they are listed, in order)
+                    # task row of each head's first growth split (a head's growth splits are empty at the
+                    # store, so they are listed last, consecutively, in item order)
                     first = np.arange(e["batch"] * e["store"].hk, dtype=np.int64) * e["splits"] + \
                         (e["splits"] - e["grow_splits"])
-                    rows = np.searchsorted(items_host, first).astype(np.int32)
+                    where = np.full(int(items_host.max()) + 1, -1, np.int64)
+                    where[items_host] = np.arange(items_host.size)
+                    rows = where[first].astype(np.int32)
                     e["store"].arrays["grow"][:e["batch"], :, 3].copy_(
                         torch.from_numpy(rows.reshape(e["batch"], e["store"].hk)))
             e[key] = self.module.plan_decode(
@@ -586,17 +589,33 @@ class DecodeCache:
 
     @staticmethod
     def _task_items(e):
-        """Work items ((sequence * Hk + head) * splits + split) of the splits that hold kept tiles, from
-        the host metadata: a split of the balanced partition is empty when its bounds coincide, one of
-        the uniform runs when it starts past its head's count."""
-        counts = np.concatenate([np.repeat(g["meta"]["count"].numpy()[None], g["batch"], 0) for g in e["groups"]])
+        """Work items ((sequence * Hk + head) * splits + split) of the splits that hold kept tiles (and every
+        growth split), from the host metadata: a split of the balanced partition is empty when its bounds
+        coincide, one of the uniform runs when it starts past its head's count.  Ordered costliest first
+        (the split kernel's measured time per tile kind, entry_costs; ties by item): the kernel deals the
+        listed splits to the XCDs round-robin in this order, so the long splits start first and every XCD
+        gets its share of each cost."""
+        groups = e["groups"]
+        counts = np.concatenate([np.repeat(g["meta"]["count"].numpy()[None], g["batch"], 0) for g in groups])
+        per_group = [entry_costs(g["meta"]) for g in groups]
+        width = max(c.shape[1] for c in per_group)
+        costs = np.concatenate([np.repeat(np.pad(c, ((0, 0), (0, width - c.shape[1])))[None], g["batch"], 0)
+                                for c, g in zip(per_group, groups)])
+        cum = np.concatenate([np.zeros(costs.shape[:2] + (1,)), costs.cumsum(2)], 2)
         if e["bounds_host"] is not None:
-            b = e["bounds_host"]
-            nonempty = b[:, :, 1:] > b[:, :, :-1]
+            b = np.minimum(e["bounds_host"], counts[:, :, None])
+            nonempty = e["bounds_host"][:, :, 1:] > e["bounds_host"][:, :, :-1]
         else:
-            nonempty = np.arange(e["splits"])[None, None, :] * e["per"] < counts[:, :, None]
+            first = np.arange(e["splits"])[None, None, :] * e["per"]
+            nonempty = first < counts[:, :, None]
+            b = np.minimum(np.concatenate([first, first[:, :, -1:] + e["per"]], 2), counts[:, :, None])
+        b = np.minimum(b, width)
+        split_cost = np.take_along_axis(cum, b[:, :, 1:], 2) - np.take_along_axis(cum, b[:, :, :-1], 2)
         items = np.flatnonzero(nonempty.reshape(-1)).astype(np.int32)
-        return items if items.size else np.zeros(1, np.int32)
+        if not items.size:
+            return np.zeros(1, np.int32)
+        order = np.lexsort((items, -split_cost.reshape(-1)[items]))
+        return items[order]
 
     def split_of(self, layer, b):
         """The split argument of the oracle's decode for sequence b of the layer: its bounds

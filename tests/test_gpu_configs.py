@@ -123,7 +123,9 @@ def test_config3_full_ragged_decode(module):
     torch.cuda.synchronize()
     e = cache.layers[0]
     assert e["bounds"] is None and e["per"] == 28, (e["per"], "C3 runs uniform splits of 28 tiles")
-    assert e["splits"] * hk * batch > 4 * module.device_cus(), "C3 takes the two-wave launch"
+    listed = DecodeCache._task_items(e).size
+    assert 4 * module.device_cus() < listed <= 8 * module.device_cus(), \
+        "C3: more splits than one resident wave per SIMD, in one-wave workgroups"
     codes = {b: O.prefill_codes(None, bits(host[b][0]), bits(host[b][1]), bands.numpy(), decode_cache=True)
              for b in check}
     ktail = np.zeros((batch, hk, 256, 128), np.uint16)

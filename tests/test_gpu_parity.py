@@ -138,7 +138,7 @@ def test_decode_uniform_split(module, per):
 
 @pytest.mark.parametrize("hq,hk,per", [(24, 8, 1), (24, 8, 2), (24, 8, 3), (32, 8, 2), (16, 2, 3), (8, 8, 2)])
 def test_decode_two_waves_per_workgroup(module, hq, hk, per):
-    """A grid larger than one wave of resident workgroups (4 per CU) runs two waves per workgroup,
+    """A grid larger than the resident one-wave workgroups (8 per CU) runs two waves per workgroup,
     taking a split's tiles alternately: per 1 leaves the second wave without tiles, per 3 gives the
     waves 2 and 1.  Groups 3 and 1 (DUP layout, packed 4-bit Q in registers), 4 (DUP, packed Q read
     from LDS) and 8 (two row blocks); mixed INT8/INT4/skipped tiles."""
@@ -147,7 +147,7 @@ def test_decode_two_waves_per_workgroup(module, hq, hk, per):
     bands = torch.tensor([kinds[h % 4] for h in range(hk) for _ in range(g)], dtype=torch.int32)
     prompt = 600
     splits = -(-10 // per)
-    batch = (4 * module.device_cus()) // (splits * hk) + 1
+    batch = (9 * module.device_cus()) // (splits * hk) + 1
     _decode_case(module, prompt, bands, batch=batch, steps=2, max_tail=4, seed=5300 + 10 * g + per, hq=hq, hk=hk,
                  per=per)
 

@@ -382,14 +382,14 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
     const dim3 grid(d.launched);
     const int g = hq / hk;
     if (xslot == nullptr) {
-      // Two waves per workgroup (alternate tiles of a split) when the grid exceeds one
-      // wave of resident workgroups (4 per CU): the dispatcher queues workgroups anyway,
-      // and two waves per SIMD interleave their dependency chains (C3: 138 -> 133 us).
-      // A grid of at most one resident wave keeps one wave per SIMD, which streams
-      // better (C1: 37.4 us, against 39.3 us with two waves per workgroup).
+      // One wave per workgroup while the grid fits the resident waves (two per SIMD, 8
+      // workgroups per CU): each wave streams a split of its own (C1, 1,024 splits: 37.4 us,
+      // against 39.3 us with two waves per workgroup; C3, 1,785 splits: 99.0-100.0 us against
+      // 101.5-102.7 us, same box).  Larger grids run two waves per workgroup (alternate tiles of
+      // a split), which interleave their dependency chains while the dispatcher queues the rest.
       int cus = 0;
       if (device_cus(&cus) != 0) return 1;
-      if ((int64_t)d.items > 4 * (int64_t)cus) launch_decode<2>(g, grid, d, s, ev_start, ev_stop);
+      if ((int64_t)d.items > 8 * (int64_t)cus) launch_decode<2>(g, grid, d, s, ev_start, ev_stop);
       else launch_decode<1>(g, grid, d, s, ev_start, ev_stop);
     } else {
       // groups of up to 4 q-heads use the DUP lane layout (both wave halves on rows 0..3)

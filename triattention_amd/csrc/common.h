@@ -87,12 +87,14 @@ __device__ __forceinline__ float texp2(float x) {
   return __uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
 }
 
-// exp2 of the per-score probabilities (P levels, fp16 P): the hardware
+// exp2 of the prefill's per-score probabilities (P levels, fp16 P): the hardware
 // v_exp_f32 (about 1 ulp), as the reference takes its per-score exp2 from the
 // hardware approximation (ex2.approx.ftz.f32).  A level can differ from the
 // one texp2 gives only where e * levels lies within a few ulp of a rounding
-// boundary (measured: 2.6e-4 of C0's outputs move, by at most 1.5e-5).
-// texp2's polynomial costs ~10 VALU per score, v_exp_f32 one transcendental.
+// boundary (measured: 2.6e-4 of C0's outputs move, by at most 1.5e-5; the
+// prefill's PV levels are 8-bit).  texp2's polynomial costs ~10 VALU per score,
+// v_exp_f32 one transcendental.  (Decode, memory-bound and with 15-level INT4
+// V, takes texp2 for its levels.)
 __device__ __forceinline__ float pexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Sign pattern of the 128-channel rotation (prefill_sm80.cu:95): bit c & 31 of
@@ -223,6 +225,30 @@ __device__ __forceinline__ float rows_max_half(float v, bool upper) {
   v = fmaxf(v, dpp_rows<0x142, 0xA>(v));
   const float lo = readlane_f(v, 31), hi = readlane_f(v, 63);
   return upper ? hi : lo;
+}
+
+// Lanes L and L ^ 32 combined: v_permlane32_swap hands each 32-lane half the other half's values
+// (a VALU operation, no LDS round trip like __shfl_xor's permute); both halves combine the same two
+// operands in the same order, so they hold identical results.
+__device__ __forceinline__ void xor32_pair(uint32_t v, uint32_t& lo, uint32_t& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  lo = r[0];  // the value of lane L % 32
+  hi = r[1];  // the value of lane L % 32 + 32
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  uint32_t lo, hi;
+  xor32_pair(__float_as_uint(v), lo, hi);
+  return fmaxf(__uint_as_float(lo), __uint_as_float(hi));
+}
+__device__ __forceinline__ float xor32_add(float v) {
+  uint32_t lo, hi;
+  xor32_pair(__float_as_uint(v), lo, hi);
+  return __uint_as_float(lo) + __uint_as_float(hi);
+}
+__device__ __forceinline__ uint32_t xor32_add(uint32_t v) {
+  uint32_t lo, hi;
+  xor32_pair(v, lo, hi);
+  return lo + hi;
 }
 
 // byte 1 of each of four words, packed (P levels out of the 49152.5 magic).

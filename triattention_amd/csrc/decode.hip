@@ -728,7 +728,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
         const float c = is4 ? -base[r] : (-slope[r][t] * MAGIC) - base[r];
         const float arg = ok[r][t] ? __builtin_fmaf(slope[r][t], x, c) : -__builtin_inff();
         const uint32_t dith = 0x47400000u | (ok[r][t] ? (uint32_t)d & 0xffu : 0u);
-        const uint32_t y = __float_as_uint(__builtin_fmaf(pexp2(arg), levels, __uint_as_float(dith)));
+        // texp2, not the hardware exp2: with 15 levels (INT4 V) a level that a 1-ulp difference
+        // moves across a rounding boundary moves the output by up to ~4e-2 (measured), and this
+        // memory-bound kernel has the VALU time for the exact exp2
+        const uint32_t y = __float_as_uint(__builtin_fmaf(texp2(arg), levels, __uint_as_float(dith)));
         const uint32_t p = (y >> 8) & 0xffu;
         psum += p;
         pls[qrow(r)][kb * 32 + lq] = (uint8_t)p;

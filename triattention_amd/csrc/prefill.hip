@@ -51,8 +51,6 @@ struct PrefillState {
   float m, den;    // running max (log2 units) and denominator, equal in lanes L and L^32
 };
 
-__device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
-
 template <int KIND>
 __device__ __forceinline__ v4i k_frag(const uint8_t* __restrict__ k_lds, int F, int L) {
   if constexpr (KIND == KQ4) {
@@ -163,8 +161,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
         p[kb][r >> 3][r & 7] = h;
         psum += (float)h;
       }
-    psum += __shfl_xor(psum, 32, 64);
-    st.den += psum;
+    st.den += xor32_add(psum);
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
@@ -204,8 +201,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
         rs = __builtin_amdgcn_udot4(w, 0x01010101u, rs, false);
         pw[kb][qd] = w ^ 0x7f7f7f7fu;  // 127 - P as s8
       }
-    rs += __shfl_xor(rs, 32, 64);
-    st.den = __builtin_fmaf((float)rs, bq, st.den * alpha);
+    st.den = __builtin_fmaf((float)xor32_add(rs), bq, st.den * alpha);
     const v4i neg127 = {(int)0x81818181u, (int)0x81818181u, (int)0x81818181u, (int)0x81818181u};
     const v4i b0 = {(int)pw[0][0], (int)pw[0][1], (int)pw[0][2], (int)pw[0][3]};
     const v4i b1 = {(int)pw[1][0], (int)pw[1][1], (int)pw[1][2], (int)pw[1][3]};
@@ -293,7 +289,7 @@ __device__ __forceinline__ void exact_step(const PrefillArgs& a, int col, int kb
   float mx = s[0];
 #pragma unroll
   for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = xor32_max(mx);
   const float tile = mx * a.sm_log2;
   // Reference max for P = 2^(x - m): acc and den scale alike, so m only needs
   // to keep P in range; it moves when a step exceeds it by more than 16.
@@ -319,8 +315,7 @@ __device__ __forceinline__ void exact_step(const PrefillArgs& a, int col, int kb
     plo[r >> 3][r & 7] = (__bf16)(p - (float)h);
     psum += p;
   }
-  psum += __shfl_xor(psum, 32, 64);
-  den += psum;
+  den += xor32_add(psum);
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb)
 #pragma unroll

@@ -390,6 +390,12 @@ def prefill_only(args):
         if name == "C0":
             cfg["kinds"] = []
         out[name] = prefill_case(module, dev, stream, name, cfg, reps, Prefill, from_bands, full_call=args.only == "prefill")
+        if name == "C2" and args.c2_kinds:
+            # the C2 inputs with every KV head of one kind (the per-kind cost of the attention tile)
+            for kind in args.c2_kinds.split(","):
+                v = dict(cfg, kinds=[kind] * 4, bands=S.kv_head_bands([kind] * 4, 7))
+                out[f"C2 all {kind}"] = prefill_case(module, dev, stream, f"C2 all {kind}", v, reps, Prefill,
+                                                     from_bands, full_call=False)
     print(json.dumps({"prefill": out}))
 
 
@@ -468,6 +474,8 @@ def main():
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--layers", type=int, default=28, help="C1 layers (own caches, one decode op each per token)")
+    ap.add_argument("--c2-kinds", default="", help="with --only c2: also time the C2 inputs with every KV head of "
+                                                   "each listed kind (i8, i4, bf16; comma-separated)")
     ap.add_argument("--no-c4", action="store_true", help="leave out the C4 generation from the default run")
     ap.add_argument("--no-calibrate", action="store_true", help="leave out the calibration sweep from the default run")
     ap.add_argument("--only", choices=("prefill", "c2"),
@@ -551,7 +559,7 @@ def main():
     def step(i, ev=None):
         # one decode op of layer i % layers: the split-KV kernel and the merge kernel; the step
         # counter advances once per token, after the last layer
-        qd, kd, vd = toks[i]
+        qd, kd, vd = toks[i % total_steps]
         plan = plans[i % layers]
         if ev is None:
             plan.run(qd, kd, vd, out)

@@ -74,6 +74,8 @@ def decode_record_bytes(cache_entry):
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_kernel_C1_traffic.md"
 COPY_PROBE_BYTES = 256 << 20
+# record bytes (K/V records and K group scales) one C1 decode launch reads: 16,384 kept tiles
+C1_RECORD_BYTES = 170_655_744
 
 
 def measured_traffic():
@@ -108,6 +110,65 @@ def copy_probe():
         torch.neg(x, out=y)
     torch.cuda.synchronize()
     print(f"copy probe: 5 x torch.neg over {COPY_PROBE_BYTES} B in, {COPY_PROBE_BYTES} B out", flush=True)
+
+
+# launch shapes of the streaming-read probe (waves, waves per workgroup, records in flight per wave)
+STREAM_SHAPES = ((1024, 1, 1), (1024, 1, 2), (1024, 1, 3), (2048, 1, 2), (2048, 2, 2), (4096, 4, 1), (4096, 4, 2),
+                 (8192, 4, 2))
+STREAM_SHAPES_DEFAULT = ((1024, 1, 3), (2048, 2, 2), (4096, 4, 2), (8192, 4, 2))
+
+
+def stream_ceiling(module, dev, nbytes, layers, shapes, reps=5, verbose=False):
+    """The device's streaming-read ceiling for a launch that reads ``nbytes``: tri_stream_read (no
+    compute, 16-byte loads per lane, contiguous 8 KiB records per wave) over ``layers`` buffers of
+    that size in turn, so that, as in the decode bench, each launch reads from HBM rather than the
+    256 MB Infinity Cache.  Returns the best (us per launch, GB/s, shape) over ``shapes``."""
+    import torch
+    records = nbytes // 8192
+    bufs = [torch.empty(records * 8192, dtype=torch.uint8, device=dev) for _ in range(layers)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    best = None
+    for shape in shapes:
+        for b in bufs:
+            module.stream_read(b, *shape, sink)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for b in bufs:
+                module.stream_read(b, *shape, sink)
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / layers)
+        us = min(times)
+        gbs = records * 8192 / (us * 1e-6) / 1e9
+        if verbose:
+            print(f"stream read: {shape[0]:5d} waves, {shape[1]} per workgroup, {shape[2]} in flight: "
+                  f"{us:7.2f} us per launch, {gbs:7.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)", flush=True)
+        if best is None or us < best[0]:
+            best = (us, gbs, shape)
+    del bufs
+    return best
+
+
+def read_ceiling(args):
+    """--read-ceiling: the streaming-read probe over every shape, at the C1 decode launch's bytes."""
+    import torch
+    from triattention_amd.kernels.extension import load_extension
+    module = load_extension()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    mat = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 1.5:
+        mat = (mat @ mat).clamp_(-1.0, 1.0)
+        torch.cuda.synchronize()
+    del mat
+    us, gbs, shape = stream_ceiling(module, dev, C1_RECORD_BYTES, args.layers, STREAM_SHAPES, verbose=True)
+    print(json.dumps({"stream_ceiling": {"bytes": C1_RECORD_BYTES, "buffers": args.layers, "us": round(us, 2),
+                                         "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                         "shape": list(shape)}}), flush=True)
 
 
 def graph_steps(run_token, tokens, stream):
@@ -472,6 +533,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="time the streaming-read probe over every launch shape at the C1 launch's bytes instead")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--layers", type=int, default=28, help="C1 layers (own caches, one decode op each per token)")
     ap.add_argument("--c2-kinds", default="", help="with --only c2: also time the C2 inputs with every KV head of "
@@ -486,6 +549,9 @@ def main():
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
+        return
+    if args.read_ceiling:
+        read_ceiling(args)
         return
     if args.c4 and args.gpus == 1:
         c4_e2e(args)
@@ -620,6 +686,10 @@ def main():
     achieved = rec_bytes / (dec_ms * 1e-3) / 1e9
     log(f"decode step {ms_per_step * 1e3:.1f} us from a HIP graph, {eager_ms_per_step * 1e3:.1f} us eager "
         f"(split-KV kernel {dec_ms * 1e3:.1f} us)")
+    # the same bytes read with no compute, in the probe's best launch shape: what this device streams
+    ceil_us, ceil_gbs, ceil_shape = stream_ceiling(module, dev, rec_bytes, layers, STREAM_SHAPES_DEFAULT)
+    log(f"streaming-read ceiling for {rec_bytes} B: {ceil_us:.1f} us ({ceil_gbs:.0f} GB/s); the split-KV kernel "
+        f"runs at {achieved / ceil_gbs:.3f} of it")
 
     result = {
         "metric": "prefill int8 TOPS (% MFMA peak); decode KV GB/s (% HBM peak); tokens/s",
@@ -648,6 +718,12 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(), "algorithmic_bytes": rec_bytes,
                      "avg_us": round(dec_ms * 1e3, 2), "working_set_bytes": layers * rec_bytes},
+        "stream_ceiling": {"achieved": round(ceil_gbs, 1), "us": round(ceil_us, 2),
+                           "frac": round(ceil_gbs / HBM_PEAK_GBS, 4), "kernel_frac_of_ceiling":
+                           round(achieved / ceil_gbs, 4), "shape": list(ceil_shape),
+                           "note": "the split-KV kernel's record bytes read by a no-compute probe "
+                                   "(tri_stream_read: waves, waves per workgroup, records in flight), "
+                                   "best of the listed shapes, from the same rotating buffers"},
     }
 
     # ------------------------------------------------------------- CPU baseline

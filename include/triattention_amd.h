@@ -260,6 +260,14 @@ int tri_decode_occupancy(int* blocks);
 /* Compute units of the current device (used to size decode splits). */
 int tri_device_cus(int* cus);
 
+/* Measurement aid, no counterpart in the reference: reads `records` records of 8192 bytes from
+ * `base` with no compute (wave i takes a contiguous run of ceil(records / waves) records, `depth`
+ * of them in flight, 16-byte loads per lane), the device's streaming-read ceiling against which
+ * the decode kernel's record stream is measured.  waves_per_group 1, 2 or 4; depth 1..3; sink: one
+ * int32 of device memory (never written in practice). */
+int tri_stream_read(const void* base, int64_t records, int waves, int waves_per_group, int depth, int32_t* sink,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

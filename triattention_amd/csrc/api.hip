@@ -16,6 +16,7 @@
 #include "cache.hip"
 #include "decode.hip"
 #include "prefill.hip"
+#include "probe.hip"
 #include "quantize.hip"
 #include "tail.hip"
 
@@ -698,6 +699,25 @@ int tri_device_cus(int* cus) {
   g_error.clear();
   if (!cus) return fail("device_cus: null output");
   return device_cus(cus);
+}
+
+int tri_stream_read(const void* base, int64_t records, int waves, int waves_per_group, int depth, int32_t* sink,
+                    void* stream) {
+  g_error.clear();
+  if (!base || !sink) return fail("stream_read: null pointer");
+  if (records <= 0 || waves <= 0) return fail("stream_read: records and waves must be positive");
+  if (waves_per_group != 1 && waves_per_group != 2 && waves_per_group != 4)
+    return fail("stream_read: waves_per_group must be 1, 2 or 4 (got %d)", waves_per_group);
+  if (depth < 1 || depth > 3) return fail("stream_read: depth must be 1, 2 or 3 (got %d)", depth);
+  const int64_t per = (records + waves - 1) / waves;
+  if (per > INT32_MAX) return fail("stream_read: too many records per wave");
+  const dim3 grid((waves + waves_per_group - 1) / waves_per_group), block(64 * waves_per_group);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* p = static_cast<const uint8_t*>(base);
+  if (depth == 1) tri::stream_read_kernel<1><<<grid, block, 0, s>>>(p, records, (int)per, sink);
+  else if (depth == 2) tri::stream_read_kernel<2><<<grid, block, 0, s>>>(p, records, (int)per, sink);
+  else tri::stream_read_kernel<3><<<grid, block, 0, s>>>(p, records, (int)per, sink);
+  return check_launch("stream_read");
 }
 
 }  // extern "C"

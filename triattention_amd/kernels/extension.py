@@ -38,7 +38,8 @@ K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
            "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_noalloc",
-           "tri_decode_tasks", "tri_cache_store", "tri_tail_spill", "tri_decode_occupancy", "tri_device_cus")
+           "tri_decode_tasks", "tri_cache_store", "tri_tail_spill", "tri_decode_occupancy", "tri_device_cus",
+           "tri_stream_read")
 KX_BYTES = 16384
 TASK_WORDS = 512  # int32 words of the decode task table per (sequence, KV head, split)
 
@@ -79,6 +80,7 @@ def load_library() -> ctypes.CDLL:
                                    P, I64, P, I64, P, I64, P, P, I64, P, I, P]
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
+    lib.tri_stream_read.argtypes = [P, I64, I, I, I, P, P]
     for name in EXPORTS:
         if name != "tri_last_error":
             getattr(lib, name).restype = ctypes.c_int
@@ -465,6 +467,13 @@ class Module:
         n = ctypes.c_int(0)
         self._call(self.lib.tri_device_cus, ctypes.byref(n))
         return int(n.value)
+
+    def stream_read(self, buf, waves: int, waves_per_group: int, depth: int, sink) -> None:
+        """Measurement aid (no reference counterpart): read every 8 KiB record of the device buffer
+        ``buf`` with no compute, ``depth`` records in flight per wave (tri_stream_read)."""
+        records = buf.numel() * buf.element_size() // 8192
+        self._call(self.lib.tri_stream_read, buf.data_ptr(), records, waves, waves_per_group, depth,
+                   sink.data_ptr(), self._stream(buf.device))
 
 
 def _geometry(t):

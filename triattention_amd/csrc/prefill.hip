@@ -336,8 +336,10 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
   const uint16_t* qp = a.qr + b * a.qsb + qh * a.qsh + (int64_t)(row_ok ? qrow : 0) * a.qst;
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    const uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * half) : z;
+    // (a conditional load, not a select between the row and a zero: a select of the two addresses
+    // would put the zero in scratch memory and make the load a flat one)
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (row_ok) w = *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * half);
     qf[ks] = __builtin_bit_cast(v8bf, w);
   }
   const int64_t rec0 = ((int64_t)b * a.nx + (a.exact[qh] - 1)) * tiles;
@@ -504,8 +506,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   v4i qf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    v4i z = {0, 0, 0, 0};
-    qf[ks] = row_ok ? *reinterpret_cast<const v4i*>(a.q8 + qrow_idx * D + ks * 32 + 16 * half) : z;
+    qf[ks] = v4i{0, 0, 0, 0};
+    if (row_ok) qf[ks] = *reinterpret_cast<const v4i*>(a.q8 + qrow_idx * D + ks * 32 + 16 * half);
   }
   const float qs8 = row_ok ? a.qa[qrow_idx] * a.sm_log2 : 1.17549435e-38f;
   PrefillState st;

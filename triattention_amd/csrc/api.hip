@@ -105,7 +105,7 @@ int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, cons
   tri::quantize_q_kernel<<<dim3((t + 31) / 32, hq, batch), 256, 0, s>>>(
       static_cast<const uint16_t*>(q), q_sb, q_sh, q_st, hq, t, static_cast<int8_t*>(q8), qa,
       static_cast<uint8_t*>(q4), qa4);
-  tri::partial_kernel<<<dim3(tri::STAT_BLOCKS, hk, batch), tri::D, 0, s>>>(static_cast<const uint16_t*>(k), k_sb,
+  tri::partial_kernel<<<dim3(tri::STAT_BLOCKS, hk, batch), tri::D / 2, 0, s>>>(static_cast<const uint16_t*>(k), k_sb,
                                                                           k_sh, k_st, hk, t, partial);
   tri::finalize_kernel<<<dim3(hk, batch), tri::D, 0, s>>>(partial, kstat, hk, t, 0);
   tri::quantize_k_kernel<<<dim3(tiles, hk, batch), 256, 0, s>>>(static_cast<const uint16_t*>(k), k_sb, k_sh, k_st,
@@ -126,7 +126,7 @@ int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batc
   const bool identity = v8p == nullptr && v4p == nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!identity)
-    tri::partial_kernel<<<dim3(tri::STAT_BLOCKS, hk, batch), tri::D, 0, s>>>(static_cast<const uint16_t*>(v), v_sb,
+    tri::partial_kernel<<<dim3(tri::STAT_BLOCKS, hk, batch), tri::D / 2, 0, s>>>(static_cast<const uint16_t*>(v), v_sb,
                                                                             v_sh, v_st, hk, t, partial);
   tri::finalize_kernel<<<dim3(hk, batch), tri::D, 0, s>>>(partial, vstat, hk, t, identity ? 1 : 0);
   tri::pack_v_kernel<<<dim3(tiles, hk, batch), 256, 0, s>>>(static_cast<const uint16_t*>(v), v_sb, v_sh, v_st, vstat,

@@ -57,29 +57,38 @@ __global__ __launch_bounds__(256) void quantize_q_kernel(const uint16_t* __restr
 
 // Per channel: sequential sum/max/min over tokens t = blk, blk+64, ...
 // common_device.cuh:32-42 (partial_kernel).  partial [B][H][64][3][128].
-__global__ __launch_bounds__(128) void partial_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t sh,
-                                                      int64_t st, int h, int t, float* __restrict__ partial) {
-  const int blk = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, c = threadIdx.x;
+// Lane i takes channels 2i and 2i + 1 (one 4-byte load per token; rows are 8-byte aligned) and
+// issues the loads of STAT_DEPTH tokens before it adds them, in token order, so each channel's
+// sum is formed in the reference's order while 32 loads per lane are in flight (C2's K: 14 us
+// against 22 us with 2-byte loads four deep; 64 deep, or 8 channels per lane with two rows per
+// load, measured no faster).
+constexpr int STAT_DEPTH = 32;
+__global__ __launch_bounds__(64) void partial_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t sh,
+                                                     int64_t st, int h, int t, float* __restrict__ partial) {
+  const int blk = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, c = 2 * threadIdx.x;
   const uint16_t* base = x + b * sb + hd * sh + c;
-  float sum = 0.f, hi = -3.402823466e38f, lo = 3.402823466e38f;
-  int tk = blk;
-  for (; tk + 3 * STAT_BLOCKS < t; tk += 4 * STAT_BLOCKS) {
-    const float v0 = bf16f(base[(int64_t)tk * st]), v1 = bf16f(base[(int64_t)(tk + STAT_BLOCKS) * st]);
-    const float v2 = bf16f(base[(int64_t)(tk + 2 * STAT_BLOCKS) * st]), v3 = bf16f(base[(int64_t)(tk + 3 * STAT_BLOCKS) * st]);
-    sum += v0; sum += v1; sum += v2; sum += v3;
-    hi = fmaxf(fmaxf(hi, v0), fmaxf(fmaxf(v1, v2), v3));
-    lo = fminf(fminf(lo, v0), fminf(fminf(v1, v2), v3));
-  }
-  for (; tk < t; tk += STAT_BLOCKS) {
-    const float v = bf16f(base[(int64_t)tk * st]);
-    sum += v;
-    hi = fmaxf(hi, v);
-    lo = fminf(lo, v);
+  float sum0 = 0.f, sum1 = 0.f, hi0 = -3.402823466e38f, hi1 = hi0, lo0 = 3.402823466e38f, lo1 = lo0;
+  for (int tk = blk; tk < t; tk += STAT_DEPTH * STAT_BLOCKS) {
+    uint32_t w[STAT_DEPTH];
+#pragma unroll
+    for (int j = 0; j < STAT_DEPTH; ++j)
+      if (tk + j * STAT_BLOCKS < t) w[j] = *reinterpret_cast<const uint32_t*>(base + (int64_t)(tk + j * STAT_BLOCKS) * st);
+#pragma unroll
+    for (int j = 0; j < STAT_DEPTH; ++j)
+      if (tk + j * STAT_BLOCKS < t) {
+        const float v0 = bf16f((uint16_t)(w[j] & 0xffffu)), v1 = bf16f((uint16_t)(w[j] >> 16));
+        sum0 += v0;
+        sum1 += v1;
+        hi0 = fmaxf(hi0, v0);
+        hi1 = fmaxf(hi1, v1);
+        lo0 = fminf(lo0, v0);
+        lo1 = fminf(lo1, v1);
+      }
   }
   float* o = partial + ((((int64_t)b * h + hd) * STAT_BLOCKS + blk) * 3) * D + c;
-  o[0] = sum;
-  o[D] = hi;
-  o[2 * D] = lo;
+  *reinterpret_cast<float2*>(o) = make_float2(sum0, sum1);
+  *reinterpret_cast<float2*>(o + D) = make_float2(hi0, hi1);
+  *reinterpret_cast<float2*>(o + 2 * D) = make_float2(lo0, lo1);
 }
 
 // mean = (sum of block sums in block order) / T, scale = range/127 (1 if 0),
@@ -92,6 +101,8 @@ __global__ __launch_bounds__(128) void finalize_kernel(const float* __restrict__
   if (!identity) {
     const float* in = partial + hb * STAT_BLOCKS * 3 * D + c;
     float sum = 0.f, hi = -3.402823466e38f, lo = 3.402823466e38f;
+    // (unrolled: the 192 loads issue together, and the sum still runs in block order)
+#pragma unroll
     for (int blk = 0; blk < STAT_BLOCKS; ++blk) {
       sum += in[blk * 3 * D];
       hi = fmaxf(hi, in[blk * 3 * D + D]);

@@ -41,6 +41,19 @@ def test_codes_and_output_small(module, t):
     assert_close(out.numpy(), ref, what=f"prefill t={t}")
 
 
+def test_statistics_past_one_load_batch(module):
+    """K/V statistics of chains longer than one batch of token loads, with a remainder: T = 2500 gives
+    the 64 block chains 39 or 40 tokens each (one full batch of 32, then the rest), bit-exact codes and
+    statistics against the oracle, outputs within the parity bar."""
+    print("\n[parity] prefill t=2500 (statistics over two load batches)", flush=True)
+    q, k, v = small(2600, 1, 4, 2, 2500)
+    bands = torch.tensor(MIXED[:2] + MIXED[3:5], dtype=torch.int32)
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5)
+    ref, codes = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    compare_codes(ops, codes[0], 0, 1, 4, 2, 2500)
+    assert_close(out.numpy(), ref, what="prefill t=2500")
+
+
 def test_zero_query_and_key_rows(module):
     """All-zero query rows (scale 0, so every score of the row is 0 and masked keys give 0 * -inf) and
     all-zero key rows: outputs finite and within the parity bar, codes bit-exact."""

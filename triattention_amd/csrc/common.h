@@ -235,10 +235,23 @@ __device__ __forceinline__ void xor32_pair(uint32_t v, uint32_t& lo, uint32_t& h
   lo = r[0];  // the value of lane L % 32
   hi = r[1];  // the value of lane L % 32 + 32
 }
+// Maxima of values that arithmetic produced (never a signaling NaN): the hardware max as is.  fmaxf
+// would first canonicalize each operand that the compiler cannot trace to arithmetic (one more VALU
+// operation per operand after a lane exchange or an LDS read); the results are the same.
+__device__ __forceinline__ float max_arith(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3_arith(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 __device__ __forceinline__ float xor32_max(float v) {
   uint32_t lo, hi;
   xor32_pair(__float_as_uint(v), lo, hi);
-  return fmaxf(__uint_as_float(lo), __uint_as_float(hi));
+  return max_arith(__uint_as_float(lo), __uint_as_float(hi));
 }
 __device__ __forceinline__ float xor32_add(float v) {
   uint32_t lo, hi;

@@ -118,7 +118,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
         mx = max(max(mx, s[kb][g0 + 3]), s[kb][g0 + 4]);
         mx = max(max(mx, s[kb][g0 + 5]), s[kb][g0 + 6]);
         mx = max(mx, s[kb][g0 + 7]);
-        const float d = KIND == KQ4 ? (float)mx : (float)(mx - (int)MAGIC_BITS);
+        // (|dot| < 2^22: the magic float minus 1.5 * 2^23 is the dot product exactly)
+        const float d = KIND == KQ4 ? (float)mx : __int_as_float(mx) - MAGIC;
         tile = fmaxf(tile, slope[kb * 2 + hg] * d);
       }
     }
@@ -175,7 +176,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
         }
   } else {
     // ---- quantized P (u8) x INT8 V' (prefill_sm80.cu:384-449)
-    const float ksmax = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
+    const float ksmax = max_arith(max3_arith(ks[0], ks[1], ks[2]), ks[3]);
     float base = tile > -__builtin_inff() ? tile : st.m;
     base += __builtin_fmaf(qs * ksmax, 0.75f, fabsf(base) * 2.4e-7f);
     // the reference divides by the level count under fast math; here: times its rounded reciprocal
@@ -185,7 +186,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
     for (int gi = 0; gi < 4; ++gi)
       c[gi] = KIND == KI8 ? __builtin_fmaf(-slope[gi], MAGIC, -base) : -base;
     uint32_t pw[2][4];
-    uint32_t rs = 0;
+    int rsn = 0;  // sum of this lane's 32 bytes 127 - P (signed dot product of the s8 operand words)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -197,11 +198,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
           const float e = pexp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
           y[i] = __float_as_uint(__builtin_fmaf(e, 255.f, PMAGIC_HALF));
         }
-        const uint32_t w = pack_byte1(y[0], y[1], y[2], y[3]);
-        rs = __builtin_amdgcn_udot4(w, 0x01010101u, rs, false);
-        pw[kb][qd] = w ^ 0x7f7f7f7fu;  // 127 - P as s8
+        pw[kb][qd] = pack_byte1(y[0], y[1], y[2], y[3]) ^ 0x7f7f7f7fu;  // 127 - P as s8
+        rsn = __builtin_amdgcn_sdot4((int)pw[kb][qd], 0x01010101, rsn, false);
       }
-    st.den = __builtin_fmaf((float)xor32_add(rs), bq, st.den * alpha);
+    // the row's 64 levels: 2 * 32 * 127 minus the sum of 127 - P over lanes L and L ^ 32 (mod 2^32)
+    const uint32_t rs = 8128u - xor32_add((uint32_t)rsn);
+    st.den = __builtin_fmaf((float)rs, bq, st.den * alpha);
     const v4i neg127 = {(int)0x81818181u, (int)0x81818181u, (int)0x81818181u, (int)0x81818181u};
     const v4i b0 = {(int)pw[0][0], (int)pw[0][1], (int)pw[0][2], (int)pw[0][3]};
     const v4i b1 = {(int)pw[1][0], (int)pw[1][1], (int)pw[1][2], (int)pw[1][3]};

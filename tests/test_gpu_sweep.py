@@ -3,7 +3,10 @@ then a few decode steps against the oracle, for shapes the fixed cases do not pi
 size 1..8, prompt lengths around tile edges and in between, random (w8, w4) band pairs (w4 below w8
 included), batches of 1-3, tails from 1 slot (every step overwrites it) to longer than the steps, and
 uniform splits of 1..7 tiles or the cache's own partition; and ragged caches, prompts of different
-lengths (sequences of 1 token included) stored one Prefill call at a time and decoded together.
+lengths (sequences of 1 token included) stored one Prefill call at a time and decoded together; and
+caches with tail growth and exact (bf16) KV heads over a few hundred steps (two to four spills of the
+tail into the cache), quantized heads against the oracle's GrowingTail, exact heads against float64
+attention over every raw key.
 
 Bar: as in test_gpu_parity (fp32 outputs within 2e-3 max-abs, 1e-3 mean-abs of the oracle)."""
 from __future__ import annotations
@@ -14,6 +17,7 @@ import torch
 
 import oracle as O
 from helpers import assert_close, compare_codes, oracle_prefill, run_prefill
+from test_gpu_parity import _attend64
 from triattention_amd import synthetic as S
 from triattention_amd.kernels.decode import DecodeCache
 from triattention_amd.synthetic import INF, bits
@@ -22,6 +26,7 @@ pytestmark = pytest.mark.gpu
 
 CASES = 40
 RAGGED_CASES = 12
+GROWTH_CASES = 8
 
 
 def draw(i):
@@ -116,3 +121,58 @@ def test_random_ragged_cache_decode(module, i):
             ktail[b, :, prior] = bits(kd[b, :, 0])
             vtail[b, :, prior] = bits(vd[b, :, 0])
         cache.advance()
+
+
+@pytest.mark.parametrize("i", range(GROWTH_CASES))
+def test_random_tail_growth_with_exact_heads(module, i):
+    r = np.random.default_rng(9700 + i)
+    c = draw(200 + i)
+    g = c["g"]
+    hk = max(2, c["hk"])
+    hq = g * hk
+    bands = torch.tensor((c["bands"] * 2)[:hq], dtype=torch.int32)
+    bf16_kv = sorted(int(h) for h in r.choice(hk, size=int(r.integers(0, hk)), replace=False))
+    max_tail = int(r.choice([64, 65, 100, 128]))
+    steps = int(r.integers(2 * max_tail + 10, 4 * max_tail + 20))
+    prompts = [int(r.integers(1, 700)) for _ in range(int(r.integers(1, 4)))]
+    print(f"\n[sweep] growth case {i}: prompts={prompts} hq={hq} hk={hk} exact={bf16_kv} max_tail={max_tail} "
+          f"steps={steps}", flush=True)
+    scale = 128 ** -0.5
+    cache = DecodeCache(module, max_tail=max_tail, grow_tail=steps)
+    cache.ragged = len(prompts) > 1
+    cache.out_dtype = torch.float32
+    gen = S.gen(9800 + i)
+    seqs, raw = [], []
+    for n in prompts:
+        q, k, v = S.outlier_tensor(gen, 1, hq, n), S.outlier_tensor(gen, 1, hk, n), S.outlier_tensor(gen, 1, hk, n)
+        run_prefill(module, q, k, v, bands, scale, decode_cache=cache, bf16_kv=bf16_kv)
+        codes = O.prefill_codes(None, bits(k[0]), bits(v[0]), bands.numpy(), decode_cache=True)
+        seqs.append(O.GrowingTail(codes, bands.numpy(), n, max_tail))
+        kr, vr = torch.zeros(hk, n + steps, 128), torch.zeros(hk, n + steps, 128)
+        kr[:, :n], vr[:, :n] = k[0].float(), v[0].float()
+        raw.append((kr, vr, n))
+    exact_q = [h for h in range(hq) if h // g in bf16_kv]
+    quant_q = [h for h in range(hq) if h // g not in bf16_kv]
+    dev = torch.device("cuda")
+    nb = len(prompts)
+    for t in range(steps):
+        qd, kd, vd = S.outlier_tensor(gen, nb, hq, 1), S.outlier_tensor(gen, nb, hk, 1), S.outlier_tensor(gen, nb, hk, 1)
+        out = cache(0, qd.to(dev), kd.to(dev), vd.to(dev), scale)
+        check = t % 23 == 0 or seqs[0].held >= max_tail - 1 or t == steps - 1
+        if check:
+            out = out.cpu().numpy()
+        for b in range(nb):
+            want = seqs[b].step(bits(qd[b, :, 0]), bits(kd[b, :, 0]), bits(vd[b, :, 0]), cache.split_of(0, b), scale,
+                                compute=check)
+            kr, vr, p = raw[b]
+            kr[:, p + t], vr[:, p + t] = kd[b, :, 0].float(), vd[b, :, 0].float()
+            if check:
+                if quant_q:
+                    assert_close(out[b, quant_q, 0], want[quant_q], what=f"growth case {i} step {t} seq {b} quantized")
+                if exact_q:
+                    r64, r32 = _attend64(qd[b, :, 0], kr[:, :p + t + 1], vr[:, :p + t + 1], scale)
+                    bar = max(2e-3, float(np.abs(r32[exact_q] - r64[exact_q]).max()))
+                    assert_close(out[b, exact_q, 0], r64[exact_q], max_abs=bar,
+                                 what=f"growth case {i} step {t} seq {b} exact")
+        cache.advance()
+    assert cache.layers[0]["store"].tb >= 64

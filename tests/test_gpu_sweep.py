@@ -6,7 +6,8 @@ uniform splits of 1..7 tiles or the cache's own partition; and ragged caches, pr
 lengths (sequences of 1 token included) stored one Prefill call at a time and decoded together; and
 caches with tail growth and exact (bf16) KV heads over a few hundred steps (two to four spills of the
 tail into the cache), quantized heads against the oracle's GrowingTail, exact heads against float64
-attention over every raw key.
+attention over every raw key; and prefill with random exact (bf16) KV heads and a bf16 or fp32 output,
+quantized heads against the oracle, exact heads against float64 attention.
 
 Bar: as in test_gpu_parity (fp32 outputs within 2e-3 max-abs, 1e-3 mean-abs of the oracle)."""
 from __future__ import annotations
@@ -16,7 +17,8 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close, compare_codes, oracle_prefill, run_prefill
+from helpers import (assert_close, assert_close_bf16, compare_codes, exact_max_abs_bar, exact_reference, oracle_prefill,
+                     run_prefill)
 from test_gpu_parity import _attend64
 from triattention_amd import synthetic as S
 from triattention_amd.kernels.decode import DecodeCache
@@ -27,6 +29,7 @@ pytestmark = pytest.mark.gpu
 CASES = 40
 RAGGED_CASES = 12
 GROWTH_CASES = 8
+EXACT_CASES = 12
 
 
 def draw(i):
@@ -176,3 +179,30 @@ def test_random_tail_growth_with_exact_heads(module, i):
                                  what=f"growth case {i} step {t} seq {b} exact")
         cache.advance()
     assert cache.layers[0]["store"].tb >= 64
+
+
+@pytest.mark.parametrize("i", range(EXACT_CASES))
+def test_random_prefill_with_exact_heads(module, i):
+    r = np.random.default_rng(9900 + i)
+    c = draw(300 + i)
+    g, hk, batch = c["g"], max(2, c["hk"]), c["batch"]
+    hq = g * hk
+    t = int(r.integers(1, 1500))
+    bands = torch.tensor((c["bands"] * 2)[:hq], dtype=torch.int32)
+    bf16_kv = sorted(int(h) for h in r.choice(hk, size=int(r.integers(1, hk + 1)), replace=False))
+    out_dtype = torch.bfloat16 if r.random() < 0.5 else torch.float32
+    print(f"\n[sweep] exact case {i}: batch={batch} hq={hq} hk={hk} t={t} exact={bf16_kv} out={out_dtype}", flush=True)
+    gen = S.gen(9950 + i)
+    q, k, v = S.outlier_tensor(gen, batch, hq, t), S.outlier_tensor(gen, batch, hk, t), S.outlier_tensor(gen, batch, hk, t)
+    scale = 128 ** -0.5
+    out, _, _ = run_prefill(module, q, k, v, bands, scale, out_dtype=out_dtype, bf16_kv=bf16_kv)
+    out = out.numpy()
+    exact_q = [h for h in range(hq) if h // g in bf16_kv]
+    quant_q = [h for h in range(hq) if h // g not in bf16_kv]
+    close = assert_close_bf16 if out_dtype == torch.bfloat16 else assert_close
+    if quant_q:
+        ref, _ = oracle_prefill(q, k, v, bands, scale)
+        close(out[:, quant_q], ref[:, quant_q], what=f"exact case {i} quantized heads")
+    ex = exact_reference(q, k, v, scale)
+    bar = exact_max_abs_bar(q, k, v, scale, exact_q, ex)
+    close(out[:, exact_q], ex[:, exact_q], max_abs=bar, what=f"exact case {i} exact heads")

@@ -307,16 +307,25 @@ __device__ __forceinline__ void exact_step(const PrefillArgs& a, int col, int kb
         for (int r = 0; r < 16; ++r) acc[cb][r] *= alpha;
     }
   }
-  v8bf phi[2], plo[2];
+  // P in pairs: one packed conversion gives the two high parts, their fp32 values are the high
+  // and low halves of that word, and a second packed conversion gives the two low parts
+  uint32_t hw[8], lw[8];
   float psum = 0.f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.sm_log2, -m));
-    const __bf16 h = (__bf16)p;
-    phi[r >> 3][r & 7] = h;
-    plo[r >> 3][r & 7] = (__bf16)(p - (float)h);
-    psum += p;
+  for (int j = 0; j < 8; ++j) {
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * j], a.sm_log2, -m));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * j + 1], a.sm_log2, -m));
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){p0, p1}, v2bf));
+    const float h0 = __uint_as_float(h << 16), h1 = __uint_as_float(h & 0xffff0000u);
+    hw[j] = h;
+    lw[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){p0 - h0, p1 - h1}, v2bf));
+    psum += p0;
+    psum += p1;
   }
+  const v8bf phi[2] = {__builtin_bit_cast(v8bf, make_uint4(hw[0], hw[1], hw[2], hw[3])),
+                       __builtin_bit_cast(v8bf, make_uint4(hw[4], hw[5], hw[6], hw[7]))};
+  const v8bf plo[2] = {__builtin_bit_cast(v8bf, make_uint4(lw[0], lw[1], lw[2], lw[3])),
+                       __builtin_bit_cast(v8bf, make_uint4(lw[4], lw[5], lw[6], lw[7]))};
   den += xor32_add(psum);
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb)
@@ -353,10 +362,15 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[cb][r] = 0.f;
   float m = -3.402823466e38f, den = 0.f;
+  // the head's records as buffer resources: step st at byte (st / 2) * KX_BYTES + (st % 2) * KX_BYTES / 2
+  const __amdgpu_buffer_rsrc_t rkx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kx, (short)0, tiles * KX_BYTES, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rvx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vx, (short)0, tiles * KX_BYTES, 0x00020000);
   auto issue = [&](int st, uint8_t* kd, uint8_t* vd) {
-    const int64_t off = (int64_t)(st >> 1) * KX_BYTES + (st & 1) * (KX_BYTES / 2);
-    lds_copy_async<KX_BYTES / 2>(kx + off, kd);
-    lds_copy_async<KX_BYTES / 2>(vx + off, vd);
+    const int off = (st >> 1) * KX_BYTES + (st & 1) * (KX_BYTES / 2);
+    lds_copy_buf<KX_BYTES / 2>(rkx, off, kd);
+    lds_copy_buf<KX_BYTES / 2>(rvx, off, vd);
   };
   issue(0, k0, v0);
   // tiles before the diagonal: no mask

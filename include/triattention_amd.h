@@ -43,9 +43,11 @@ int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, cons
 /* Replaces pack_v (common_host.cuh:27-45).
  * v: bf16 [batch][hk][t][128]; vstat f32 [batch][hk][3][128].  Statistics are
  * the identity (0, 1, 1) when both v8p and v4p are NULL (common_host.cuh:39).
- * v16p/v8p/v4p: V16/V8/V4 records [batch][hk][tiles] or NULL. */
+ * v16p/v8p/v4p: V16/V8/V4 records [batch][hk][tiles] or NULL.
+ * v8sum (extension; NULL, or with v8p, 16-byte aligned): int32 [batch][hk][tiles][128], -127 times
+ * each channel's sum of the tile's 64 V8 codes, for tri_attention's v8sum. */
 int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batch, int hk, int t, float* partial,
-               float* vstat, void* v16p, void* v8p, void* v4p, void* stream);
+               float* vstat, void* v16p, void* v8p, void* v4p, int32_t* v8sum, void* stream);
 
 /* Replaces attention (prefill_sm80.cu:510-543), band-table form only (the
  * reference's task-table form has no caller, prefill.py:103).
@@ -61,13 +63,16 @@ int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batc
  * and computes exact causal attention of the raw bf16 qr [batch][hq][t][128]
  * (strides q_sb, q_sh, q_st; rows 16-byte aligned) against the KX/VX records
  * [batch][nx][tiles] that tri_pack_exact wrote, with fp32 softmax and
- * accumulation (extension for maps that keep some heads unquantized). */
+ * accumulation (extension for maps that keep some heads unquantized).
+ * v8sum (extension): NULL, or what tri_pack_v wrote for these V8 records; the
+ * P V product of each INT8/INT4 tile then starts from it instead of computing
+ * it with two MFMAs per 32 channels (the same integers either way). */
 int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int batch, int hq, int hk, int t,
                   const void* v16p, const void* v8p, const float* vstat, const void* q8, const void* k8p,
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
                   double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
-                  const void* kx, const void* vx, int nx, void* stream);
+                  const void* kx, const void* vx, int nx, const int32_t* v8sum, void* stream);
 
 /* No counterpart in the reference: the bf16 records of the exact heads that
  * tri_attention reads (extension).  k/v bf16 [batch][hk][t][128] with element

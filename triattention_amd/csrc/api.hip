@@ -115,13 +115,14 @@ int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, cons
 }
 
 int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batch, int hk, int t, float* partial,
-               float* vstat, void* v16p, void* v8p, void* v4p, void* stream) {
+               float* vstat, void* v16p, void* v8p, void* v4p, int32_t* v8sum, void* stream) {
   g_error.clear();
   if (!v || !partial || !vstat) return fail("pack_v: null buffer");
   if (batch < 1 || hk < 1 || t < 1) return fail("pack_v: empty shape");
   if (!aligned(v, 8) || (v_st | v_sh | v_sb) % 4 != 0) return fail("pack_v: V rows must be 8-byte aligned");
   if ((v16p && !aligned(v16p, 16)) || (v8p && !aligned(v8p, 16)) || (v4p && !aligned(v4p, 8)))
     return fail("pack_v: record buffers must be 16-byte aligned");
+  if (v8sum && (!v8p || !aligned(v8sum, 16))) return fail("pack_v: V8 sums need the V8 records, 16-byte aligned");
   const int tiles = (t + tri::BN - 1) / tri::BN;
   const bool identity = v8p == nullptr && v4p == nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -131,7 +132,8 @@ int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batc
   tri::finalize_kernel<<<dim3(hk, batch), tri::D, 0, s>>>(partial, vstat, hk, t, identity ? 1 : 0);
   tri::pack_v_kernel<<<dim3(tiles, hk, batch), 256, 0, s>>>(static_cast<const uint16_t*>(v), v_sb, v_sh, v_st, vstat,
                                                             hk, t, static_cast<uint8_t*>(v16p),
-                                                            static_cast<uint8_t*>(v8p), static_cast<uint8_t*>(v4p));
+                                                            static_cast<uint8_t*>(v8p), static_cast<uint8_t*>(v4p),
+                                                            v8sum);
   return check_launch("pack_v");
 }
 
@@ -140,7 +142,7 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
                   double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
-                  const void* kx, const void* vx, int nx, void* stream) {
+                  const void* kx, const void* vx, int nx, const int32_t* v8sum, void* stream) {
   g_error.clear();
   const int tiles = (t + tri::BN - 1) / tri::BN;
   if (!order || !bands || !v16p || !vstat || !q8 || !k8p || !qa8 || !ka8 || !out)
@@ -160,6 +162,7 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
       (int4 && (!aligned(k4p, 16) || !aligned(ka4, 16))))
     return fail("attention: record and K-scale buffers must be 16-byte aligned");
   if (int4 && v8p == nullptr) return fail("attention: INT4 key tiles need the INT8 V records");
+  if (v8sum && (!v8p || !aligned(v8sum, 16))) return fail("attention: V8 sums need the V8 records, 16-byte aligned");
   if (exact != nullptr && (!qr || !aligned(qr, 16) || (q_sb | q_sh | q_st) % 8 != 0))
     return fail("attention: exact heads need 16-byte aligned bf16 q rows");
   if (exact != nullptr && (nx < 1 || nx > hk || !kx || !vx || !aligned(kx, 16) || !aligned(vx, 16)))
@@ -195,8 +198,10 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
   a.hk = hk;
   a.t = t;
   a.sm_log2 = (float)(scale * 1.4426950408889634);
+  a.v8s = v8sum;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  tri::prefill_kernel<<<dim3(n_order, batch), 128, 0, s>>>(a);
+  if (v8sum) tri::prefill_kernel<true><<<dim3(n_order, batch), 128, 0, s>>>(a);
+  else tri::prefill_kernel<false><<<dim3(n_order, batch), 128, 0, s>>>(a);
   return check_launch("attention");
 }
 

@@ -42,6 +42,9 @@ struct PrefillArgs {
   const uint8_t* kx;      // KX records [batch][nx][tiles]
   const uint8_t* vx;      // VX records [batch][nx][tiles]
   int nx;
+  // extension (may be null): per V8 record, -127 times each channel's sum of its 64 codes (int32 [128]),
+  // the starting value of the tile's P V accumulators (else two MFMAs compute it)
+  const int32_t* v8s;
 };
 
 enum Kind { KF16 = 0, KI8 = 1, KQ4 = 2 };
@@ -63,11 +66,14 @@ __device__ __forceinline__ v4i k_frag(const uint8_t* __restrict__ k_lds, int F, 
   }
 }
 
-template <int KIND>
+// SUMS: the quantized P V accumulators start from the tile's -127 * sum(V8) in LDS (vs_lds, channel
+// order) instead of two MFMAs against a constant -127 operand
+template <int KIND, bool SUMS = false>
 __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState& st, const v4i (&qf)[4], float qs,
                                              const float (&ks)[4], int col, bool masked, int qrow,
                                              const uint8_t* __restrict__ k_lds, const uint8_t* __restrict__ v_lds,
-                                             const uint8_t* __restrict__ v_hi = nullptr) {
+                                             const uint8_t* __restrict__ v_hi = nullptr,
+                                             const int32_t* __restrict__ vs_lds = nullptr) {
   const int L = threadIdx.x & 63, half = L >> 5;
   // ---- S^T = K Q^T over 128 features, two 32-key blocks
   v16i s[2];
@@ -213,8 +219,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
       const v4i va = *reinterpret_cast<const v4i*>(v_lds + (cb * 2 + 0) * 1024 + L * 16);
       const v4i vb = *reinterpret_cast<const v4i*>(v_lds + (cb * 2 + 1) * 1024 + L * 16);
       v16i d = {};
-      d = mfma_i8(va, neg127, d);
-      d = mfma_i8(vb, neg127, d);
+      if constexpr (SUMS) {
+        // accumulator r of channel block cb is channel cb*32 + 8*(r/4) + 4*half + r%4
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v4i w = *reinterpret_cast<const v4i*>(vs_lds + cb * 32 + 8 * j + 4 * half);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) d[4 * j + i] = w[i];
+        }
+      } else {
+        d = mfma_i8(va, neg127, d);
+        d = mfma_i8(vb, neg127, d);
+      }
       d = mfma_i8(va, b0, d);
       d = mfma_i8(vb, b1, d);  // = -sum_k P_k v_k
 #pragma unroll
@@ -484,6 +500,8 @@ struct Tag {
   static constexpr int value = V;
 };
 
+// SUMS: a.v8s is given (the P V accumulators of quantized tiles start from it)
+template <bool SUMS>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillArgs a) {
   // LDS: two K buffers (8 KiB) and two V buffers (8 KiB), distinct objects so
   // that the compiler can tell a read of one buffer from a load into the other;
@@ -491,6 +509,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   __shared__ __align__(16) uint8_t k_lds0[K8_BYTES], k_lds1[K8_BYTES];
   __shared__ __align__(16) uint8_t v_lds0[V8_BYTES], v_lds1[V8_BYTES];
   __shared__ __align__(16) float ks_lds0[4], ks_lds1[4];  // the tile's 4 K group scales
+  __shared__ __align__(16) int32_t vs_lds0[SUMS ? D : 4], vs_lds1[SUMS ? D : 4];  // its -127 * V8 sums
   const int rows = (a.t + BN - 1) / BN;
   // Launch sequence: BandTable's order is KV-head-major (prefill.py:24-25), so the workgroups running at
   // any one time would all belong to one KV head.  Workgroup j takes entry (kv * rows + qd) * g + r of it
@@ -586,33 +605,42 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
         (void*)(a.k4 ? a.k4 + rec0 * K4_BYTES : a.k8), (short)0, a.k4 ? tiles * K4_BYTES : 0, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv8 =
         __builtin_amdgcn_make_buffer_rsrc((void*)(a.v8 + rec0 * V8_BYTES), (short)0, tiles * V8_BYTES, 0x00020000);
-    auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd) {
+    // (a local copy: reading the kernel argument inside the lambda would put the argument block in
+    // private memory)
+    const int32_t* v8s = SUMS ? a.v8s + rec0 * D : nullptr;
+    auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd, int32_t* vsd) __attribute__((always_inline)) {
       const int col = tile_col(i);
       if (i < n8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd);
       else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd);
       lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd);
-      // the scales ride along in the same kind of copy, so reading them later
-      // waits on nothing but the records' own wait
+      // the scales (and the V8 sums: 512 bytes, 16 per lane of the first 32) ride along in the same
+      // kind of copy, so reading them later waits on nothing but the records' own wait
       if (tid == 0)
         __builtin_amdgcn_global_load_lds(static_cast<const void*>((i < n8 ? ka8 : ka4p) + col * 4),
                                          (__attribute__((address_space(3))) void*)sd, 16, 0, 0);
+      if constexpr (SUMS) {
+        if (tid < 32)
+          __builtin_amdgcn_global_load_lds(static_cast<const void*>(v8s + col * D + tid * 4),
+                                           (__attribute__((address_space(3))) void*)vsd, 16, 0, 0);
+      }
     };
     // tile i of kind KIND: wait for its records (and for every wave to finish
     // tile i-1, whose buffers receive tile i+1), start tile i+1's loads, compute
-    auto step = [&](auto kind, int i, const uint8_t* kc, const uint8_t* vc, const float* sc, uint8_t* kn,
-                    uint8_t* vn, float* sn) {
+    auto step = [&](auto kind, int i, const uint8_t* kc, const uint8_t* vc, const float* sc, const int32_t* vsc,
+                    uint8_t* kn, uint8_t* vn, float* sn, int32_t* vsn) __attribute__((always_inline)) {
       lds_wait();
-      if (i + 1 < total) issue(i + 1, kn, vn, sn);
+      if (i + 1 < total) issue(i + 1, kn, vn, sn, vsn);
       const int col = tile_col(i);
       const float4 k4v = *reinterpret_cast<const float4*>(sc);
       const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
-      if constexpr (decltype(kind)::value == KI8) prefill_tile<KI8>(a, st, qf, qs8, ks, col, false, qrow, kc, vc);
-      else prefill_tile<KQ4>(a, st, q4f, qs4, ks, col, false, qrow, kc, vc);
+      if constexpr (decltype(kind)::value == KI8)
+        prefill_tile<KI8, SUMS>(a, st, qf, qs8, ks, col, false, qrow, kc, vc, nullptr, vsc);
+      else prefill_tile<KQ4, SUMS>(a, st, q4f, qs4, ks, col, false, qrow, kc, vc, nullptr, vsc);
     };
     // Tiles [i, end) of one kind, the first in buffer set PARITY.  Each kind has a
     // loop of its own: with both kinds in one loop body the compiler copies the
     // accumulators between register sets at every tile (~30 VALU per tile).
-    auto run = [&](auto kind, auto parity, int i, int end) {
+    auto run = [&](auto kind, auto parity, int i, int end) __attribute__((always_inline)) {
       constexpr bool p = decltype(parity)::value != 0;
       uint8_t* k0 = p ? k_lds1 : k_lds0;
       uint8_t* k1 = p ? k_lds0 : k_lds1;
@@ -620,13 +648,15 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
       uint8_t* v1 = p ? v_lds0 : v_lds1;
       float* s0 = p ? ks_lds1 : ks_lds0;
       float* s1 = p ? ks_lds0 : ks_lds1;
+      int32_t* w0 = p ? vs_lds1 : vs_lds0;
+      int32_t* w1 = p ? vs_lds0 : vs_lds1;
       for (; i < end; i += 2) {
-        step(kind, i, k0, v0, s0, k1, v1, s1);
-        if (i + 1 < end) step(kind, i + 1, k1, v1, s1, k0, v0, s0);
+        step(kind, i, k0, v0, s0, w0, k1, v1, s1, w1);
+        if (i + 1 < end) step(kind, i + 1, k1, v1, s1, w1, k0, v0, s0, w0);
       }
     };
     __syncthreads();  // every wave is done with the F16 pass's LDS
-    issue(0, k_lds0, v_lds0, ks_lds0);
+    issue(0, k_lds0, v_lds0, ks_lds0, vs_lds0);
     run(Tag<KI8>{}, Tag<0>{}, 0, n8);
     if (n8 & 1) run(Tag<KQ4>{}, Tag<1>{}, n8, total);
     else run(Tag<KQ4>{}, Tag<0>{}, n8, total);

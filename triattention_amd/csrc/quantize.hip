@@ -216,11 +216,15 @@ __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restr
 // v' = (v - mean) * inv of one 64-key tile (rows src + r * st for r < rows, zeros past) into the V16
 // (fp16), V8 and V4 records (any may be null); vn is the workgroup's LDS staging.  256 threads.
 // common_device.cuh:132-172 (vnorm, pack_v_kernel).
+// Extension: v8s (with v8; may be null) receives -127 times each channel's sum of the tile's 64 V8 codes
+// (int32 [128], channel order), the value the prefill's P V product starts from (vsum: LDS of 128 ints).
 __device__ __forceinline__ void pack_v_tile(const uint16_t* __restrict__ src, int64_t st, int rows,
                                             const float* __restrict__ mean, const float* __restrict__ inv,
                                             uint8_t* __restrict__ v16, uint8_t* __restrict__ v8,
-                                            uint8_t* __restrict__ v4, float (*vn)[D + 1]) {
+                                            uint8_t* __restrict__ v4, float (*vn)[D + 1],
+                                            int32_t* __restrict__ v8s = nullptr, int* vsum = nullptr) {
   const int tid = threadIdx.x;
+  if (v8s != nullptr && tid < D) vsum[tid] = 0;
   for (int i = tid; i < BN * D / 4; i += 256) {
     const int r = i / (D / 4), c0 = (i % (D / 4)) * 4;
     float x[4] = {0.f, 0.f, 0.f, 0.f};
@@ -255,6 +259,7 @@ __device__ __forceinline__ void pack_v_tile(const uint16_t* __restrict__ src, in
     const int s = tid + it * 256, F = s >> 6, L = s & 63, kb = F & 1, cb = F >> 1;
     const int ch = cb * 32 + (L & 31), g = L >> 5;
     uint32_t b8[4] = {0, 0, 0, 0}, b4[4] = {0, 0, 0, 0};
+    int sum8 = 0;
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
       const float x = vn[kb * 32 + 8 * (p / 4) + 4 * g + p % 4][ch];
@@ -262,11 +267,18 @@ __device__ __forceinline__ void pack_v_tile(const uint16_t* __restrict__ src, in
       const int q4 = max(-7, min(7, (int)__builtin_rintf(x * (7.f / 127.f))));
       b8[p / 4] |= ((uint32_t)q8 & 0xffu) << (8 * (p % 4));
       b4[p / 4] |= ((uint32_t)q4 & 0xfu) << (8 * (p % 4));
+      sum8 += q8;
     }
+    // four threads hold 16 keys each of channel ch: integer adds, so the sum is order-free
+    if (v8s != nullptr) atomicAdd(&vsum[ch], sum8);
     if (v8 != nullptr) *reinterpret_cast<uint4*>(v8 + F * 1024 + L * 16) = make_uint4(b8[0], b8[1], b8[2], b8[3]);
     if (v4 != nullptr)
       *reinterpret_cast<uint2*>(v4 + (F >> 1) * 1024 + L * 16 + (F & 1) * 8) =
           make_uint2(b4[0] | (b4[1] << 4), b4[2] | (b4[3] << 4));
+  }
+  if (v8s != nullptr) {
+    __syncthreads();
+    if (tid < D) v8s[tid] = -127 * vsum[tid];
   }
 }
 
@@ -274,14 +286,15 @@ __device__ __forceinline__ void pack_v_tile(const uint16_t* __restrict__ src, in
 __global__ __launch_bounds__(256) void pack_v_kernel(const uint16_t* __restrict__ v, int64_t sb, int64_t sh,
                                                      int64_t st, const float* __restrict__ vstat, int hk, int t,
                                                      uint8_t* __restrict__ v16, uint8_t* __restrict__ v8,
-                                                     uint8_t* __restrict__ v4) {
+                                                     uint8_t* __restrict__ v4, int32_t* __restrict__ v8s) {
   __shared__ float vn[BN][D + 1];
+  __shared__ int vsum[D];
   const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN;
   const int64_t hb = (int64_t)b * hk + hd, rec = hb * tiles + tile;
   const float* mean = vstat + hb * 3 * D;
   pack_v_tile(v + b * sb + hd * sh + (int64_t)tile * BN * st, st, t - tile * BN, mean, mean + 2 * D,
               v16 != nullptr ? v16 + rec * V16_BYTES : nullptr, v8 != nullptr ? v8 + rec * V8_BYTES : nullptr,
-              v4 != nullptr ? v4 + rec * V4_BYTES : nullptr, vn);
+              v4 != nullptr ? v4 + rec * V4_BYTES : nullptr, vn, v8s != nullptr ? v8s + rec * D : nullptr, vsum);
 }
 
 }  // namespace tri

@@ -60,9 +60,9 @@ def load_library() -> ctypes.CDLL:
     lib.tri_last_error.argtypes = []
     lib.tri_prepare_qk.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I,
                                    P, P, P, P, P, P, P, P, P, P, P]
-    lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P]
+    lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P, P]
     lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_,
-                                  P, P, I64, I64, I64, P, P, I, P]
+                                  P, P, I64, I64, I64, P, P, I, P, P]
     lib.tri_pack_exact.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I, P, I, P, P, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64,
@@ -145,8 +145,11 @@ class Module:
                        _ptr(kstat), _ptr(q4), _ptr(qa4), _ptr(k4p), _ptr(ka4), self._stream(q.device))
 
     # ------------------------------------------------------------------ pack_v
-    def pack_v(self, v, partial, vstat, v16p=None, v8p=None, v4p=None):
-        """Normalised BF16 V' into FP16/INT8/INT4 PV operands."""
+    def pack_v(self, v, partial, vstat, v16p=None, v8p=None, v4p=None, v8sum=None):
+        """Normalised BF16 V' into FP16/INT8/INT4 PV operands.
+
+        Extension: ``v8sum`` (int32 [B*Hkv*tiles*128], with ``v8p``) receives -127 times each channel's
+        sum of each tile's V8 codes, which ``attention(..., v8sum=...)`` starts its P V products from."""
         _check(v.is_cuda and v.dtype == torch.bfloat16 and v.dim() == 4 and v.size(3) == D and v.stride(3) == 1,
                "BF16 V [B,Hkv,T,128]")
         b, hk, t, _ = v.shape
@@ -156,19 +159,21 @@ class Module:
         for x, words in ((v16p, V16_WORDS), (v8p, V8_WORDS), (v4p, V4_WORDS)):
             _check(x is None or (x.dtype == torch.uint32 and x.is_contiguous() and x.numel() == b * hk * tiles * words),
                    "packed V size")
+        _check(v8sum is None or (v8p is not None and _v8sum_ok(v8sum, b * hk * tiles)), "V8 sums")
         with torch.cuda.device(v.device):
             self._call(self.lib.tri_pack_v, _ptr(v), v.stride(0), v.stride(1), v.stride(2), b, hk, t, _ptr(partial),
-                       _ptr(vstat), _ptr(v16p), _ptr(v8p), _ptr(v4p), self._stream(v.device))
+                       _ptr(vstat), _ptr(v16p), _ptr(v8p), _ptr(v4p), _ptr(v8sum), self._stream(v.device))
 
     # --------------------------------------------------------------- attention
     def attention(self, order, bands, groups, entries, v16p, v8p, v4p, vstat, q8, k8p, qa8, ka8, q4, k4p, qa4, ka4,
-                  out, scale, exact=None, q=None, kx=None, vx=None, nx=0):
+                  out, scale, exact=None, q=None, kx=None, vx=None, nx=0, v8sum=None):
         """Banded causal attention: per key tile skip / INT8 QK x FP16 or INT8 PV / INT4 QK x INT8 PV.
 
         Extension: ``exact`` (int32 [Hq] on the device, 0 or 1 + record slot
         of the q-head's KV head) with the raw bf16 ``q`` [B,Hq,T,128] and the
         ``kx``/``vx`` records of ``pack_exact`` computes the flagged q-heads as
-        exact causal attention on the unquantized operands."""
+        exact causal attention on the unquantized operands.  ``v8sum``: what
+        ``pack_v(..., v8sum=...)`` wrote for ``v8p`` (the same result, fewer MFMAs)."""
         _check(q8.dtype == torch.int8 and q8.dim() == 4 and q8.size(3) == D and q8.is_contiguous(), "Q8 [B,Hq,T,128]")
         b, h, t, _ = q8.shape
         hk = vstat.numel() // (b * 3 * D)
@@ -192,6 +197,7 @@ class Module:
             _check(1 <= nx <= hk and kx is not None and vx is not None and
                    kx.numel() * kx.element_size() >= b * nx * tiles * KX_BYTES and
                    vx.numel() * vx.element_size() >= b * nx * tiles * KX_BYTES, "exact heads: KX/VX records")
+        _check(v8sum is None or (v8p is not None and _v8sum_ok(v8sum, b * hk * tiles)), "V8 sums")
         qs = q.stride() if exact is not None else (0, 0, 0)
         with torch.cuda.device(q8.device):
             self._call(self.lib.tri_attention, _ptr(order), order.numel(), _ptr(bands), b, h, hk, t, _ptr(v16p),
@@ -199,7 +205,7 @@ class Module:
                        _ptr(qa4), _ptr(ka4), _ptr(out), dt, out.stride(0), out.stride(1), out.stride(2),
                        float(scale), _ptr(exact), _ptr(q if exact is not None else None), qs[0], qs[1], qs[2],
                        _ptr(kx if exact is not None else None), _ptr(vx if exact is not None else None),
-                       int(nx) if exact is not None else 0, self._stream(q8.device))
+                       int(nx) if exact is not None else 0, _ptr(v8sum), self._stream(q8.device))
         return out
 
     def pack_exact(self, k, v, exact, nx, kx, vx):
@@ -533,6 +539,12 @@ class SpillPlan:
                 self.module._call(self.module.lib.tri_tail_spill, *self.args)
         else:
             self.module._call(self.module.lib.tri_tail_spill, *self.args)
+
+
+def _v8sum_ok(x, tiles_all):
+    """int32 V8 sums of ``tiles_all`` (sequence, KV head, tile) records, 128 per tile, 16-byte aligned."""
+    return (x.dtype == torch.int32 and x.is_contiguous() and x.numel() == tiles_all * D and
+            x.data_ptr() % 16 == 0)
 
 
 def _only_f16(bands, tiles: int) -> bool:

@@ -93,6 +93,8 @@ SCRATCH = (
     (f"v{F16}", lambda L: L.batch * L.hk * L.tiles * WORDS[F16], torch.uint32, lambda L: F16 in L.formats),
     (f"v{I8}", lambda L: L.batch * L.hk * L.tiles * WORDS[I8], torch.uint32, lambda L: I8 in L.formats or L.int4),
     (f"v{I4}", lambda L: L.batch * L.hk * L.tiles * WORDS[I4], torch.uint32, lambda L: I4 in L.formats),
+    # -127 * each channel's sum of every INT8 V record (extension: the P V products start from it)
+    ("v8sum", lambda L: L.batch * L.hk * L.tiles * 128, torch.int32, lambda L: I8 in L.formats or L.int4),
 )
 
 
@@ -206,7 +208,8 @@ class Prefill:
         packed = ops["packed"]
         self.module.prepare_qk(q, k, ops["q8"], ops["qa"], ops["kp"], ops["ka"], ops["partial"], ops["kstat"],
                                ops["q4"], ops["qa4"], ops["k4"], ops["ka4"])
-        self.module.pack_v(v, ops["partial"], ops["vstat"], packed[F16], packed[I8], packed[I4])
+        v8sum = ops["v8sum"] if attend else None  # (only the prompt's attention reads the sums)
+        self.module.pack_v(v, ops["partial"], ops["vstat"], packed[F16], packed[I8], packed[I4], v8sum=v8sum)
         exact, nx = self.exact(layer, hq, hk, device)
         kx = vx = None
         if exact is not None:
@@ -219,7 +222,7 @@ class Prefill:
             extra = {} if exact is None else dict(exact=exact, q=q, kx=kx, vx=vx, nx=nx)
             self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4],
                                   ops["vstat"], ops["q8"], ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"],
-                                  ops["qa4"], ops["ka4"], out, scale, **extra)
+                                  ops["qa4"], ops["ka4"], out, scale, v8sum=v8sum, **extra)
         if decode is not None:
             exact_kv = sorted(set(int(h) for h in self.bands_fn.bf16(layer))) if exact is not None else []
             self.decode_cache.store(layer, t, ops["kp"], ops["ka"], ops["kstat"], ops["vstat"], packed, decode[0],

@@ -59,7 +59,7 @@ def lib():
         L.ora_pack_v.argtypes = [P, I64, I64, I, I, P, P, P, P]
         L.ora_band_tiles.restype = I
         L.ora_band_tiles.argtypes = [I, I, I, P, P]
-        L.ora_prefill.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, P, I]
+        L.ora_prefill.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, P, P, I]
         L.ora_decode_state.restype = I
         L.ora_decode_state.argtypes = [I, I, I, I]
         L.ora_decode_vfmt.restype = I
@@ -67,7 +67,7 @@ def lib():
         L.ora_decode.argtypes = [I, I, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I64, P, I, I, P]
         L.ora_num_threads.restype = I
         L.ora_set_mutation.argtypes = [I]
-        L.ora_prefill_rows.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, P, I64, P, I]
+        L.ora_prefill_rows.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, P, I64, P, P, I]
         L.ora_prefill_trace.restype = I
         L.ora_prefill_trace.argtypes = [I, I, I, P, F, P, P, P, P, P, P, P, P, P, P, P, I, I, I, P, P, P, P, P, P, P]
         L.ora_decode_trace.restype = I
@@ -228,15 +228,20 @@ def prefill_codes(q_bits, k_bits, v_bits, bands, decode_cache: bool = False):
                 v16=v16, v8=v8, v4=v4, int4=int4, formats=formats, identity=identity)
 
 
-def prefill_attention(codes, bands, hq: int, hk: int, t: int, scale: float, threads: int = 0):
-    """fp32 output [Hq, T, 128] of the banded quantized attention (prefill_sm80.cu:259-488)."""
+def prefill_attention(codes, bands, hq: int, hk: int, t: int, scale: float, threads: int = 0, tol: bool = False):
+    """fp32 output [Hq, T, 128] of the banded quantized attention (prefill_sm80.cu:259-488).
+
+    With ``tol``, also the per-element bound of how far the output moves where a two-ulp change of a
+    per-score exp2 rounds a P level or an fp16 probability to its neighbour (the kernels' hardware
+    exp2, like the reference's ex2.approx, may land on either side): returns (out, tol)."""
     b = _c(bands, np.int32).reshape(hq, 2)
     out = np.empty((hq, t, D), np.float32)
+    bound = np.empty((hq, t, D), np.float32) if tol else None
     v8 = codes["v8"] if codes["v8"] is not None else np.zeros((1,), np.int8)
     lib().ora_prefill(hq, hk, t, _p(b), sm_log2(scale), _p(codes["q8"]), _p(codes["qa"]), _p(codes["q4"]),
                       _p(codes["qa4"]), _p(codes["k8"]), _p(codes["ka"]), _p(codes["k4"]), _p(codes["ka4"]),
-                      _p(codes["v16"]), _p(v8), _p(codes["vstat"]), _p(out), int(threads))
-    return out
+                      _p(codes["v16"]), _p(v8), _p(codes["vstat"]), _p(out), _p(bound), int(threads))
+    return (out, bound) if tol else out
 
 
 def _prefill_operands(codes, bands, hq, scale):
@@ -247,13 +252,15 @@ def _prefill_operands(codes, bands, hq, scale):
             _p(codes["vstat"])), (b, v8)
 
 
-def prefill_rows(codes, bands, hq: int, hk: int, t: int, scale: float, rows, threads: int = 0):
-    """Rows ``rows`` (flat q-head * t + token indices) of ``prefill_attention``'s output, [len(rows), 128]."""
+def prefill_rows(codes, bands, hq: int, hk: int, t: int, scale: float, rows, threads: int = 0, tol: bool = False):
+    """Rows ``rows`` (flat q-head * t + token indices) of ``prefill_attention``'s output, [len(rows), 128]
+    (with ``tol``: (out, tol) as for prefill_attention)."""
     rows = _c(rows, np.int64).reshape(-1)
     out = np.empty((rows.size, D), np.float32)
+    bound = np.empty((rows.size, D), np.float32) if tol else None
     args, keep = _prefill_operands(codes, bands, hq, scale)
-    lib().ora_prefill_rows(hq, hk, t, *args, _p(rows), rows.size, _p(out), int(threads))
-    return out
+    lib().ora_prefill_rows(hq, hk, t, *args, _p(rows), rows.size, _p(out), _p(bound), int(threads))
+    return (out, bound) if tol else out
 
 
 def prefill_trace(codes, bands, hq: int, hk: int, t: int, scale: float, qh: int, i: int):
@@ -275,14 +282,19 @@ def set_mutation(value: int) -> None:
 
 
 MUTATIONS = dict(no_margin=1, no_half=2, dither_byte=3, no_rel_margin=4, bq_levels=5, v4_restore=6, no_dither=7,
-                 slope_group=8, grown_mask=9, grown_state=10)
+                 slope_group=8, grown_mask=9, grown_state=10, exp_up=11, exp_down=12)
 
 
-def prefill(q_bits, k_bits, v_bits, bands, scale: float, decode_cache: bool = False, threads: int = 0):
-    """Whole Prefill call of one sequence: codes plus fp32 attention output."""
+def prefill(q_bits, k_bits, v_bits, bands, scale: float, decode_cache: bool = False, threads: int = 0,
+            tol: bool = False):
+    """Whole Prefill call of one sequence: codes plus fp32 attention output (with ``tol``: output,
+    codes and the exp2-rounding bound of prefill_attention)."""
     hq, t, _ = q_bits.shape
     hk = k_bits.shape[0]
     codes = prefill_codes(q_bits, k_bits, v_bits, bands, decode_cache)
+    if tol:
+        out, bound = prefill_attention(codes, bands, hq, hk, t, scale, threads, tol=True)
+        return out, codes, bound
     return prefill_attention(codes, bands, hq, hk, t, scale, threads), codes
 
 

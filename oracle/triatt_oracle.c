@@ -338,6 +338,8 @@ enum {
   MUT_SLOPE_GROUP = 8,   /* P-level arguments all use the first 16-key group's slope */
   MUT_GROWN_MASK = 9,    /* tiles taken from the tail masked like prompt tiles (keys past the prompt invalid) */
   MUT_GROWN_STATE = 10,  /* tiles taken from the tail classified against the prompt's tile count */
+  MUT_EXP_UP = 11,       /* prefill per-score exp2 two ulps up (a hardware exp2 on the other side) */
+  MUT_EXP_DOWN = 12,     /* the same, two ulps down */
 };
 static int g_mutation = MUT_NONE;
 void ora_set_mutation(int m) { g_mutation = m; }
@@ -390,7 +392,28 @@ typedef struct {
   const uint16_t* v16;
 } prefill_args;
 
-static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, ora_trace* tr) {
+/* exp2 results two ulps either side of e: the hardware exp2 of the kernels' per-score probabilities
+ * (v_exp_f32, within 1 ulp, like the reference's ex2.approx) and texp2 (0.952 ulp) may differ by that. */
+static void exp2_neighbours(float e, float* lo, float* hi) {
+  *lo = nextafterf(nextafterf(e, -INFINITY), -INFINITY);
+  *hi = nextafterf(nextafterf(e, INFINITY), INFINITY);
+  if (*lo < 0.f) *lo = 0.f;
+}
+
+/* The per-score exp2 of prefill: texp2, or under MUT_EXP_UP / MUT_EXP_DOWN its neighbour two ulps away. */
+static float score_exp2(float arg) {
+  const float e = ora_texp2(arg);
+  if (g_mutation != MUT_EXP_UP && g_mutation != MUT_EXP_DOWN) return e;
+  float lo, hi;
+  exp2_neighbours(e, &lo, &hi);
+  return g_mutation == MUT_EXP_UP ? hi : lo;
+}
+
+/* tol_row (may be NULL): per channel, how far the output can move when every probability that a
+ * two-ulp change of its exp2 would round to the next P level (quantized tiles) or fp16 value (F16
+ * tiles) takes that neighbour: the sum of those steps times |V'|, through the denominator as well,
+ * in output units.  Everywhere else the output is determined by the reference's operation sequence. */
+static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, ora_trace* tr, float* tol_row) {
   const int g = a->hq / a->hk, kh = qh / g, tiles = (a->t + BN - 1) / BN, qb = i / BN;
   const int64_t qrow = (int64_t)qh * a->t + i;
   int cols[4096], kind[4096];
@@ -407,7 +430,8 @@ static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, or
   float m = -FLT_MAX, denom = 0.f;
   double acc64[D];
   float out[D];
-  for (int c = 0; c < D; ++c) out[c] = 0.f;
+  double amb[D], amb_den = 0.0;  /* ambiguity bound of out and denom (tol_row) */
+  for (int c = 0; c < D; ++c) out[c] = 0.f, amb[c] = 0.0;
   int dot[BN], valid[BN];
   for (int e = 0; e < n; ++e) {
     const int col = cols[e], kd = kind[e];
@@ -441,6 +465,10 @@ static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, or
     const float alpha = ora_texp2(m - nmax);
     m = nmax;
     for (int c = 0; c < D; ++c) out[c] = out[c] * alpha;
+    if (tol_row) {
+      for (int c = 0; c < D; ++c) amb[c] *= alpha;
+      amb_den *= alpha;
+    }
     if (kd == 0) {
       /* fp16 P x fp16 V' (prefill_sm80.cu:358-383) */
       denom *= alpha;
@@ -449,8 +477,20 @@ static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, or
       for (int k = 0; k < BN; ++k) {
         const float x = valid[k] ? (float)dot[k] + MAGIC_F : -INFINITY;
         const float arg = fmaf(slope[k / 16], x, fmaf(-slope[k / 16], MAGIC_F, -m));
-        p16[k] = ora_f32_to_f16(ora_texp2(arg));
+        const float e = score_exp2(arg);
+        p16[k] = ora_f32_to_f16(e);
         pf[k] = ora_f16_to_f32(p16[k]);
+        if (tol_row) {
+          float lo, hi;
+          exp2_neighbours(e, &lo, &hi);
+          const double step = fmax(fabs((double)ora_f16_to_f32(ora_f32_to_f16(lo)) - pf[k]),
+                                   fabs((double)ora_f16_to_f32(ora_f32_to_f16(hi)) - pf[k]));
+          if (step > 0.0) {
+            const uint16_t* vr = a->v16 + (((int64_t)kh * tiles + col) * BN + k) * D;
+            amb_den += step;
+            for (int c = 0; c < D; ++c) amb[c] += step * fabs((double)ora_f16_to_f32(vr[c]));
+          }
+        }
       }
       if (tr) {
         int pb[BN];
@@ -483,8 +523,18 @@ static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, or
         float arg;
         if (four) arg = fmaf(sl, x, -base);
         else arg = fmaf(sl, x + MAGIC_F, fmaf(-sl, MAGIC_F, -base));
-        P[k] = p_level(ora_texp2(arg), 255.f, pmagic_half());
+        const float e = score_exp2(arg);
+        P[k] = p_level(e, 255.f, pmagic_half());
         rs += P[k];
+        if (tol_row) {
+          float lo, hi;
+          exp2_neighbours(e, &lo, &hi);
+          if (p_level(lo, 255.f, pmagic_half()) != P[k] || p_level(hi, 255.f, pmagic_half()) != P[k]) {
+            const int8_t* vr = a->v8 + (((int64_t)kh * tiles + col) * BN + k) * D;
+            amb_den += bq;
+            for (int c = 0; c < D; ++c) amb[c] += (double)bq * abs((int)vr[c]);
+          }
+        }
       }
       trace_tile(tr, col, kd, 0, m, base, bq, P);
       denom = fmaf((float)rs, bq, denom * alpha);
@@ -502,12 +552,22 @@ static void prefill_row(const prefill_args* a, int qh, int i, float* out_row, or
   const float* mean = a->vstat + (int64_t)kh * 3 * D;
   const float* scale = mean + D;
   for (int c = 0; c < D; ++c) out_row[c] = fmaf(out[c] * inv, scale[c], mean[c]);
+  if (tol_row) {
+    /* |d(o / l)| <= (|do| + |o / l| |dl|) / (l - |dl|), with 1% on top for the fp32 roundings */
+    const double den = (double)denom - amb_den;
+    for (int c = 0; c < D; ++c) {
+      const double o = (double)out[c] / (denom > 0.f ? (double)denom : 1.0);
+      tol_row[c] = amb_den == 0.0 ? 0.f
+                   : den > 0.0 ? (float)(1.01 * (amb[c] + fabs(o) * amb_den) / den * scale[c])
+                               : INFINITY;
+    }
+  }
 }
 
 void ora_prefill(int hq, int hk, int t, const int32_t* bands, float sm_log2, const int8_t* q8, const float* qa,
                  const uint8_t* q4, const float* qa4, const int8_t* k8, const float* ka, const int8_t* k4,
                  const float* ka4, const uint16_t* v16, const int8_t* v8, const float* vstat, float* out,
-                 int nthreads) {
+                 float* tol, int nthreads) {
   prefill_args a = {hq, hk, t, bands, sm_log2, q8, k8, k4, v8, q4, qa, ka, qa4, ka4, vstat, v16};
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -515,7 +575,7 @@ void ora_prefill(int hq, int hk, int t, const int32_t* bands, float sm_log2, con
 #endif
   for (int64_t r = 0; r < (int64_t)hq * t; ++r) {
     const int qh = (int)(r / t), i = (int)(r % t);
-    prefill_row(&a, qh, i, out + r * D, NULL);
+    prefill_row(&a, qh, i, out + r * D, NULL, tol ? tol + r * D : NULL);
   }
   (void)nthreads;
 }
@@ -525,13 +585,14 @@ void ora_prefill(int hq, int hk, int t, const int32_t* bands, float sm_log2, con
 void ora_prefill_rows(int hq, int hk, int t, const int32_t* bands, float sm_log2, const int8_t* q8, const float* qa,
                       const uint8_t* q4, const float* qa4, const int8_t* k8, const float* ka, const int8_t* k4,
                       const float* ka4, const uint16_t* v16, const int8_t* v8, const float* vstat,
-                      const int64_t* rows, int64_t nrows, float* out, int nthreads) {
+                      const int64_t* rows, int64_t nrows, float* out, float* tol, int nthreads) {
   prefill_args a = {hq, hk, t, bands, sm_log2, q8, k8, k4, v8, q4, qa, ka, qa4, ka4, vstat, v16};
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
 #pragma omp parallel for schedule(dynamic, 1)
 #endif
-  for (int64_t r = 0; r < nrows; ++r) prefill_row(&a, (int)(rows[r] / t), (int)(rows[r] % t), out + r * D, NULL);
+  for (int64_t r = 0; r < nrows; ++r)
+    prefill_row(&a, (int)(rows[r] / t), (int)(rows[r] % t), out + r * D, NULL, tol ? tol + r * D : NULL);
   (void)nthreads;
 }
 
@@ -545,7 +606,7 @@ int ora_prefill_trace(int hq, int hk, int t, const int32_t* bands, float sm_log2
                       float* out_row) {
   prefill_args a = {hq, hk, t, bands, sm_log2, q8, k8, k4, v8, q4, qa, ka, qa4, ka4, vstat, v16};
   ora_trace tr = {cap, 0, col, kind, NULL, m, base, bq, p};
-  prefill_row(&a, qh, i, out_row, &tr);
+  prefill_row(&a, qh, i, out_row, &tr, NULL);
   return tr.n;
 }
 

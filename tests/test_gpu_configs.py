@@ -208,9 +208,10 @@ def test_config2_full_sampled_rows(module):
         rows = [(h, i) for h in range(hq) for i in _sample_tokens(t, rng)]
         quant = [(h, i) for h, i in rows if h // g not in bf16_kv]
         exact = [(h, i) for h, i in rows if h // g in bf16_kv]
-        ref = O.prefill_rows(codes, c["bands"].numpy(), hq, hk, t, c["scale"], [h * t + i for h, i in quant])
+        ref, tol = O.prefill_rows(codes, c["bands"].numpy(), hq, hk, t, c["scale"], [h * t + i for h, i in quant],
+                                  tol=True)
         got = np.stack([out[b, h, i] for h, i in quant])
-        assert_close(got, ref, what=f"C2 sequence {b} quantized heads ({len(quant)} rows)")
+        assert_close(got, ref, what=f"C2 sequence {b} quantized heads ({len(quant)} rows)", tol=tol)
         r64, r32 = exact_rows(c["q"][b], c["k"][b], c["v"][b], exact, c["scale"])
         bar = max(2e-3, float(np.abs(r32 - r64).max()))
         got = np.stack([out[b, h, i] for h, i in exact])
@@ -276,8 +277,9 @@ def test_config4_full_shape_generation(module):
     quant = [(h, i) for h, i in rows if h // g not in exact_kv]
     exact = [(h, i) for h, i in rows if h // g in exact_kv]
     codes = O.prefill_codes(bits(q[0]), bits(k[0]), bits(v[0]), b, decode_cache=True)
-    ref = O.prefill_rows(codes, b, 28, 4, t, scale, [h * t + i for h, i in quant])
-    assert_close_bf16(np.stack([out[0, h, i].numpy() for h, i in quant]), ref, what=f"C4 layer {layer} prefill")
+    ref, tol = O.prefill_rows(codes, b, 28, 4, t, scale, [h * t + i for h, i in quant], tol=True)
+    assert_close_bf16(np.stack([out[0, h, i].numpy() for h, i in quant]), ref, what=f"C4 layer {layer} prefill",
+                      tol=tol)
     r64, r32 = exact_rows(q[0], k[0], v[0], exact, scale)
     bar = max(2e-3, float(np.abs(r32 - r64).max()))
     assert_close_bf16(np.stack([out[0, h, i].numpy() for h, i in exact]), r64, max_abs=bar,

@@ -161,3 +161,32 @@ def test_planted_decode_mistake_fails_the_pin(planted, name):
     planted(O.MUTATIONS[name])
     with pytest.raises(TW.Mismatch):
         pin_decode(3, 2)
+
+
+@pytest.mark.parametrize("seed,t", [(91, 700), (92, 333), (93, 129)])
+def test_exp2_rounding_bound_covers_both_neighbours(seed, t):
+    """The per-element bound the GPU prefill comparisons add to 2e-3: where a two-ulp change of a
+    per-score exp2 rounds a P level or an fp16 probability to its neighbour, the output may move by at
+    most ``tol``.  Pinned by moving every per-score exp2 two ulps up, then down (planted in the
+    oracle): each run stays within tol of the unmoved output, and the bound is tight where it is
+    not zero (some element moves by more than half its bound)."""
+    hq, hk = 8, 2
+    q, k, v = _inputs(seed, hq, hk, t)
+    bands = np.array([[INF, INF], [1, INF], [2, 5], [1, 1], [3, INF], [1, 2], [INF, INF], [2, 2]], np.int32)
+    out, codes, tol = O.prefill(bits(q), bits(k), bits(v), bands, SCALE, tol=True)
+    assert np.isfinite(tol).all() and (tol >= 0).all()
+    assert (tol > 0).any(), "the case should hold ambiguous probabilities"
+    assert (tol == 0).mean() > 0.5, "most outputs are determined exactly"
+    ratio = 0.0
+    for name in ("exp_up", "exp_down"):
+        O.set_mutation(O.MUTATIONS[name])
+        try:
+            moved = O.prefill_attention(codes, bands, hq, hk, t, SCALE)
+        finally:
+            O.set_mutation(0)
+        diff = np.abs(moved.astype(np.float64) - out)
+        slack = 1e-6 * (1.0 + np.abs(out))  # fp32 roundings of the unmoved terms
+        assert (diff <= tol + slack).all(), f"{name}: max excess {(diff - tol - slack).max():.3e}"
+        assert (diff[tol == 0] <= slack[tol == 0]).all()
+        ratio = max(ratio, float((diff[tol > 0] / tol[tol > 0]).max()))
+    assert ratio > 0.5, f"bound not tight: largest move {ratio:.2f} of it"

@@ -239,7 +239,8 @@ __device__ __forceinline__ void xor32_pair(uint32_t v, uint32_t& lo, uint32_t& h
 }
 // Maxima of values that arithmetic produced (never a signaling NaN): the hardware max as is.  fmaxf
 // would first canonicalize each operand that the compiler cannot trace to arithmetic (one more VALU
-// operation per operand after a lane exchange or an LDS read); the results are the same.
+// operation per operand after a lane exchange or an LDS read); the results are the same.  Not for MFMA
+// results: the compiler does not pad an inline-asm read of an accumulator for the MFMA's latency.
 __device__ __forceinline__ float max_arith(float a, float b) {
   float r;
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));

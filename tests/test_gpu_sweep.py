@@ -12,6 +12,8 @@ quantized heads against the oracle, exact heads against float64 attention.
 Bar: as in test_gpu_parity (fp32 outputs within 2e-3 max-abs, 1e-3 mean-abs of the oracle)."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -26,10 +28,12 @@ from triattention_amd.synthetic import INF, bits
 
 pytestmark = pytest.mark.gpu
 
-CASES = 40
-RAGGED_CASES = 12
-GROWTH_CASES = 8
-EXACT_CASES = 12
+# TRI_SWEEP_SCALE=n runs n times as many cases of each kind (the extra cases draw new seeds)
+SCALE = max(1, int(os.environ.get("TRI_SWEEP_SCALE", "1")))
+CASES = 40 * SCALE
+RAGGED_CASES = 12 * SCALE
+GROWTH_CASES = 8 * SCALE
+EXACT_CASES = 12 * SCALE
 
 
 def draw(i):

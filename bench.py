@@ -116,6 +116,8 @@ def copy_probe():
 STREAM_SHAPES = ((1024, 1, 1), (1024, 1, 2), (1024, 1, 3), (2048, 1, 2), (2048, 2, 2), (4096, 4, 1), (4096, 4, 2),
                  (8192, 4, 2))
 STREAM_SHAPES_DEFAULT = ((1024, 1, 3), (2048, 2, 2), (4096, 4, 2), (8192, 4, 2))
+# more waves, for launches of many more bytes (used where every wave gets at least two records per slot)
+STREAM_SHAPES_LARGE = ((16384, 4, 2), (32768, 4, 2))
 
 
 def stream_ceiling(module, dev, nbytes, layers, shapes, reps=5, verbose=False):
@@ -153,7 +155,9 @@ def stream_ceiling(module, dev, nbytes, layers, shapes, reps=5, verbose=False):
 
 
 def read_ceiling(args):
-    """--read-ceiling: the streaming-read probe over every shape, at the C1 decode launch's bytes."""
+    """--read-ceiling: the streaming-read probe over every shape, at the C1 decode launch's bytes, or
+    at each byte count of --ceiling-bytes (the buffers rotate over at least 4.8 GB, so every launch
+    reads HBM rather than the 256 MB Infinity Cache)."""
     import torch
     from triattention_amd.kernels.extension import load_extension
     module = load_extension()
@@ -165,10 +169,15 @@ def read_ceiling(args):
         mat = (mat @ mat).clamp_(-1.0, 1.0)
         torch.cuda.synchronize()
     del mat
-    us, gbs, shape = stream_ceiling(module, dev, C1_RECORD_BYTES, args.layers, STREAM_SHAPES, verbose=True)
-    print(json.dumps({"stream_ceiling": {"bytes": C1_RECORD_BYTES, "buffers": args.layers, "us": round(us, 2),
-                                         "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                                         "shape": list(shape)}}), flush=True)
+    sizes = [int(x) for x in args.ceiling_bytes.split(",")] if args.ceiling_bytes else [C1_RECORD_BYTES]
+    for nbytes in sizes:
+        buffers = args.layers if nbytes == C1_RECORD_BYTES else max(2, -(-4_800_000_000 // nbytes))
+        shapes = STREAM_SHAPES + tuple(s for s in STREAM_SHAPES_LARGE if nbytes >= s[0] * 2 * 8192 * s[2])
+        print(f"== {nbytes} B per launch, {buffers} buffers", flush=True)
+        us, gbs, shape = stream_ceiling(module, dev, nbytes, buffers, shapes, verbose=True)
+        print(json.dumps({"stream_ceiling": {"bytes": nbytes, "buffers": buffers, "us": round(us, 2),
+                                             "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                             "shape": list(shape)}}), flush=True)
 
 
 def graph_steps(run_token, tokens, stream):
@@ -535,6 +544,8 @@ def main():
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time the streaming-read probe over every launch shape at the C1 launch's bytes instead")
+    ap.add_argument("--ceiling-bytes", default="",
+                    help="with --read-ceiling: comma-separated byte counts per launch (default: the C1 launch's)")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--layers", type=int, default=28, help="C1 layers (own caches, one decode op each per token)")
     ap.add_argument("--c2-kinds", default="", help="with --only c2: also time the C2 inputs with every KV head of "

@@ -130,3 +130,46 @@ def test_all_exact_bands_fn():
     fn = M._AllExact(4)
     assert fn.bf16(7) == [0, 1, 2, 3]
     assert fn(0, 12).shape == (12, 2)
+
+
+def _save_local_checkpoint(tmp_path, model_type="qwen2"):
+    """A tiny bf16 checkpoint plus a word-level tokenizer with a chat template, saved to a directory."""
+    from tokenizers import Tokenizer, models, pre_tokenizers
+
+    model = tiny_qwen2(layers=1)
+    model.generation_config.eos_token_id = [3, 5]
+    model.to(torch.bfloat16).save_pretrained(tmp_path)
+    vocab = {w: i for i, w in enumerate(["<unk>", "<s>", "hello", "</s>", "world", "<|im_end|>"])}
+    raw = Tokenizer(models.WordLevel(vocab, unk_token="<unk>"))
+    raw.pre_tokenizer = pre_tokenizers.Whitespace()
+    tok = transformers.PreTrainedTokenizerFast(tokenizer_object=raw, unk_token="<unk>", bos_token="<s>",
+                                               eos_token="</s>")
+    tok.chat_template = ("{% for m in messages %}<{{ m.role }}> {{ m.content }} {% endfor %}"
+                         "{% if add_generation_prompt %}<assistant> {{ date_string }}{% endif %}")
+    tok.save_pretrained(tmp_path)
+    return model
+
+
+def test_loaders_read_a_local_checkpoint(tmp_path):
+    saved = _save_local_checkpoint(tmp_path)
+    tok = M.load_tokenizer(tmp_path)
+    model = M.load_model(tmp_path, device="cpu")
+    assert model.dtype == torch.bfloat16 and not model.training
+    # qwen2 checkpoints get the reference's YaRN long-context RoPE (models.py:23-27)
+    rope = model.config.rope_parameters
+    assert rope["rope_type"] == "yarn" and rope["factor"] == 4.0
+    assert rope["original_max_position_embeddings"] == 32768 and rope["rope_theta"] == 1e6
+    assert model.config.max_position_embeddings == 4 * 32768
+    for a, b in zip(saved.state_dict().values(), model.state_dict().values()):
+        assert torch.equal(a, b)
+    assert M.render_prompt(tok, "hello world") == "<user> hello world <assistant> 30 Jul 2026"
+    # the tokenizer's end id (3) and the generation config's list [3, 5]
+    assert M.eos_ids(tok, model) == {3, 5}
+
+
+def test_loaders_refuse_anything_but_a_local_directory(tmp_path):
+    for name in ("Qwen/Qwen2-7B-Instruct", tmp_path / "missing"):
+        with pytest.raises(FileNotFoundError, match="not a local model directory"):
+            M.load_model(name, device="cpu")
+        with pytest.raises(FileNotFoundError, match="not a local model directory"):
+            M.load_tokenizer(name)

@@ -23,11 +23,17 @@ reference's tail is max_new_tokens long, and its kernels cap it at 1024), the
 decode cache grows, taking the oldest 64 tail tokens into a new quantized tile
 whenever the tail is full.
 
-Loading checkpoints and tokenizers, chat templates and end-of-sequence ids
-(models.py:16-42) are the caller's: any HF causal LM whose attention modules
-call the registered attention function can be handed to ``TriAttention``.
+Checkpoint and tokenizer loading, the chat prompt and end-of-sequence ids
+(``load_tokenizer``, ``load_model``, ``render_prompt``, ``eos_ids``;
+models.py:16-42) behave as the reference's, with one policy of this build:
+they read local directories only (``local_files_only``) and refuse anything
+else with a clear error, so a model name never turns into a download.  Any HF
+causal LM whose attention modules call the registered attention function can
+be handed to ``TriAttention``, however it was loaded.
 """
 from __future__ import annotations
+
+import os
 
 import torch
 
@@ -35,6 +41,69 @@ from .kernels.decode import DecodeCache
 from .kernels.extension import load_extension
 from .kernels.prefill import Prefill
 from .maps import INF, load_map, preset
+
+
+def _local_dir(path):
+    """``path`` as a local checkpoint directory; anything else (a hub model name) is refused."""
+    path = os.fspath(path)
+    if not os.path.isdir(path):
+        raise FileNotFoundError(f"{path!r} is not a local model directory (this build never downloads a model "
+                                f"or tokenizer; pass the path of a saved checkpoint)")
+    return path
+
+
+def load_tokenizer(path):
+    """The checkpoint's tokenizer (models.py:16-18).  Mistral-3 checkpoints load with
+    ``fix_mistral_regex``, as the reference asks of them."""
+    from transformers import AutoConfig, AutoTokenizer
+
+    path = _local_dir(path)
+    kind = AutoConfig.from_pretrained(path, local_files_only=True).model_type
+    extra = {"fix_mistral_regex": True} if kind == "mistral3" else {}
+    return AutoTokenizer.from_pretrained(path, local_files_only=True, **extra)
+
+
+def _long_context(config):
+    """Qwen2 checkpoints run with YaRN RoPE scaling, 4x their 32,768-token window (models.py:23-27)."""
+    if config.model_type != "qwen2":
+        return config
+    config.rope_parameters = {"rope_type": "yarn", "factor": 4.0, "original_max_position_embeddings": 32768,
+                              "rope_theta": config.rope_parameters["rope_theta"]}
+    config.max_position_embeddings = 32768 * 4
+    return config
+
+
+def load_model(path, device="cuda"):
+    """A bf16 checkpoint in eval mode on ``device`` (models.py:21-31): causal LMs through
+    ``AutoModelForCausalLM``, checkpoints with a vision tower through ``AutoModelForImageTextToText``.
+    Extension: ``device`` (the reference always moves the model to the current GPU)."""
+    import transformers
+
+    path = _local_dir(path)
+    config = _long_context(transformers.AutoConfig.from_pretrained(path, local_files_only=True))
+    auto = (transformers.AutoModelForImageTextToText if getattr(config, "vision_config", None) is not None
+            else transformers.AutoModelForCausalLM)
+    model = auto.from_pretrained(path, config=config, dtype=torch.bfloat16, local_files_only=True)
+    return model.to(device).eval()
+
+
+def render_prompt(tokenizer, prompt):
+    """One user turn through the tokenizer's chat template, ready for the assistant's reply, with the
+    reference's fixed date string (models.py:34-36)."""
+    messages = [{"role": "user", "content": prompt}]
+    return tokenizer.apply_chat_template(messages, tokenize=False, add_generation_prompt=True,
+                                         date_string="30 Jul 2026")
+
+
+def eos_ids(tokenizer, model):
+    """Every id that ends generation: the tokenizer's end-of-sequence id(s) together with the model's
+    generation config's (models.py:39-41)."""
+    found = set()
+    for ids in (tokenizer.eos_token_id, model.generation_config.eos_token_id):
+        if ids is None:
+            continue
+        found.update(ids if isinstance(ids, (list, tuple, set)) else [ids])
+    return found
 
 
 class _AllExact:

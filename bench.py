@@ -8,7 +8,8 @@ token per sequence.  ``value`` = algorithmic HBM bytes of the step / step time
 resident in HBM; one token runs the decode op of each of the 28 layers of
 Llama-3.2-3B, every layer with its own cache, so the records stream from HBM
 rather than from the 256 MB Infinity Cache.  Also
-reported: tokens/s, the decode kernel's roofline
+reported: model tokens/s (batch over one token of all 28 layers' decode ops;
+the per-op rate is named layer_op_tokens_per_s), the decode kernel's roofline
 (HIP events that the kernel's own launch records, inside the timed region), the CPU oracle timed
 on a bounded sample, prefill attention TOPS on configs[0] and configs[2] (C0, C2),
 and the ragged decode of configs[3] (C3).
@@ -21,7 +22,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-pref
 
 ``roofline.traffic`` is the decode kernel's HBM bytes per launch measured with
 those counters; it is read from profiles/decode_kernel_C1_traffic.md, which
-holds the commands and the raw counter values (null when that file is absent).
+holds the commands, the raw counter values and the hash of the kernel sources
+they were taken on (null, with a note, when that file is absent or the hash
+differs from the sources here).
 """
 from __future__ import annotations
 
@@ -74,18 +77,46 @@ def decode_record_bytes(cache_entry):
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_kernel_C1_traffic.md"
 COPY_PROBE_BYTES = 256 << 20
+# Ministral-8B, whose shape configs[3] names, has 36 decoder layers
+C3_LAYERS = 36
 # record bytes (K/V records and K group scales) one C1 decode launch reads: 16,384 kept tiles
 C1_RECORD_BYTES = 170_655_744
 
 
+# the sources the split-KV decode kernel is compiled from: a counter summary taken on other sources
+# no longer describes the kernel that runs
+TRAFFIC_SOURCES = (ROOT / "triattention_amd" / "csrc" / "decode.hip", ROOT / "triattention_amd" / "csrc" / "common.h")
+
+
+def decode_source_hash():
+    """First 16 hex digits of the SHA-256 of the decode kernel's sources (decode.hip, then common.h)."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in TRAFFIC_SOURCES:
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
-    """HBM bytes per decode_kernel launch from the committed counter summary, or None."""
+    """(HBM bytes per decode_kernel launch, note) from the committed counter summary.  The bytes are
+    None when the summary is missing or was taken on other kernel sources than the ones built here
+    (its kernel_source_sha16 line against decode_source_hash()), so a stale counter is never
+    reported as current."""
     if not TRAFFIC_PROFILE.exists():
-        return None
+        return None, "no counter summary"
+    fields = {}
     for line in TRAFFIC_PROFILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1].strip())
-    return None
+        if ":" in line and line.split(":", 1)[0] in ("traffic_bytes_per_launch", "kernel_source_sha16"):
+            key, val = line.split(":", 1)
+            fields[key] = val.strip()
+    here = decode_source_hash()
+    if fields.get("kernel_source_sha16") != here:
+        return None, (f"counter summary taken on decode kernel sources {fields.get('kernel_source_sha16')}, "
+                      f"these are {here}: not reported")
+    if "traffic_bytes_per_launch" not in fields:
+        return None, "no traffic line in the counter summary"
+    return int(fields["traffic_bytes_per_launch"]), (f"FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated, "
+                                                     f"{TRAFFIC_PROFILE.name} (kernel sources {here})")
 
 
 def kernel_events(n, stream):
@@ -284,7 +315,11 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
             "split_kernel_us": round(dec_ms * 1e3, 2),
             "split_kernel_gbs": round(rec_bytes / (dec_ms * 1e-3) / 1e9, 2),
             "frac_hbm_peak": round(rec_bytes / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "tokens_per_s": round(batch / (ms * 1e-3), 1)}
+            "layer_op_tokens_per_s": round(batch / (ms * 1e-3), 1),
+            "model_tokens_per_s": {"value": round(batch / (C3_LAYERS * graph_ms * 1e-3), 1), "layers": C3_LAYERS,
+                                   "what": f"batch / ({C3_LAYERS} x the replayed one-layer step): the attention "
+                                           "part of a Ministral-8B decode step, every layer taken as costly as "
+                                           "the one measured (extrapolated from one layer)"}}
 
 
 def c4_config():
@@ -531,7 +566,8 @@ def prefill_case(module, dev, stream, name, cfg, reps, Prefill, from_bands, full
             "algorithmic_ops": ops_alg, "int8_tops": round(tops, 2),
             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "mixed_bound_us": round(mixed_us, 2), "frac_mixed_bound": round(mixed_us / (att_ms * 1e3), 4),
-            "tokens_per_s": round(b * t / (full_ms * 1e-3), 1) if full_call else None}
+            # prompt tokens through ONE layer's Prefill call per second (not a model's prefill rate)
+            "layer_call_prompt_tokens_per_s": round(b * t / (full_ms * 1e-3), 1) if full_call else None}
 
 
 def main():
@@ -702,6 +738,7 @@ def main():
     log(f"streaming-read ceiling for {rec_bytes} B: {ceil_us:.1f} us ({ceil_gbs:.0f} GB/s); the split-KV kernel "
         f"runs at {achieved / ceil_gbs:.3f} of it")
 
+    traffic, traffic_note = measured_traffic()
     result = {
         "metric": "prefill int8 TOPS (% MFMA peak); decode KV GB/s (% HBM peak); tokens/s",
         "value": round(value, 2),
@@ -723,11 +760,15 @@ def main():
         "config": {"workload": "C1 decode: batch 32, Hq 24 / Hk 8, head_dim 128, prompt 4096 in the quantized "
                                "cache, 25% INT8 / 75% INT4 KV heads, one bf16 token per sequence",
                    "global_batch": batch, "seq_len": prompt, "parallelism": "single GPU"},
-        "tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
+        # one decode op serves every sequence's next token for ONE layer; a model token needs all layers
+        "layer_op_tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
+        "model_tokens_per_s": {"value": round(batch / (ms_per_step * layers * 1e-3), 1), "layers": layers,
+                               "what": f"batch / (one token of all {layers} layers' decode ops in the replayed "
+                                       "graph): the attention part of a Llama-3.2-3B decode step, measured"},
         "step_bytes": int(step_bytes),
         "roofline": {"bound": "hbm", "kernel": "decode_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(), "algorithmic_bytes": rec_bytes,
+                     "traffic": traffic, "traffic_note": traffic_note, "algorithmic_bytes": rec_bytes,
                      "avg_us": round(dec_ms * 1e3, 2), "working_set_bytes": layers * rec_bytes},
         "stream_ceiling": {"achieved": round(ceil_gbs, 1), "us": round(ceil_us, 2),
                            "frac": round(ceil_gbs / HBM_PEAK_GBS, 4), "kernel_frac_of_ceiling":
@@ -766,7 +807,7 @@ def main():
             "value": round(step_bytes / cpu_step / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"the C oracle's decode of all {batch} sequences at step 0 (the whole C1 step, no "
                       f"extrapolation), one sequence per task on {threads} threads, median of 3",
-            "ms_per_step": round(cpu_step * 1e3, 2), "tokens_per_s": round(batch / cpu_step, 2),
+            "ms_per_step": round(cpu_step * 1e3, 2), "layer_op_tokens_per_s": round(batch / cpu_step, 2),
             "host_cpu_count": os.cpu_count()}
         result["parity_spot_check"] = {"sequences": batch, "max_abs_vs_oracle_bf16": max(errs)}
 
@@ -789,7 +830,7 @@ def main():
                 times.append(time.perf_counter() - t0)
             cpu_ms = statistics.median(times) * 1e3
             result.setdefault("cpu_baseline", {})["prefill_C0"] = {
-                "ms_per_call": round(cpu_ms, 2), "tokens_per_s": round(1024 / (cpu_ms * 1e-3), 1),
+                "ms_per_call": round(cpu_ms, 2), "layer_call_prompt_tokens_per_s": round(1024 / (cpu_ms * 1e-3), 1),
                 "int8_tops": round(r0["algorithmic_ops"] / (cpu_ms * 1e-3) / 1e12, 4), "threads": threads,
                 "gpu_speedup_full_call": round(cpu_ms * 1e3 / r0["prefill_call_us"], 1)}
             log(f"CPU oracle C0 prefill: {cpu_ms:.1f} ms per call ({threads} threads)")

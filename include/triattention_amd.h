@@ -222,8 +222,11 @@ int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int h
  * the process ends) instead of caller buffers; every other argument as for tri_decode, and the
  * same kernels.  Calls whose batch x hq x splits partials do not fit (more than 48,395) are rejected
  * with an error.  No memory is allocated or freed.  Every call on one GPU shares that GPU's scratch
- * (each call writes every partial it reads), so calls that overlap on one GPU, e.g. on two streams,
- * race. */
+ * (each call writes every partial it reads).  Calls on one stream are ordered by the stream; a call
+ * on another stream while the last call's work is still pending is refused with an error (the library
+ * records an event after each call; it creates that event, with the scratch address, at its first call
+ * on a device).  A call made under stream capture is not checked: replays of a graph that holds it
+ * must not overlap calls on other streams. */
 int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c, const float* ka,
                        const float* ka4, const int32_t* entry, const int32_t* kinfo, const int32_t* count,
                        const int32_t* fmt, const int32_t* slot, const void* v8c, const void* v4c, const float* vstat,

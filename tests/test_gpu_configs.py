@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close, assert_close_bf16, compare_codes, run_prefill
+from helpers import assert_close, assert_close_bf16, compare_codes, run_prefill, sample_tokens
 from triattention_amd import synthetic as S
 from triattention_amd.kernels.decode import DecodeCache
 from triattention_amd.kernels.prefill import Prefill
@@ -182,11 +182,6 @@ def test_ragged_decode_shared_prefill_equal_tile_counts(module):
         cache.advance()
 
 
-def _sample_tokens(t, rng, extra=4):
-    fixed = [0, 1, 63, 64, 65, t // 2 - 1, t // 2, t - 1]
-    return sorted(set([i for i in fixed if 0 <= i < t] + rng.integers(0, t, extra).tolist()))
-
-
 def test_config2_full_sampled_rows(module):
     """C2 (B4, Hq 28 / Hk 4, T 8192, log-uniform channel scales, KV heads INT8 / INT4 / bf16): every code,
     scale and record of every sequence bit-exact; sampled rows of every q-head (first and last tiles, the
@@ -205,7 +200,7 @@ def test_config2_full_sampled_rows(module):
         print(f"[parity] C2 sequence {b}: codes and sampled rows", flush=True)
         codes = O.prefill_codes(bits(c["q"][b]), bits(c["k"][b]), bits(c["v"][b]), c["bands"].numpy())
         compare_codes(ops, codes, b, batch, hq, hk, t)
-        rows = [(h, i) for h in range(hq) for i in _sample_tokens(t, rng)]
+        rows = [(h, i) for h in range(hq) for i in sample_tokens(t, rng)]
         quant = [(h, i) for h, i in rows if h // g not in bf16_kv]
         exact = [(h, i) for h, i in rows if h // g in bf16_kv]
         ref, tol = O.prefill_rows(codes, c["bands"].numpy(), hq, hk, t, c["scale"], [h * t + i for h, i in quant],
@@ -273,7 +268,7 @@ def test_config4_full_shape_generation(module):
     exact_kv = bf16[str(layer)]
     g = 7
     rng = np.random.default_rng(1404)
-    rows = [(h, i) for h in range(28) for i in _sample_tokens(t, rng, extra=2)]
+    rows = [(h, i) for h in range(28) for i in sample_tokens(t, rng, extra=2)]
     quant = [(h, i) for h, i in rows if h // g not in exact_kv]
     exact = [(h, i) for h, i in rows if h // g in exact_kv]
     codes = O.prefill_codes(bits(q[0]), bits(k[0]), bits(v[0]), b, decode_cache=True)

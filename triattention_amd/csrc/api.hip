@@ -309,6 +309,7 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   if (d.tasks && (n_tasks < 1 || !aligned(tasks, 16))) return fail("decode: a task table needs n_tasks >= 1, 16-byte aligned");
   d.tiles_max = tiles_max;
   d.splits = splits;
+  d.total = (int64_t)splits * hk * batch;
   {
     // Work scatter (workgroup lin takes item lin * scatter mod launched; the XCD is lin % 8).
     // - Affine (launched = items, scatter a prime not dividing it): with items % 8 == 0 the XCD fixes
@@ -419,22 +420,35 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
 constexpr int64_t NOALLOC_FLOATS = (int64_t)24 << 18;  // 24 MiB of fp32
 static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
 
-static int noalloc_scratch(float** out) {
-  static std::mutex mu;
-  static float* ptrs[64] = {};
+// Per device: the scratch address, and the stream and completion event of the last call that used the
+// scratch.  A call on another stream while that event is pending would overwrite partials the earlier
+// call's kernels still read, so it is refused; calls on one stream are ordered by the stream itself.
+struct NoallocDevice {
+  float* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t stream = nullptr;
+  bool used = false;
+};
+static std::mutex g_noalloc_mu;
+static NoallocDevice g_noalloc[64];
+
+// Set-up on the first call on a device (that device current): the scratch array's address and one event.
+static int noalloc_device(NoallocDevice** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail("decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
   if (dev < 0 || dev >= 64) return fail("decode_noalloc: device %d beyond the 64 this library tracks", dev);
-  std::lock_guard<std::mutex> lock(mu);
-  if (ptrs[dev] == nullptr) {
+  NoallocDevice& d = g_noalloc[dev];
+  if (d.ptr == nullptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
       return fail("decode_noalloc: hipGetSymbolAddress of the scratch array: %s", hipGetErrorString(e));
-    ptrs[dev] = static_cast<float*>(p);
+    e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+    if (e != hipSuccess) return fail("decode_noalloc: hipEventCreateWithFlags: %s", hipGetErrorString(e));
+    d.ptr = static_cast<float*>(p);
   }
-  *out = ptrs[dev];
+  *out = &d;
   return 0;
 }
 
@@ -487,18 +501,40 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
                 "scratch (at most %lld); use tri_decode with caller buffers",
                 (long long)n, batch, hq, (long long)splits, (long long)NOALLOC_FLOATS, (long long)most);
   }
-  float* s = nullptr;
-  if (noalloc_scratch(&s) != 0) return 1;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  NoallocDevice* nd = nullptr;
+  if (noalloc_device(&nd) != 0) return 1;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  // (under stream capture nothing runs now, and querying or recording events is not allowed: a captured
+  // call is not checked, and the caller keeps graph replays off other streams' calls)
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(hs, &cap);
+  if (e != hipSuccess) return fail("decode_noalloc: hipStreamIsCapturing: %s", hipGetErrorString(e));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  if (!capturing && nd->used && nd->stream != hs) {
+    e = hipEventQuery(nd->done);
+    if (e == hipErrorNotReady)
+      return fail("decode_noalloc: this GPU's scratch is still in use by a call on another stream; wait for that "
+                  "stream (or call on it) before calling on this one");
+    if (e != hipSuccess) return fail("decode_noalloc: hipEventQuery: %s", hipGetErrorString(e));
+  }
+  float* s = nd->ptr;
   float* pm = s;
   float* pl = s + pad;
   float* po = s + 2 * pad;
   if (tasks && xslot == nullptr) {
     // splits a task table leaves out are never written: the scratch (which holds whatever the last
     // call left) gets the empty partial in every slot first
-    tri::fill_empty_partials_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
-        pm, pl, po, n);
+    tri::fill_empty_partials_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, hs>>>(pm, pl, po, n);
   }
-  return decode_impl(TRI_DECODE_ARGS, 3);
+  const int rc = decode_impl(TRI_DECODE_ARGS, 3);
+  if (rc == 0 && !capturing) {
+    e = hipEventRecord(nd->done, hs);
+    if (e != hipSuccess) return fail("decode_noalloc: hipEventRecord: %s", hipGetErrorString(e));
+    nd->stream = hs;
+    nd->used = true;
+  }
+  return rc;
 }
 
 int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
@@ -531,6 +567,7 @@ int tri_decode_tasks(const float* ka, const float* ka4, const int32_t* entry, co
   d.tiles_max = tiles_max;
   d.bounds = bounds;
   d.splits = splits;
+  d.total = all;
   tri::decode_tasks_kernel<<<dim3((unsigned)listed), 64, 0, static_cast<hipStream_t>(stream)>>>(d, items, tasks);
   return check_launch("decode_tasks");
 }

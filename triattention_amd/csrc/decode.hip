@@ -52,6 +52,7 @@ struct DecodeArgs {
   // item lin * scatter mod launched (a permutation), and the one padding item (>= items) exits
   int64_t scatter;
   int items, launched;
+  int64_t total;  // work items of the cache layout: splits x hk x batch (a task row naming another is padding)
   // split partition (extension): null for the reference's uniform split of `per` tiles, else
   // [B][Hk][splits + 1] entry bounds, split s of a head covering entries [bounds[s], bounds[s + 1])
   const int32_t* bounds;
@@ -106,6 +107,14 @@ constexpr int TASK_WORDS = 512;
 __global__ __launch_bounds__(64) void decode_tasks_kernel(DecodeArgs a, const int32_t* items, int32_t* tasks) {
   const int L = threadIdx.x;
   const int item = items ? items[blockIdx.x] : (int)blockIdx.x;
+  int32_t* t = tasks + (int64_t)blockIdx.x * TASK_WORDS;
+  if (item < 0 || item >= a.total) {
+    // an item outside the layout: an empty row (no entry, no record) whose work item -1 marks it as
+    // padding for the split kernel
+    *reinterpret_cast<int4*>(t + 4 * L) = make_int4(NO_RECORD, NO_RECORD, 1 << 9, L == 0 ? -1 : 0);
+    *reinterpret_cast<float4*>(t + 256 + 4 * L) = make_float4(1.f, 1.f, 1.f, 1.f);
+    return;
+  }
   const int split = item % a.splits, kh = (item / a.splits) % a.hk, b = item / (a.splits * a.hk);
   const int64_t hb = (int64_t)b * a.hk + kh;
   int first, last;
@@ -124,7 +133,6 @@ __global__ __launch_bounds__(64) void decode_tasks_kernel(DecodeArgs a, const in
     w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
     ks = *reinterpret_cast<const float4*>(((is4 && a.ka4) ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
   }
-  int32_t* t = tasks + (int64_t)blockIdx.x * TASK_WORDS;
   *reinterpret_cast<int4*>(t + 4 * L) = w;
   *reinterpret_cast<float4*>(t + 256 + 4 * L) = ks;
 }
@@ -304,8 +312,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
       task_w = *reinterpret_cast<const int4*>(t + 4 * (threadIdx.x & 63));
       task_k = *reinterpret_cast<const float4*>(t + 256 + 4 * (threadIdx.x & 63));
       item = __builtin_amdgcn_readlane(task_w.w, 0);
+      // (a row naming no work item of this layout -- the builder's padding row, or a stale or foreign
+      // table -- is padding too; the entry count is clamped to one wave's metadata)
+      if (item < 0 || item >= a.total) return;
       first = 0;
-      last = __builtin_amdgcn_readlane(task_w.w, 1);
+      last = min(max(__builtin_amdgcn_readlane(task_w.w, 1), 0), MAX_PER);
     }
     const int nsplit = a.splits, nkh = a.hk;
     split = item % nsplit;

@@ -119,6 +119,15 @@ def measured_traffic():
                                                      f"{TRAFFIC_PROFILE.name} (kernel sources {here})")
 
 
+MERGE_FORM = "auto"  # --merge-form: "four" keeps the four-wave merge for every tail
+
+
+def short_merge(cache, layer):
+    """Whether the decode op of ``layer`` merges with the one-wave form (the cache's choice by tail length,
+    unless --merge-form four)."""
+    return MERGE_FORM == "auto" and cache.short_tail(layer)
+
+
 def kernel_events(n, stream):
     """n (start, stop) HIP event pairs for the split-KV kernel: the launch records them as the kernel's
     own start and stop (hipExtLaunchKernel through tri_decode_partials_timed), so the timed loop holds
@@ -286,7 +295,7 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
     for i in range(steps):
         qd, kd, vd = toks[warmup + i]
         plan.run(qd, kd, vd, out, 1, events=evs[i])
-        plan.run(qd, kd, vd, out, 2)
+        plan.run(qd, kd, vd, out, 2, short_tail=short_merge(cache, 0))
         cache.advance()
     end.record(stream)
     torch.cuda.synchronize()
@@ -295,7 +304,7 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
 
     def token():
         qd, kd, vd = toks[warmup]
-        plan.run(qd, kd, vd, out)
+        plan.run(qd, kd, vd, out, short_tail=short_merge(cache, 0))
         cache.advance()
     graph_ms = graph_steps(token, steps, stream)
     ms = eager_ms
@@ -582,6 +591,9 @@ def main():
                     help="time the streaming-read probe over every launch shape at the C1 launch's bytes instead")
     ap.add_argument("--ceiling-bytes", default="",
                     help="with --read-ceiling: comma-separated byte counts per launch (default: the C1 launch's)")
+    ap.add_argument("--merge-form", choices=("auto", "four"), default="auto",
+                    help="decode merge: the one-wave form while the tail holds at most 64 tokens (auto), or "
+                         "the four-wave form always")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--layers", type=int, default=28, help="C1 layers (own caches, one decode op each per token)")
     ap.add_argument("--c2-kinds", default="", help="with --only c2: also time the C2 inputs with every KV head of "
@@ -594,6 +606,8 @@ def main():
     ap.add_argument("--c4", action="store_true", help="run the C4 end-to-end generation instead")
     ap.add_argument("--calibrate", action="store_true", help="time the calibration sweep's Prefill executors instead")
     args = ap.parse_args()
+    global MERGE_FORM
+    MERGE_FORM = args.merge_form
     if args.copy_probe:
         copy_probe()
         return
@@ -674,11 +688,12 @@ def main():
         # counter advances once per token, after the last layer
         qd, kd, vd = toks[i % total_steps]
         plan = plans[i % layers]
+        short = short_merge(cache, i % layers)
         if ev is None:
-            plan.run(qd, kd, vd, out)
+            plan.run(qd, kd, vd, out, short_tail=short)
         else:
             plan.run(qd, kd, vd, out, 1, events=ev)
-            plan.run(qd, kd, vd, out, 2)
+            plan.run(qd, kd, vd, out, 2, short_tail=short)
         if i % layers == layers - 1:
             cache.advance()
 
@@ -700,6 +715,7 @@ def main():
         torch.cuda.synchronize()
     # C1 is one token after the prompt: restart the step counter (the bf16 tail length)
     cache.step.fill_(1)
+    cache.host_step = 1
     log(f"warmup {args.warmup} steps")
     for i in range(1, 1 + args.warmup):
         step(i)
@@ -720,7 +736,8 @@ def main():
     # advance) captured as a HIP graph and replayed; ms_per_step is per decode op (per layer).
     def token():
         for layer in range(layers):
-            plans[layer].run(*toks[(1 + args.warmup + layer) % total_steps], out)
+            plans[layer].run(*toks[(1 + args.warmup + layer) % total_steps], out,
+                             short_tail=short_merge(cache, layer))
         cache.advance()
     tokens = max(4, -(-args.steps // layers))
     ms_per_step = graph_steps(token, tokens, stream) / layers
@@ -752,6 +769,8 @@ def main():
                        "each -- then the step advance) captured as a HIP graph and replayed, as the model path "
                        "runs decode; ms_per_step is per decode op; eager_ms_per_step launches each kernel from "
                        "Python",
+        "merge": ("one wave per (sequence, q-head): the tail holds at most 64 tokens" if MERGE_FORM == "auto"
+                  else "four waves per (sequence, q-head) (--merge-form four)"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

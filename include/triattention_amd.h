@@ -159,6 +159,36 @@ int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c,
                      const void* vxc, int64_t n_kx, const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, const int64_t* tail_base, double scale,
                      void* stream);
 
+/* tri_decode and tri_decode_merge with the merge run as one wave per (sequence, q-head) instead of
+ * four: no reference counterpart.  Every load of the first 64 tail tokens and 16 splits is issued at
+ * once and no workgroup barrier is needed, so it is the faster merge while the tail (the step minus
+ * the tokens moved into the cache) holds at most 64 tokens; any tail length gives a correct result,
+ * longer ones more slowly than tri_decode's merge.  Its arithmetic follows the reference's merge order
+ * (common_device.cuh:373-469) exactly: tail scores as 32-lane butterfly sums, split sums in four
+ * interleaved groups, tail tokens one after another.  Same arguments as tri_decode. */
+int tri_decode_short_tail(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c,
+                          const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
+                          const int32_t* count, const int32_t* fmt, const int32_t* slot, const void* v8c,
+                          const void* v4c, const float* vstat, const float* kstat, void* ktail, void* vtail,
+                          int64_t t_sb, int64_t t_sh, int64_t t_st, int max_tail, const void* kcur, const void* vcur,
+                          int64_t c_sb, int64_t c_sh, const int64_t* step, void* out, int out_dtype, int64_t o_sb,
+                          int64_t o_sh, float* pm, float* pl, float* po, const int32_t* prompt, int batch, int hq,
+                          int hk, int maxn, int per, int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8,
+                          int64_t n_v4, const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
+                          const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, const int64_t* tail_base,
+                          double scale, void* stream);
+int tri_decode_merge_short_tail(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c,
+                          const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
+                          const int32_t* count, const int32_t* fmt, const int32_t* slot, const void* v8c,
+                          const void* v4c, const float* vstat, const float* kstat, void* ktail, void* vtail,
+                          int64_t t_sb, int64_t t_sh, int64_t t_st, int max_tail, const void* kcur, const void* vcur,
+                          int64_t c_sb, int64_t c_sh, const int64_t* step, void* out, int out_dtype, int64_t o_sb,
+                          int64_t o_sh, float* pm, float* pl, float* po, const int32_t* prompt, int batch, int hq,
+                          int hk, int maxn, int per, int tiles_max, int64_t n_k8, int64_t n_k4, int64_t n_v8,
+                          int64_t n_v4, const int32_t* xslot, const void* kxc, const void* vxc, int64_t n_kx,
+                          const int32_t* bounds, int nsplit, const void* tasks, int n_tasks, const int64_t* tail_base,
+                          double scale, void* stream);
+
 /* Measurement (no reference counterpart): tri_decode_partials with the split-KV
  * kernel launched through hipExtLaunchKernel, which records the two hipEvent_t
  * handles (either may be null) as the kernel's own start and stop, so that a

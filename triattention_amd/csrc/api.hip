@@ -409,7 +409,11 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
       }
     }
   }
-  if (phase & 2) tri::decode_merge_kernel<<<dim3(hq, batch), 256, 0, s>>>(mg);
+  if (phase & 2) {
+    // phase bit 4: the merge as one wave per (sequence, q-head), for short tails
+    if (phase & 4) tri::decode_merge1_kernel<<<dim3(hq, batch), 64, 0, s>>>(mg);
+    else tri::decode_merge_kernel<<<dim3(hq, batch), 256, 0, s>>>(mg);
+  }
   return check_launch("decode");
 }
 
@@ -471,6 +475,8 @@ static int noalloc_device(NoallocDevice** out) {
 int tri_decode(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3); }
 int tri_decode_partials(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 1); }
 int tri_decode_merge(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 2); }
+int tri_decode_short_tail(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 3 | 4); }
+int tri_decode_merge_short_tail(TRI_DECODE_PARAMS) { return decode_impl(TRI_DECODE_ARGS, 2 | 4); }
 int tri_decode_partials_timed(TRI_DECODE_PARAMS, void* ev_start, void* ev_stop) {
   return decode_impl(TRI_DECODE_ARGS, 1, static_cast<hipEvent_t>(ev_start), static_cast<hipEvent_t>(ev_stop));
 }

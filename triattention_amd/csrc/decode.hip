@@ -1038,3 +1038,187 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
 }
 
 }  // namespace tri
+
+namespace tri {
+
+// The merge as ONE wave per (sequence, q-head), for short tails: every load that does not depend on
+// another is issued first -- the first 32 tail tokens' K rows, the first 16 tokens' V rows and the
+// first 16 splits' partials -- so a short tail costs one memory round trip, no workgroup barrier is
+// needed, and the work grows with the tail (longer tails and more splits continue in loops and stay
+// exact, only slower than decode_merge_kernel).  The arithmetic follows the reference's merge order
+// exactly (common_device.cuh:373-469): a tail score is the 32-lane butterfly sum of fma chains over 4
+// channels each, here laid out on 8 lanes per token (lane j holds the chains of channels 16j..16j+15,
+// the butterfly's xor-16, 8 and 4 stages are DPP exchanges between lanes j ^ 4, 2, 1 and its xor-2
+// and 1 stages add in registers); the split sums run in four interleaved groups (splits w, w + 4, ...)
+// added in group order; the tail tokens are then added one after another.  XCD-aware (sequence,
+// q-head) mapping as decode_merge_kernel.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_merge1_kernel(MergeArgs a) {
+  __shared__ float ts[MAX_TAIL];  // tail scores
+  int hq, b;
+  {
+    const int total = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int q8 = total >> 3, r8 = total & 7, x = lin & 7;
+    const int w = x * q8 + min(x, r8) + (lin >> 3);
+    hq = w % gridDim.x;
+    b = w / gridDim.x;
+  }
+  const int g = a.hq / a.hk, kh = hq / g;
+  const int L = threadIdx.x;
+  const int64_t held = *a.step - (a.tail_base != nullptr ? *a.tail_base : 0);
+  const int prior = (int)max((int64_t)0, min((int64_t)a.max_tail - 1, held)), tail = prior + 1;
+  const int64_t hb = (int64_t)b * a.hk + kh;
+  const float* vmean = a.vstat + hb * 3 * D;
+  const float* vscale = vmean + D;
+  const uint16_t* kc = a.kcur + b * a.csb + kh * a.csh;
+  const uint16_t* vc = a.vcur + b * a.csb + kh * a.csh;
+  const uint16_t* kt = a.ktail + b * a.tsb + kh * a.tsh;
+  const uint16_t* vt = a.vtail + b * a.tsb + kh * a.tsh;
+  const int64_t pbase = ((int64_t)b * a.hq + hq) * a.splits;
+  const int splits = a.splits;
+  // score layout: token 8u + (L >> 3) in pass u, lane j = L & 7 channels 16j..16j+15; value layout:
+  // channels 2L, 2L + 1
+  const int tg = L >> 3, c16 = (L & 7) * 16, c2 = 2 * L;
+  // ---- loads issued up front
+  float qv[16], mu[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    qv[i] = bf16f(a.q[b * a.qsb + hq * a.qsh + c16 + i]);
+    mu[i] = a.kstat[hb * 3 * D + c16 + i];
+  }
+  auto krow = [&](int t, uint4 (&raw)[2]) {
+    const int tt = min(t, tail - 1);
+    const uint16_t* row = (tt < prior ? kt + (int64_t)tt * a.tst : kc) + c16;
+    raw[0] = *reinterpret_cast<const uint4*>(row);
+    raw[1] = *reinterpret_cast<const uint4*>(row + 8);
+  };
+  auto vrow = [&](int t) {
+    const int tt = min(t, tail - 1);
+    return *reinterpret_cast<const uint32_t*>((tt < prior ? vt + (int64_t)tt * a.tst : vc) + c2);
+  };
+  const int npass = (tail + 7) >> 3;
+  uint4 kraw[4][2];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (u < npass) krow(8 * u + tg, kraw[u]);
+  uint32_t vraw[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t)
+    if (t < tail) vraw[t] = vrow(t);
+  const float pms = L < splits ? a.pm[pbase + L] : -3.402823466e38f;
+  const float pls = L < splits ? a.pl[pbase + L] : 0.f;
+  float2 pov[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u)
+    if (u < splits) pov[u] = *reinterpret_cast<const float2*>(a.po + (pbase + u) * D + c2);
+  const float2 vmv = *reinterpret_cast<const float2*>(vmean + c2), vsv = *reinterpret_cast<const float2*>(vscale + c2);
+  if (hq % g == 0) {
+    *reinterpret_cast<uint32_t*>(a.ktail + b * a.tsb + kh * a.tsh + prior * a.tst + c2) =
+        *reinterpret_cast<const uint32_t*>(kc + c2);
+    *reinterpret_cast<uint32_t*>(a.vtail + b * a.tsb + kh * a.tsh + prior * a.tst + c2) =
+        *reinterpret_cast<const uint32_t*>(vc + c2);
+  }
+  // ---- tail scores q . (k - kmean) * sm_log2 (the reference's 32-lane butterfly, see above)
+  auto score = [&](const uint4 (&raw)[2], int t) {
+    const uint32_t w[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int ch = 4 * i + c;
+        const float kx = bf16f((uint16_t)(w[ch >> 1] >> (16 * (ch & 1))));
+        p[i] = __builtin_fmaf(qv[ch], kx - mu[ch], p[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] += lane_xor8<4>(p[i]);  // butterfly stage 16
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] += lane_xor8<2>(p[i]);  // stage 8
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] += lane_xor8<1>(p[i]);  // stage 4
+    const float s = (p[0] + p[2]) + (p[1] + p[3]);          // stages 2 and 1
+    if ((L & 7) == 0 && t < tail) ts[t] = s * a.sm_log2;
+  };
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (u < npass) score(kraw[u], 8 * u + tg);
+  for (int u = 4; u < npass; ++u) {
+    uint4 raw[2];
+    krow(8 * u + tg, raw);
+    score(raw, 8 * u + tg);
+  }
+  __syncthreads();
+  // ---- reference max over the splits and the tail
+  float m = pms;
+  for (int sp = 64 + L; sp < splits; sp += 64) m = fmaxf(m, a.pm[pbase + sp]);
+  for (int t = L; t < tail; t += 64) m = fmaxf(m, ts[t]);
+  m = wave_max(m);
+  // ---- split sums: group w holds splits w, w + 4, ... in order; the groups are added in order
+  auto split_m = [&](int sp) {
+    return sp < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pms), sp)) : a.pm[pbase + sp];
+  };
+  auto split_l = [&](int sp) {
+    return sp < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pls), sp)) : a.pl[pbase + sp];
+  };
+  float total = 0.f, acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float wl = 0.f, wo0 = 0.f, wo1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int sp = w + 4 * k;
+      if (sp < splits) {
+        const float wt = texp2(split_m(sp) - m);
+        wl = __builtin_fmaf(split_l(sp), wt, wl);
+        wo0 = __builtin_fmaf(pov[sp].x, wt, wo0);
+        wo1 = __builtin_fmaf(pov[sp].y, wt, wo1);
+      }
+    }
+    for (int sp = w + 16; sp < splits; sp += 4) {
+      const float wt = texp2(split_m(sp) - m);
+      wl = __builtin_fmaf(split_l(sp), wt, wl);
+      const float2 p = *reinterpret_cast<const float2*>(a.po + (pbase + sp) * D + c2);
+      wo0 = __builtin_fmaf(p.x, wt, wo0);
+      wo1 = __builtin_fmaf(p.y, wt, wo1);
+    }
+    total += wl;
+    acc0 += wo0;
+    acc1 += wo1;
+  }
+  acc0 = __builtin_fmaf(acc0, vsv.x, total * vmv.x);
+  acc1 = __builtin_fmaf(acc1, vsv.y, total * vmv.y);
+  // ---- tail values, one token after another (lane t holds token t's weight for t < 64)
+  const float e_own = L < tail ? texp2(ts[L] - m) : 0.f;
+  auto add = [&](float e, uint32_t raw) {
+    total += e;
+    acc0 = __builtin_fmaf(e, bf16f((uint16_t)(raw & 0xffffu)), acc0);
+    acc1 = __builtin_fmaf(e, bf16f((uint16_t)(raw >> 16)), acc1);
+  };
+  auto weight = [&](int t) {
+    return t < 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e_own), t)) : texp2(ts[t] - m);
+  };
+#pragma unroll
+  for (int t = 0; t < 16; ++t)
+    if (t < tail) add(weight(t), vraw[t]);
+  for (int t0 = 16; t0 < tail; t0 += 16) {
+    uint32_t raw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) raw[i] = vrow(t0 + i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (t0 + i < tail) add(weight(t0 + i), raw[i]);
+  }
+  const float r0 = acc0 / total, r1 = acc1 / total;
+  // (element stores: the output rows carry no alignment contract)
+  const int64_t o = b * a.osb + hq * a.osh + c2;
+  if (a.out_dtype == 0) {
+    static_cast<float*>(a.out)[o] = r0;
+    static_cast<float*>(a.out)[o + 1] = r1;
+  } else {
+    static_cast<uint16_t*>(a.out)[o] = f32_to_bf16(r0);
+    static_cast<uint16_t*>(a.out)[o + 1] = f32_to_bf16(r1);
+  }
+}
+
+}  // namespace tri

@@ -275,6 +275,7 @@ class DecodeCache:
         self._called = set()
         self.capturing = False
         self._capture_set = set()
+        self._capture_forms = {}
 
     def codes(self, rows):
         if rows not in self.formats:
@@ -453,26 +454,44 @@ class DecodeCache:
     def __call__(self, layer, q, k, v, scale):
         e = self._grow_step(layer)
         st = e["store"]
-        hq = q.shape[1]
-        splits = e["splits"]
-        key = ("partials", hq)
-        if key not in e:
-            # every slot starts as the empty partial: splits that hold no kept tile are left out of the
-            # launch (the task table lists the others) and keep it
-            n = e["batch"] * hq * splits
-            e[key] = (torch.full((n,), -3.4028234663852886e38, device=q.device), torch.zeros(n, device=q.device),
-                      torch.zeros(n * 128, device=q.device))
         dtype = self.out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=dtype, device=q.device)
         plan = self.plan(layer, q, k, out, scale)
         if st.grow_tiles:
             self._spill_plan(e).run()
-        plan.run(q, k, v, out)
+        short = self.short_tail(layer)
+        if self.capturing:
+            self._capture_forms[layer] = short
+        plan.run(q, k, v, out, short_tail=short)
         return out
+
+    # the merge runs as one wave per (sequence, q-head) while the tail holds at most this many tokens
+    SHORT_TAIL = 64
+
+    def tail_tokens(self, layer):
+        """Tokens the merge of ``layer``'s next decode step reads from its tail (host mirror): the
+        step's own token and those before it, past the tokens moved into the cache (after this step's
+        spill, if it finds the tail full with room left), at most max_tail."""
+        st = self.layers[layer]["store"]
+        tb = st.tb if st.grow_tiles else 0
+        if st.grow_tiles and self.host_step - tb >= self.max_tail and tb // BN < st.grow_tiles:
+            tb += BN
+        return min(self.max_tail - 1, max(0, self.host_step - tb)) + 1
+
+    def short_tail(self, layer):
+        """Whether ``layer``'s next merge takes the one-wave form (tail_tokens at most SHORT_TAIL)."""
+        return self.tail_tokens(layer) <= self.SHORT_TAIL
 
     def plan(self, layer, q, k, out, scale):
         """The layer's validated decode call for q / k (and v) / out of these shapes (built once, then reused)."""
         e = self.layers[layer]
+        key = ("partials", q.shape[1])
+        if key not in e:
+            # every slot starts as the empty partial: splits that hold no kept tile are left out of the
+            # launch (the task table lists the others) and keep it
+            n = e["batch"] * q.shape[1] * e["splits"]
+            e[key] = (torch.full((n,), -3.4028234663852886e38, device=q.device), torch.zeros(n, device=q.device),
+                      torch.zeros(n * 128, device=q.device))
         key = ("plan", _geometry(q), _geometry(k), _geometry(out), float(scale))
         if key not in e:
             hq = q.shape[1]
@@ -643,16 +662,22 @@ class DecodeCache:
     def begin_capture(self):
         self.capturing = True
         self._capture_set = set()
+        self._capture_forms = {}
 
     def end_capture(self):
         self.capturing = False
 
     def graph_ready(self) -> bool:
         """Whether a captured step can replay now: no captured layer finds its tail full with its room
-        used up (that step must run eagerly, which grows the room, and the step be captured again)."""
+        used up (that step must run eagerly, which grows the room, and the step be captured again), and
+        every captured layer's merge form still fits its tail (else the step is captured again with the
+        other form; the captured one would still be correct, only slower)."""
         for layer in self._capture_set:
             st = self.layers[layer]["store"]
             if st.grow_tiles and self.host_step - st.tb >= self.max_tail and st.tb // BN >= st.grow_tiles:
+                return False
+        for layer, short in self._capture_forms.items():
+            if self.short_tail(layer) != short:
                 return False
         return True
 

@@ -37,7 +37,8 @@ STAT_BLOCKS = 64
 K8_WORDS, K4_WORDS, V16_WORDS, V8_WORDS, V4_WORDS = 2048, 1024, 4096, 2048, 1024
 
 EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "tri_pack_exact", "tri_decode",
-           "tri_decode_partials", "tri_decode_merge", "tri_decode_partials_timed", "tri_decode_noalloc",
+           "tri_decode_partials", "tri_decode_merge", "tri_decode_short_tail", "tri_decode_merge_short_tail",
+           "tri_decode_partials_timed", "tri_decode_noalloc",
            "tri_decode_tasks", "tri_cache_store", "tri_tail_spill", "tri_decode_occupancy", "tri_device_cus",
            "tri_stream_read")
 KX_BYTES = 16384
@@ -67,7 +68,8 @@ def load_library() -> ctypes.CDLL:
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64,
                    P, P, P, I64, P, I, P, I, P, D_, P]
-    for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge"):
+    for name in ("tri_decode", "tri_decode_partials", "tri_decode_merge", "tri_decode_short_tail",
+                 "tri_decode_merge_short_tail"):
         getattr(lib, name).argtypes = decode_args
     lib.tri_decode_partials_timed.argtypes = decode_args + [P, P]
     # tri_decode without pm / pl / po (arguments 31-33 of tri_decode)
@@ -497,12 +499,16 @@ class DecodePlan:
         self.module, self.args, self.keep = module, args, keep
         self.qgeom, self.cgeom, self.ogeom = _geometry(q), _geometry(kcur), _geometry(out)
         self.device = q.device
-        self.fns = {3: module.lib.tri_decode, 1: module.lib.tri_decode_partials, 2: module.lib.tri_decode_merge}
+        lib = module.lib
+        self.fns = {3: lib.tri_decode, 1: lib.tri_decode_partials, 2: lib.tri_decode_merge}
+        self.short_fns = {3: lib.tri_decode_short_tail, 1: lib.tri_decode_partials, 2: lib.tri_decode_merge_short_tail}
 
-    def run(self, q, kcur, vcur, out, phase=3, events=None):
+    def run(self, q, kcur, vcur, out, phase=3, events=None, short_tail=False):
         """Launch ``phase`` (3: both kernels, 1: the split-KV kernel, 2: the merge).  ``events`` (phase 1
         only): a pair of recorded torch.cuda.Event objects that the split-KV kernel's launch records as
-        its own start and stop (``tri_decode_partials_timed``)."""
+        its own start and stop (``tri_decode_partials_timed``).  ``short_tail``: the merge as one wave
+        per (sequence, q-head), the faster form while the tail holds at most 64 tokens (any tail gives a
+        correct result)."""
         if _geometry(q) != self.qgeom or _geometry(kcur) != self.cgeom or _geometry(vcur) != self.cgeom or \
                 _geometry(out) != self.ogeom:
             raise RuntimeError("decode plan: q / k / v / out differ in shape, strides, dtype or device from the plan")
@@ -510,7 +516,7 @@ class DecodePlan:
         a[self.Q], a[self.KC], a[self.VC], a[self.OUT] = q.data_ptr(), kcur.data_ptr(), vcur.data_ptr(), out.data_ptr()
         index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         a[self.STREAM] = torch.cuda.current_stream(index).cuda_stream
-        fn, extra = self.fns[phase], ()
+        fn, extra = (self.short_fns if short_tail else self.fns)[phase], ()
         if events is not None:
             if phase != 1:
                 raise RuntimeError("decode plan: events time the split-KV kernel (phase 1) only")

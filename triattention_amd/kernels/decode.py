@@ -275,7 +275,6 @@ class DecodeCache:
         self._called = set()
         self.capturing = False
         self._capture_set = set()
-        self._capture_forms = {}
 
     def codes(self, rows):
         if rows not in self.formats:
@@ -459,10 +458,7 @@ class DecodeCache:
         plan = self.plan(layer, q, k, out, scale)
         if st.grow_tiles:
             self._spill_plan(e).run()
-        short = self.short_tail(layer)
-        if self.capturing:
-            self._capture_forms[layer] = short
-        plan.run(q, k, v, out, short_tail=short)
+        plan.run(q, k, v, out, short_tail=self.short_tail(layer))
         return out
 
     # the merge runs as one wave per (sequence, q-head) while the tail holds at most this many tokens
@@ -479,7 +475,12 @@ class DecodeCache:
         return min(self.max_tail - 1, max(0, self.host_step - tb)) + 1
 
     def short_tail(self, layer):
-        """Whether ``layer``'s next merge takes the one-wave form (tail_tokens at most SHORT_TAIL)."""
+        """Whether ``layer``'s next merge takes the one-wave form: tail_tokens at most SHORT_TAIL.  A step
+        being captured is replayed at later steps, with longer tails, so it takes the one-wave form only
+        if no tail can outgrow SHORT_TAIL (max_tail at most SHORT_TAIL); either form is correct for any
+        tail, the other one only slower."""
+        if self.capturing:
+            return self.max_tail <= self.SHORT_TAIL
         return self.tail_tokens(layer) <= self.SHORT_TAIL
 
     def plan(self, layer, q, k, out, scale):
@@ -662,22 +663,16 @@ class DecodeCache:
     def begin_capture(self):
         self.capturing = True
         self._capture_set = set()
-        self._capture_forms = {}
 
     def end_capture(self):
         self.capturing = False
 
     def graph_ready(self) -> bool:
         """Whether a captured step can replay now: no captured layer finds its tail full with its room
-        used up (that step must run eagerly, which grows the room, and the step be captured again), and
-        every captured layer's merge form still fits its tail (else the step is captured again with the
-        other form; the captured one would still be correct, only slower)."""
+        used up (that step must run eagerly, which grows the room, and the step be captured again)."""
         for layer in self._capture_set:
             st = self.layers[layer]["store"]
             if st.grow_tiles and self.host_step - st.tb >= self.max_tail and st.tb // BN >= st.grow_tiles:
-                return False
-        for layer, short in self._capture_forms.items():
-            if self.short_tail(layer) != short:
                 return False
         return True
 

@@ -535,7 +535,7 @@ def prefill_case(module, dev, stream, name, cfg, reps, Prefill, from_bands, full
     def attn():
         module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
                          ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], outp,
-                         cfg["scale"], exact=exact, q=q0, kx=kx, vx=vx, nx=nx, v8sum=ops["v8sum"])
+                         cfg["scale"], exact=exact, q=q0, kx=kx, vx=vx, nx=nx, v8sum=ops["v8sum"], k4x=ops["k4x"])
 
     # untimed calls until ~0.5 s of this workload has run: the clocks rise under sustained
     # load (C2's first calls are ~17% slower than its tenth)

@@ -34,11 +34,13 @@ const char* tri_last_error(void);
  * [batch][hk][tiles], ka f32 [batch][hk][tiles][4], partial f32 scratch
  * [batch][hk][64][3][128], kstat f32 [batch][hk][3][128] (mean, scale, 1/scale).
  * q4/qa4/k4p/ka4 are all NULL or all set: q4 u8 [batch][hq][t][64] (low nibble =
- * even feature), qa4 f32 [batch][hq][t], k4p K4 records, ka4 f32 [batch][hk][tiles][4]. */
+ * even feature), qa4 f32 [batch][hq][t], k4p K4 records, ka4 f32 [batch][hk][tiles][4].
+ * Extension: k4x (NULL, or with the INT4 buffers) receives the K4 records once more, each code
+ * expanded to a byte of 16 * code in the K8 record layout (8 KiB per tile), for tri_attention's k4x. */
 int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
                    int64_t k_sh, int64_t k_st, int batch, int hq, int hk, int t, void* q8, float* qa, void* kp,
                    float* ka, float* partial, float* kstat, void* q4, float* qa4, void* k4p, float* ka4,
-                   void* stream);
+                   void* k4x, void* stream);
 
 /* Replaces pack_v (common_host.cuh:27-45).
  * v: bf16 [batch][hk][t][128]; vstat f32 [batch][hk][3][128].  Statistics are
@@ -66,13 +68,16 @@ int tri_pack_v(const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int batc
  * accumulation (extension for maps that keep some heads unquantized).
  * v8sum (extension): NULL, or what tri_pack_v wrote for these V8 records; the
  * P V product of each INT8/INT4 tile then starts from it instead of computing
- * it with two MFMAs per 32 channels (the same integers either way). */
+ * it with two MFMAs per 32 channels (the same integers either way).
+ * k4x (extension): NULL, or what tri_prepare_qk wrote as k4x for these K4
+ * records; INT4 key tiles then read those bytes instead of expanding the packed
+ * nibbles in every tile (the same integers either way). */
 int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int batch, int hq, int hk, int t,
                   const void* v16p, const void* v8p, const float* vstat, const void* q8, const void* k8p,
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
                   double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
-                  const void* kx, const void* vx, int nx, const int32_t* v8sum, void* stream);
+                  const void* kx, const void* vx, int nx, const int32_t* v8sum, const void* k4x, void* stream);
 
 /* No counterpart in the reference: the bf16 records of the exact heads that
  * tri_attention reads (extension).  k/v bf16 [batch][hk][t][128] with element

@@ -28,7 +28,7 @@ def test_library_exports_header_symbols():
 
 def test_validation_errors_need_no_gpu():
     lib = load_library()
-    rc = lib.tri_prepare_qk(*([None] + [0] * 3 + [None] + [0] * 3 + [1, 1, 1, 1] + [None] * 11))
+    rc = lib.tri_prepare_qk(*([None] + [0] * 3 + [None] + [0] * 3 + [1, 1, 1, 1] + [None] * 12))
     assert rc != 0 and b"null buffer" in lib.tri_last_error()
     blocks = None
     assert lib.tri_decode_occupancy(blocks) != 0 and b"null output" in lib.tri_last_error()
@@ -45,14 +45,21 @@ def test_exact_head_validation_needs_no_gpu():
     assert rc != 0 and b"16-byte aligned" in lib.tri_last_error()
     # attention with exact heads but no records
     rc = lib.tri_attention(fake, 4, fake, 1, 4, 2, 64, fake, fake, fake, fake, fake, fake, fake, None, None, None, None,
-                           fake, 0, 0, 0, 0, 0.125, fake, fake, 0, 0, 0, fake, fake, 0, None, None)
+                           fake, 0, 0, 0, 0, 0.125, fake, fake, 0, 0, 0, fake, fake, 0, None, None, None)
     assert rc != 0 and b"KX/VX records" in lib.tri_last_error()
     # V8 sums without the V8 records they sum (pack_v and attention)
     rc = lib.tri_pack_v(fake, 0, 0, 128, 1, 2, 64, fake, fake, fake, None, None, fake, None)
     assert rc != 0 and b"V8 sums need the V8 records" in lib.tri_last_error()
     rc = lib.tri_attention(fake, 4, fake, 1, 4, 2, 64, fake, None, fake, fake, fake, fake, fake, None, None, None, None,
-                           fake, 0, 0, 0, 0, 0.125, None, None, 0, 0, 0, None, None, 0, fake, None)
+                           fake, 0, 0, 0, 0, 0.125, None, None, 0, 0, 0, None, None, 0, fake, None, None)
     assert rc != 0 and b"V8 sums need the V8 records" in lib.tri_last_error()
+    # expanded K4 records without the INT4 operands (prepare_qk and attention)
+    rc = lib.tri_prepare_qk(fake, 0, 0, 128, fake, 0, 0, 128, 1, 2, 2, 64, fake, fake, fake, fake, fake, fake,
+                            None, None, None, None, fake, None)
+    assert rc != 0 and b"expanded K4 records need the INT4 buffers" in lib.tri_last_error()
+    rc = lib.tri_attention(fake, 4, fake, 1, 4, 2, 64, fake, fake, fake, fake, fake, fake, fake, None, None, None, None,
+                           fake, 0, 0, 0, 0, 0.125, None, None, 0, 0, 0, None, None, 0, None, fake, None)
+    assert rc != 0 and b"expanded K4 records need the INT4 operands" in lib.tri_last_error()
 
 
 def _decode_args(fake, per=8, kcur=None, tst=128):

@@ -14,6 +14,7 @@ import torch
 import oracle as O
 from helpers import assert_close, compare_codes, exact_max_abs_bar, exact_reference, oracle_prefill, run_prefill
 from triattention_amd import synthetic as S
+from triattention_amd.kernels import records as R
 from triattention_amd.kernels.decode import DecodeCache
 from triattention_amd.kernels.prefill import Prefill
 from triattention_amd.maps import from_bands
@@ -419,21 +420,30 @@ def test_exact_bf16_heads_in_the_same_launch(module, t, bf16_kv):
 
 def test_attention_with_and_without_v8_sums(module):
     """The P V products of INT8/INT4 tiles start from pack_v's -127 * sum(V8) (the Prefill path) or from
-    two MFMAs against a constant operand (the reference-shaped call without sums): the same integers, so
-    the outputs are bit-identical, and both match the oracle."""
-    print("\n[parity] attention with and without V8 sums", flush=True)
+    two MFMAs against a constant operand (the reference-shaped call without sums), and INT4 key tiles read
+    prepare_qk's expanded K4 records (the Prefill path) or expand the packed ones: the same integers, so
+    the outputs of all four forms are bit-identical, and they match the oracle.  The expanded records
+    are 16 times the K4 codes in the K8 layout, bit for bit."""
+    print("\n[parity] attention with and without V8 sums and expanded K4 records", flush=True)
     q, k, v = small(3500, 2, 8, 2, 777)
     bands = torch.tensor([[INF, INF], [1, INF], [2, 5], [1, 1], [3, INF], [1, 2], [INF, INF], [2, 2]],
                          dtype=torch.int32)
     out, ops, pre = run_prefill(module, q, k, v, bands, 128 ** -0.5)
-    assert ops["v8sum"] is not None
+    assert ops["v8sum"] is not None and ops["k4x"] is not None
+    # the expanded records: K4 codes in the K8 layout, as bytes of 16 * code
+    k4 = R.unpack_k4(ops["k4"].cpu().numpy())
+    k4x = R.unpack_k8(ops["k4x"].cpu().numpy())
+    assert k4.shape == k4x.shape == (2 * 2 * 13, 64, 128)
+    np.testing.assert_array_equal(k4x.astype(np.int32), 16 * k4.astype(np.int32))
     table = next(iter(pre.tables.values()))
     pk = ops["packed"]
-    plain = torch.empty_like(out).cuda()
-    module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"], ops["kp"],
-                     ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], plain, 128 ** -0.5)
-    torch.cuda.synchronize()
-    assert torch.equal(out, plain.cpu())
+    for sums, wide in ((None, None), (ops["v8sum"], None), (None, ops["k4x"])):
+        plain = torch.empty_like(out).cuda()
+        module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
+                         ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], plain,
+                         128 ** -0.5, v8sum=sums, k4x=wide)
+        torch.cuda.synchronize()
+        assert torch.equal(out, plain.cpu()), (sums is not None, wide is not None)
     ref, _, tol = oracle_prefill(q, k, v, bands, 128 ** -0.5)
     assert_close(out.numpy(), ref, what="prefill with V8 sums", tol=tol)
 

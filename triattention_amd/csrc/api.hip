@@ -88,7 +88,7 @@ const char* tri_last_error(void) { return g_error.c_str(); }
 int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
                    int64_t k_sh, int64_t k_st, int batch, int hq, int hk, int t, void* q8, float* qa, void* kp,
                    float* ka, float* partial, float* kstat, void* q4, float* qa4, void* k4p, float* ka4,
-                   void* stream) {
+                   void* k4x, void* stream) {
   g_error.clear();
   if (!q || !k || !q8 || !qa || !kp || !ka || !partial || !kstat) return fail("prepare_qk: null buffer");
   if (batch < 1 || hq < 1 || hk < 1 || t < 1) return fail("prepare_qk: empty shape");
@@ -100,6 +100,7 @@ int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, cons
     return fail("prepare_qk: Q/K rows must be 8-byte aligned");
   if (!aligned(kp, 16) || !aligned(q8, 16) || (int4 && (!aligned(k4p, 16) || !aligned(q4, 4))))
     return fail("prepare_qk: output buffers must be 16-byte aligned");
+  if (k4x && (!int4 || !aligned(k4x, 16))) return fail("prepare_qk: expanded K4 records need the INT4 buffers, 16-byte aligned");
   const int tiles = (t + tri::BN - 1) / tri::BN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   tri::quantize_q_kernel<<<dim3((t + 31) / 32, hq, batch), 256, 0, s>>>(
@@ -110,7 +111,8 @@ int tri_prepare_qk(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, cons
   tri::finalize_kernel<<<dim3(hk, batch), tri::D, 0, s>>>(partial, kstat, hk, t, 0);
   tri::quantize_k_kernel<<<dim3(tiles, hk, batch), 256, 0, s>>>(static_cast<const uint16_t*>(k), k_sb, k_sh, k_st,
                                                                 kstat, hk, t, static_cast<uint8_t*>(kp), ka,
-                                                                static_cast<uint8_t*>(k4p), ka4);
+                                                                static_cast<uint8_t*>(k4p), ka4,
+                                                                static_cast<uint8_t*>(k4x));
   return check_launch("prepare_qk");
 }
 
@@ -142,7 +144,7 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
                   const float* qa8, const float* ka8, const void* q4, const void* k4p, const float* qa4,
                   const float* ka4, void* out, int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
                   double scale, const int32_t* exact, const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st,
-                  const void* kx, const void* vx, int nx, const int32_t* v8sum, void* stream) {
+                  const void* kx, const void* vx, int nx, const int32_t* v8sum, const void* k4x, void* stream) {
   g_error.clear();
   const int tiles = (t + tri::BN - 1) / tri::BN;
   if (!order || !bands || !v16p || !vstat || !q8 || !k8p || !qa8 || !ka8 || !out)
@@ -163,6 +165,8 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
     return fail("attention: record and K-scale buffers must be 16-byte aligned");
   if (int4 && v8p == nullptr) return fail("attention: INT4 key tiles need the INT8 V records");
   if (v8sum && (!v8p || !aligned(v8sum, 16))) return fail("attention: V8 sums need the V8 records, 16-byte aligned");
+  if (k4x && (!int4 || !aligned(k4x, 16)))
+    return fail("attention: expanded K4 records need the INT4 operands, 16-byte aligned");
   if (exact != nullptr && (!qr || !aligned(qr, 16) || (q_sb | q_sh | q_st) % 8 != 0))
     return fail("attention: exact heads need 16-byte aligned bf16 q rows");
   if (exact != nullptr && (nx < 1 || nx > hk || !kx || !vx || !aligned(kx, 16) || !aligned(vx, 16)))
@@ -199,6 +203,7 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
   a.t = t;
   a.sm_log2 = (float)(scale * 1.4426950408889634);
   a.v8s = v8sum;
+  a.k4x = static_cast<const uint8_t*>(k4x);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (v8sum) tri::prefill_kernel<true><<<dim3(n_order, batch), 128, 0, s>>>(a);
   else tri::prefill_kernel<false><<<dim3(n_order, batch), 128, 0, s>>>(a);

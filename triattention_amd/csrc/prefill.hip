@@ -45,9 +45,13 @@ struct PrefillArgs {
   // extension (may be null): per V8 record, -127 times each channel's sum of its 64 codes (int32 [128]),
   // the starting value of the tile's P V accumulators (else two MFMAs compute it)
   const int32_t* v8s;
+  // extension (may be null): the INT4 K records expanded to 16 * code bytes in the INT8 record layout
+  // (8 KiB per tile), which INT4 tiles then read as INT8 tiles read theirs
+  const uint8_t* k4x;
 };
 
-enum Kind { KF16 = 0, KI8 = 1, KQ4 = 2 };
+// KQ4X: an INT4 tile whose K record is the expanded form (k4x); its arithmetic is KQ4's
+enum Kind { KF16 = 0, KI8 = 1, KQ4 = 2, KQ4X = 3 };
 
 struct PrefillState {
   v16f acc[4];     // O^T accumulators, 4 channel blocks of 32
@@ -74,10 +78,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
                                              const uint8_t* __restrict__ k_lds, const uint8_t* __restrict__ v_lds,
                                              const uint8_t* __restrict__ v_hi = nullptr,
                                              const int32_t* __restrict__ vs_lds = nullptr) {
+  constexpr bool IS4 = KIND == KQ4 || KIND == KQ4X;  // INT4 arithmetic (16 * dot)
   const int L = threadIdx.x & 63, half = L >> 5;
   // ---- S^T = K Q^T over 128 features, two 32-key blocks
   v16i s[2];
-  const int init = KIND == KQ4 ? 0 : (int)MAGIC_BITS;
+  const int init = IS4 ? 0 : (int)MAGIC_BITS;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -92,7 +97,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   // the 1/16 is folded into the slope, which is exact).  Only fp16 tiles can
   // be the diagonal tile or reach past t: INT8/INT4 tiles are never masked.
   auto score = [&](int kb, int r) -> float {
-    float v = KIND == KQ4 ? (float)s[kb][r] : __int_as_float(s[kb][r]);
+    float v = IS4 ? (float)s[kb][r] : __int_as_float(s[kb][r]);
     if constexpr (KIND == KF16) {
       if (masked) {
         const int key = col * BN + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -105,7 +110,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
   // ---- scaled row max (prefill_sm80.cu:244-253)
   float slope[4];
 #pragma unroll
-  for (int gi = 0; gi < 4; ++gi) slope[gi] = KIND == KQ4 ? qs * ks[gi] * 0.0625f : qs * ks[gi];
+  for (int gi = 0; gi < 4; ++gi) slope[gi] = IS4 ? qs * ks[gi] * 0.0625f : qs * ks[gi];
   float tile = -__builtin_inff();
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
@@ -125,7 +130,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
         mx = max(max(mx, s[kb][g0 + 5]), s[kb][g0 + 6]);
         mx = max(mx, s[kb][g0 + 7]);
         // (|dot| < 2^22: the magic float minus 1.5 * 2^23 is the dot product exactly)
-        const float d = KIND == KQ4 ? (float)mx : __int_as_float(mx) - MAGIC;
+        const float d = IS4 ? (float)mx : __int_as_float(mx) - MAGIC;
         tile = fmaxf(tile, slope[kb * 2 + hg] * d);
       }
     }
@@ -605,12 +610,16 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
         (void*)(a.k4 ? a.k4 + rec0 * K4_BYTES : a.k8), (short)0, a.k4 ? tiles * K4_BYTES : 0, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv8 =
         __builtin_amdgcn_make_buffer_rsrc((void*)(a.v8 + rec0 * V8_BYTES), (short)0, tiles * V8_BYTES, 0x00020000);
+    const bool k4x = a.k4x != nullptr;  // INT4 tiles read the expanded records (8 KiB each)
+    const __amdgpu_buffer_rsrc_t rk4x = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(k4x ? a.k4x + rec0 * K8_BYTES : a.k8), (short)0, k4x ? tiles * K8_BYTES : 0, 0x00020000);
     // (a local copy: reading the kernel argument inside the lambda would put the argument block in
     // private memory)
     const int32_t* v8s = SUMS ? a.v8s + rec0 * D : nullptr;
     auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd, int32_t* vsd) __attribute__((always_inline)) {
       const int col = tile_col(i);
       if (i < n8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd);
+      else if (k4x) lds_copy_buf<K8_BYTES>(rk4x, col * K8_BYTES, kd);
       else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd);
       lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd);
       // the scales (and the V8 sums: 512 bytes, 16 per lane of the first 32) ride along in the same
@@ -633,9 +642,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
       const int col = tile_col(i);
       const float4 k4v = *reinterpret_cast<const float4*>(sc);
       const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
-      if constexpr (decltype(kind)::value == KI8)
-        prefill_tile<KI8, SUMS>(a, st, qf, qs8, ks, col, false, qrow, kc, vc, nullptr, vsc);
-      else prefill_tile<KQ4, SUMS>(a, st, q4f, qs4, ks, col, false, qrow, kc, vc, nullptr, vsc);
+      constexpr int KIND = decltype(kind)::value;
+      if constexpr (KIND == KI8) prefill_tile<KI8, SUMS>(a, st, qf, qs8, ks, col, false, qrow, kc, vc, nullptr, vsc);
+      else prefill_tile<KIND, SUMS>(a, st, q4f, qs4, ks, col, false, qrow, kc, vc, nullptr, vsc);
     };
     // Tiles [i, end) of one kind, the first in buffer set PARITY.  Each kind has a
     // loop of its own: with both kinds in one loop body the compiler copies the
@@ -658,8 +667,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();  // every wave is done with the F16 pass's LDS
     issue(0, k_lds0, v_lds0, ks_lds0, vs_lds0);
     run(Tag<KI8>{}, Tag<0>{}, 0, n8);
-    if (n8 & 1) run(Tag<KQ4>{}, Tag<1>{}, n8, total);
-    else run(Tag<KQ4>{}, Tag<0>{}, n8, total);
+    if (k4x) {
+      if (n8 & 1) run(Tag<KQ4X>{}, Tag<1>{}, n8, total);
+      else run(Tag<KQ4X>{}, Tag<0>{}, n8, total);
+    } else {
+      if (n8 & 1) run(Tag<KQ4>{}, Tag<1>{}, n8, total);
+      else run(Tag<KQ4>{}, Tag<0>{}, n8, total);
+    }
   }
 
   // ---- epilogue: out = fma(acc / den, scale, mean) (prefill_sm80.cu:466-487)

@@ -122,10 +122,14 @@ __global__ __launch_bounds__(128) void finalize_kernel(const float* __restrict__
 // owns the 16-key group w, one key per 8 lanes (16 features per lane, DPP rotation), two passes of 8
 // keys; c8 / c4 are the workgroup's LDS staging.  256 threads.
 // common_device.cuh:58-131 (quantize_k_kernel).
+// Extension: rec4x (with rec4; may be null) receives the INT4 codes once more, expanded to one byte of
+// 16 * code each in the INT8 record's layout (8 KiB): the bytes the prefill kernel would otherwise expand
+// from rec4 in every tile it reads.
 __device__ __forceinline__ void quantize_k_tile(const uint16_t* __restrict__ src, int64_t st, int rows,
                                                 const float* __restrict__ mean, uint8_t* __restrict__ rec8,
                                                 float* __restrict__ ka, uint8_t* __restrict__ rec4,
-                                                float* __restrict__ ka4, uint8_t (*c8)[D], uint8_t (*c4)[D]) {
+                                                float* __restrict__ ka4, uint8_t (*c8)[D], uint8_t (*c4)[D],
+                                                uint8_t* __restrict__ rec4x = nullptr) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, sub = lane & 7;
   float mc[16];
 #pragma unroll
@@ -196,6 +200,10 @@ __device__ __forceinline__ void quantize_k_tile(const uint16_t* __restrict__ src
     const uint4 n = *reinterpret_cast<const uint4*>(&c4[key][f0]);  // one nibble value per byte
     const uint32_t w0 = n.x | (n.y << 4), w1 = n.z | (n.w << 4);
     *reinterpret_cast<uint2*>(rec4 + (F >> 1) * 1024 + L * 16 + (F & 1) * 8) = make_uint2(w0, w1);
+    if (rec4x != nullptr)
+      *reinterpret_cast<uint4*>(rec4x + F * 1024 + L * 16) =
+          make_uint4((n.x << 4) & 0xf0f0f0f0u, (n.y << 4) & 0xf0f0f0f0u, (n.z << 4) & 0xf0f0f0f0u,
+                     (n.w << 4) & 0xf0f0f0f0u);
   }
 }
 
@@ -203,14 +211,15 @@ __device__ __forceinline__ void quantize_k_tile(const uint16_t* __restrict__ src
 __global__ __launch_bounds__(256) void quantize_k_kernel(const uint16_t* __restrict__ k, int64_t sb, int64_t sh,
                                                          int64_t st, const float* __restrict__ kstat, int hk, int t,
                                                          uint8_t* __restrict__ k8, float* __restrict__ ka,
-                                                         uint8_t* __restrict__ k4, float* __restrict__ ka4) {
+                                                         uint8_t* __restrict__ k4, float* __restrict__ ka4,
+                                                         uint8_t* __restrict__ k4x) {
   __shared__ __align__(16) uint8_t c8[BN][D];
   __shared__ __align__(16) uint8_t c4[BN][D];
   const int tile = blockIdx.x, hd = blockIdx.y, b = blockIdx.z, tiles = (t + BN - 1) / BN;
   const int64_t hb = (int64_t)b * hk + hd, rec = hb * tiles + tile;
   quantize_k_tile(k + b * sb + hd * sh + (int64_t)tile * BN * st, st, t - tile * BN, kstat + hb * 3 * D,
                   k8 + rec * K8_BYTES, ka + rec * 4, k4 != nullptr ? k4 + rec * K4_BYTES : nullptr,
-                  k4 != nullptr ? ka4 + rec * 4 : nullptr, c8, c4);
+                  k4 != nullptr ? ka4 + rec * 4 : nullptr, c8, c4, k4x != nullptr ? k4x + rec * K8_BYTES : nullptr);
 }
 
 // v' = (v - mean) * inv of one 64-key tile (rows src + r * st for r < rows, zeros past) into the V16

@@ -60,10 +60,10 @@ def load_library() -> ctypes.CDLL:
     lib.tri_last_error.restype = ctypes.c_char_p
     lib.tri_last_error.argtypes = []
     lib.tri_prepare_qk.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I,
-                                   P, P, P, P, P, P, P, P, P, P, P]
+                                   P, P, P, P, P, P, P, P, P, P, P, P]
     lib.tri_pack_v.argtypes = [P, I64, I64, I64, I, I, I, P, P, P, P, P, P, P]
     lib.tri_attention.argtypes = [P, I, P, I, I, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, I64, I64, I64, D_,
-                                  P, P, I64, I64, I64, P, P, I, P, P]
+                                  P, P, I64, I64, I64, P, P, I, P, P, P]
     lib.tri_pack_exact.argtypes = [P, I64, I64, I64, P, I64, I64, I64, I, I, I, I, P, I, P, P, P]
     decode_args = [P, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I,
                    P, P, I64, I64, P, P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, I64, I64, I64, I64,
@@ -125,8 +125,11 @@ class Module:
         return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
     # -------------------------------------------------------------- prepare_qk
-    def prepare_qk(self, q, k, q8, qa, kp, ka, partial, kstat, q4=None, qa4=None, k4p=None, ka4=None):
-        """Per-token INT8 (and INT4) Q and centred per-block INT8 (and INT4) K operands."""
+    def prepare_qk(self, q, k, q8, qa, kp, ka, partial, kstat, q4=None, qa4=None, k4p=None, ka4=None, k4x=None):
+        """Per-token INT8 (and INT4) Q and centred per-block INT8 (and INT4) K operands.
+
+        Extension: ``k4x`` (uint32, as many words as ``kp``, with the INT4 buffers) receives the K4 records
+        expanded to 16 * code bytes in the K8 layout, which ``attention(..., k4x=...)`` reads."""
         _check(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 4 and q.size(3) == D and q.stride(3) == 1 and
                k.dtype == torch.bfloat16 and k.dim() == 4 and k.size(0) == q.size(0) and k.size(2) == q.size(2) and
                k.size(3) == D and k.stride(3) == 1, "BF16 Q/K [B,H,T,128] with contiguous features")
@@ -141,10 +144,12 @@ class Module:
                (not int4 or (q4.numel() == b * hq * t * D // 2 and qa4.numel() == b * hq * t and
                              k4p.numel() == b * hk * tiles * K4_WORDS and ka4.numel() == b * hk * tiles * 4)),
                "INT4 Q/K buffers (all or none)")
+        _check(k4x is None or (int4 and k4x.dtype == torch.uint32 and k4x.is_contiguous() and
+                               k4x.numel() == b * hk * tiles * K8_WORDS), "expanded K4 records (with the INT4 buffers)")
         with torch.cuda.device(q.device):
             self._call(self.lib.tri_prepare_qk, _ptr(q), q.stride(0), q.stride(1), q.stride(2), _ptr(k), k.stride(0),
                        k.stride(1), k.stride(2), b, hq, hk, t, _ptr(q8), _ptr(qa), _ptr(kp), _ptr(ka), _ptr(partial),
-                       _ptr(kstat), _ptr(q4), _ptr(qa4), _ptr(k4p), _ptr(ka4), self._stream(q.device))
+                       _ptr(kstat), _ptr(q4), _ptr(qa4), _ptr(k4p), _ptr(ka4), _ptr(k4x), self._stream(q.device))
 
     # ------------------------------------------------------------------ pack_v
     def pack_v(self, v, partial, vstat, v16p=None, v8p=None, v4p=None, v8sum=None):
@@ -168,14 +173,15 @@ class Module:
 
     # --------------------------------------------------------------- attention
     def attention(self, order, bands, groups, entries, v16p, v8p, v4p, vstat, q8, k8p, qa8, ka8, q4, k4p, qa4, ka4,
-                  out, scale, exact=None, q=None, kx=None, vx=None, nx=0, v8sum=None):
+                  out, scale, exact=None, q=None, kx=None, vx=None, nx=0, v8sum=None, k4x=None):
         """Banded causal attention: per key tile skip / INT8 QK x FP16 or INT8 PV / INT4 QK x INT8 PV.
 
         Extension: ``exact`` (int32 [Hq] on the device, 0 or 1 + record slot
         of the q-head's KV head) with the raw bf16 ``q`` [B,Hq,T,128] and the
         ``kx``/``vx`` records of ``pack_exact`` computes the flagged q-heads as
         exact causal attention on the unquantized operands.  ``v8sum``: what
-        ``pack_v(..., v8sum=...)`` wrote for ``v8p`` (the same result, fewer MFMAs)."""
+        ``pack_v(..., v8sum=...)`` wrote for ``v8p`` (the same result, fewer MFMAs).  ``k4x``: what
+        ``prepare_qk(..., k4x=...)`` wrote for ``k4p`` (the same result, fewer VALU instructions)."""
         _check(q8.dtype == torch.int8 and q8.dim() == 4 and q8.size(3) == D and q8.is_contiguous(), "Q8 [B,Hq,T,128]")
         b, h, t, _ = q8.shape
         hk = vstat.numel() // (b * 3 * D)
@@ -200,6 +206,8 @@ class Module:
                    kx.numel() * kx.element_size() >= b * nx * tiles * KX_BYTES and
                    vx.numel() * vx.element_size() >= b * nx * tiles * KX_BYTES, "exact heads: KX/VX records")
         _check(v8sum is None or (v8p is not None and _v8sum_ok(v8sum, b * hk * tiles)), "V8 sums")
+        _check(k4x is None or (q4 is not None and k4x.dtype == torch.uint32 and k4x.is_contiguous() and
+                               k4x.numel() == b * hk * tiles * K8_WORDS), "expanded K4 records (with the INT4 operands)")
         qs = q.stride() if exact is not None else (0, 0, 0)
         with torch.cuda.device(q8.device):
             self._call(self.lib.tri_attention, _ptr(order), order.numel(), _ptr(bands), b, h, hk, t, _ptr(v16p),
@@ -207,7 +215,7 @@ class Module:
                        _ptr(qa4), _ptr(ka4), _ptr(out), dt, out.stride(0), out.stride(1), out.stride(2),
                        float(scale), _ptr(exact), _ptr(q if exact is not None else None), qs[0], qs[1], qs[2],
                        _ptr(kx if exact is not None else None), _ptr(vx if exact is not None else None),
-                       int(nx) if exact is not None else 0, _ptr(v8sum), self._stream(q8.device))
+                       int(nx) if exact is not None else 0, _ptr(v8sum), _ptr(k4x), self._stream(q8.device))
         return out
 
     def pack_exact(self, k, v, exact, nx, kx, vx):

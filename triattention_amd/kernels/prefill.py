@@ -88,6 +88,8 @@ SCRATCH = (
     ("qa4", lambda L: L.batch * L.hq * L.t, torch.float32, lambda L: L.int4),
     ("k4", lambda L: L.batch * L.hk * L.tiles * 1024, torch.uint32, lambda L: L.int4),
     ("ka4", lambda L: L.batch * L.hk * L.tiles * 4, torch.float32, lambda L: L.int4),
+    # the K4 records expanded to 16 * code bytes in the K8 layout (extension: INT4 key tiles read these)
+    ("k4x", lambda L: L.batch * L.hk * L.tiles * 2048, torch.uint32, lambda L: L.int4),
     # V records: FP16 always; INT8 for INT8 bands and for every INT4 band (INT4 key tiles pair with
     # INT8 V, prefill_sm80.cu:462-465); INT4 when the decode cache asks for it
     (f"v{F16}", lambda L: L.batch * L.hk * L.tiles * WORDS[F16], torch.uint32, lambda L: F16 in L.formats),
@@ -206,8 +208,9 @@ class Prefill:
         layout = Layout(batch, hq, hk, t, Q4 in table.formats, frozenset(formats))
         ops = self.operands(layout, device)
         packed = ops["packed"]
+        k4x = ops["k4x"] if attend else None  # (only the prompt's attention reads the expanded records)
         self.module.prepare_qk(q, k, ops["q8"], ops["qa"], ops["kp"], ops["ka"], ops["partial"], ops["kstat"],
-                               ops["q4"], ops["qa4"], ops["k4"], ops["ka4"])
+                               ops["q4"], ops["qa4"], ops["k4"], ops["ka4"], k4x=k4x)
         v8sum = ops["v8sum"] if attend else None  # (only the prompt's attention reads the sums)
         self.module.pack_v(v, ops["partial"], ops["vstat"], packed[F16], packed[I8], packed[I4], v8sum=v8sum)
         exact, nx = self.exact(layer, hq, hk, device)
@@ -222,7 +225,7 @@ class Prefill:
             extra = {} if exact is None else dict(exact=exact, q=q, kx=kx, vx=vx, nx=nx)
             self.module.attention(table.order, table.bands, None, None, packed[F16], packed[I8], packed[I4],
                                   ops["vstat"], ops["q8"], ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"],
-                                  ops["qa4"], ops["ka4"], out, scale, v8sum=v8sum, **extra)
+                                  ops["qa4"], ops["ka4"], out, scale, v8sum=v8sum, k4x=k4x, **extra)
         if decode is not None:
             exact_kv = sorted(set(int(h) for h in self.bands_fn.bf16(layer))) if exact is not None else []
             self.decode_cache.store(layer, t, ops["kp"], ops["ka"], ops["kstat"], ops["vstat"], packed, decode[0],

@@ -220,6 +220,48 @@ def read_ceiling(args):
                                              "shape": list(shape)}}), flush=True)
 
 
+ISSUE_MODES = {0: ("32 v_fma_f32", 32), 1: ("8 v_exp_f32", 8), 2: ("24 v_fma_f32 + 8 v_exp_f32", 32),
+               3: ("4 v_mfma_i32_32x32x32_i8", 4), 4: ("4 v_mfma_f32_32x32x16_bf16", 4),
+               5: ("4 i8 MFMA + 64 v_fma_f32, one wave", 68),
+               6: ("first wave of a SIMD 4 i8 MFMA, the others 32 v_fma_f32", None)}
+
+
+def issue_probe(args):
+    """--issue-probe: SIMD cycles per instruction of the attention tiles' instruction kinds at 1-4 waves
+    per SIMD (tri_issue_probe; shader-clock cycles from s_memtime).  A SIMD's time is its slowest wave's,
+    its work every instruction its waves issued; the median over the device's SIMDs is reported."""
+    import torch
+    from triattention_amd.kernels.extension import load_extension
+    module = load_extension()
+    torch.cuda.set_device(0)
+    iters = 4096
+    rows = []
+    for mode, (what, per_iter) in ISSUE_MODES.items():
+        for w in range(1, 5):
+            if mode == 6 and w < 2:
+                continue
+            module.issue_probe(mode, w, 64)  # (warm-up launch)
+            r = module.issue_probe(mode, w, iters)
+            cyc, ticks = r[:, 0].double(), r[:, 1].double()
+            ghz = float(statistics.median((cyc / ticks * 0.1).tolist()))
+            per_wg = 4 * w
+            wg = cyc.view(-1, per_wg)  # [CUs, waves of the workgroup]; wave i on SIMD i % 4
+            simd_time = wg.view(-1, w, 4).amax(dim=1)  # [CUs, 4]
+            if mode == 6:
+                mfma_rate = iters * 4 / simd_time  # MFMAs per cycle: one MFMA wave per SIMD
+                valu_rate = iters * 32 * (w - 1) / simd_time
+                row = {"mode": mode, "what": what, "waves_per_simd": w, "clock_ghz": round(ghz, 3),
+                       "mfma_cycles_each": round(float(1 / mfma_rate.median()), 2),
+                       "fma_cycles_each": round(float(1 / valu_rate.median()), 2)}
+            else:
+                cpi = simd_time / (iters * per_iter * w)
+                row = {"mode": mode, "what": what, "waves_per_simd": w, "clock_ghz": round(ghz, 3),
+                       "simd_cycles_per_instruction": round(float(cpi.median()), 2)}
+            rows.append(row)
+            print(json.dumps(row), flush=True)
+    print(json.dumps({"issue_probe": rows}), flush=True)
+
+
 def graph_steps(run_token, tokens, stream):
     """ms per token of ``run_token`` (one token's launches: every layer's decode op and the step
     advance) captured once as a HIP graph and replayed ``tokens`` times, as the model path replays
@@ -505,6 +547,13 @@ def prefill_only(args):
         cfg = make()
         if name == "C0":
             cfg["kinds"] = []
+        if name == "C2" and args.c2_kind:
+            # only the C2 inputs with every KV head of one kind (counter runs of one kind)
+            kind = args.c2_kind
+            v = dict(cfg, kinds=[kind] * 4, bands=S.kv_head_bands([kind] * 4, 7))
+            out[f"C2 all {kind}"] = prefill_case(module, dev, stream, f"C2 all {kind}", v, reps, Prefill, from_bands,
+                                                 full_call=False)
+            continue
         out[name] = prefill_case(module, dev, stream, name, cfg, reps, Prefill, from_bands, full_call=args.only == "prefill")
         if name == "C2" and args.c2_kinds:
             # the C2 inputs with every KV head of one kind (the per-kind cost of the attention tile)
@@ -591,6 +640,8 @@ def main():
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time the streaming-read probe over every launch shape at the C1 launch's bytes instead")
+    ap.add_argument("--issue-probe", action="store_true",
+                    help="SIMD cycles per instruction of the attention tiles' instruction kinds (tri_issue_probe)")
     ap.add_argument("--ceiling-bytes", default="",
                     help="with --read-ceiling: comma-separated byte counts per launch (default: the C1 launch's)")
     ap.add_argument("--merge-form", choices=("auto", "four"), default="auto",
@@ -600,6 +651,8 @@ def main():
     ap.add_argument("--layers", type=int, default=28, help="C1 layers (own caches, one decode op each per token)")
     ap.add_argument("--c2-kinds", default="", help="with --only c2: also time the C2 inputs with every KV head of "
                                                    "each listed kind (i8, i4, bf16; comma-separated)")
+    ap.add_argument("--c2-kind", default="", help="with --only c2: time only the C2 inputs with every KV head of "
+                                                  "this kind (i8, i4 or bf16) instead of the C2 mix")
     ap.add_argument("--no-c4", action="store_true", help="leave out the C4 generation from the default run")
     ap.add_argument("--no-calibrate", action="store_true", help="leave out the calibration sweep from the default run")
     ap.add_argument("--only", choices=("prefill", "c2"),
@@ -615,6 +668,9 @@ def main():
     MERGE_FORM = args.merge_form
     if args.copy_probe:
         copy_probe()
+        return
+    if args.issue_probe:
+        issue_probe(args)
         return
     if args.read_ceiling:
         read_ceiling(args)

@@ -311,6 +311,15 @@ int tri_device_cus(int* cus);
 int tri_stream_read(const void* base, int64_t records, int waves, int waves_per_group, int depth, int32_t* sink,
                     void* stream);
 
+/* Measurement aid, no reference counterpart: the issue cost of the instruction kinds the attention
+ * tiles are made of.  One workgroup per CU of 256 * waves_per_simd threads (1..4 waves per SIMD) runs
+ * `iters` iterations of `mode` (0: 32 v_fma_f32; 1: 8 v_exp_f32; 2: 24 v_fma_f32 + 8 v_exp_f32;
+ * 3: 4 v_mfma_i32_32x32x32_i8; 4: 4 v_mfma_f32_32x32x16_bf16; 5: 4 i8 MFMA + 64 v_fma_f32 in one wave;
+ * 6: the first wave of each SIMD 4 i8 MFMA, the others 32 v_fma_f32) and writes, per wave
+ * w = workgroup * 4 * waves_per_simd + wave, its elapsed shader-clock cycles (s_memtime) to out[2w]
+ * and 100 MHz ticks (s_memrealtime) to out[2w + 1].  out: int64 [2 * CUs * 4 * waves_per_simd]. */
+int tri_issue_probe(int mode, int waves_per_simd, int iters, int64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

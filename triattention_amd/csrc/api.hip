@@ -773,4 +773,29 @@ int tri_stream_read(const void* base, int64_t records, int waves, int waves_per_
   return check_launch("stream_read");
 }
 
+int tri_issue_probe(int mode, int waves_per_simd, int iters, int64_t* out, void* stream) {
+  g_error.clear();
+  if (!out) return fail("issue_probe: null output");
+  if (mode < 0 || mode >= tri::ISSUE_MODES) return fail("issue_probe: mode must be in [0, %d)", tri::ISSUE_MODES);
+  if (waves_per_simd < 1 || waves_per_simd > 4) return fail("issue_probe: waves per SIMD must be 1..4");
+  if (mode == 6 && waves_per_simd < 2) return fail("issue_probe: mode 6 needs at least two waves per SIMD");
+  if (iters < 1 || iters > (1 << 20)) return fail("issue_probe: iterations must be in [1, 2^20]");
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return fail("issue_probe: no device");
+  using K = void (*)(int, int64_t*, float, float, int);
+  static const K kernels[tri::ISSUE_MODES] = {tri::issue_probe_kernel<0>, tri::issue_probe_kernel<1>,
+                                             tri::issue_probe_kernel<2>, tri::issue_probe_kernel<3>,
+                                             tri::issue_probe_kernel<4>, tri::issue_probe_kernel<5>,
+                                             tri::issue_probe_kernel<6>};
+  // 100 KiB of LDS per workgroup: at most one workgroup per CU
+  constexpr int LDS = 100 * 1024;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernels[mode]), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          LDS) != hipSuccess)
+    return fail("issue_probe: hipFuncSetAttribute");
+  hipLaunchKernelGGL(kernels[mode], dim3(cus), dim3(256 * waves_per_simd), LDS, static_cast<hipStream_t>(stream), iters,
+                     out, 1.0001f, 0.5f, 3);
+  return check_launch("issue_probe");
+}
+
 }  // extern "C"

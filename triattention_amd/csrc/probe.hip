@@ -42,3 +42,93 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t* base, i
 }
 
 }  // namespace tri
+
+namespace tri {
+
+// Issue-cost probe: how many SIMD cycles the instruction kinds of the attention tiles take when one
+// or more waves issue them.  One workgroup per CU of 256 * W threads (W waves per SIMD: wave i runs
+// on SIMD i % 4; 100 KiB of LDS keeps every other workgroup off the CU), each wave timing ITERS
+// iterations of MODE with s_memtime (shader clock) and s_memrealtime (100 MHz), written to
+// out[2 * wave], out[2 * wave + 1].  Modes (per iteration):
+//   0: 32 independent v_fma_f32            1: 8 independent v_exp_f32
+//   2: 24 v_fma_f32 and 8 v_exp_f32       3: 4 independent v_mfma_i32_32x32x32_i8
+//   4: 4 independent v_mfma_f32_32x32x16_bf16
+//   5: 4 v_mfma_i32_32x32x32_i8 and 64 v_fma_f32 in the same wave
+//   6: the first wave of each SIMD 4 v_mfma_i32_32x32x32_i8, the others 32 v_fma_f32
+// No reference counterpart: a measurement aid for the kernels' cost model.
+constexpr int ISSUE_MODES = 7;
+
+__device__ __forceinline__ void probe_fma8(float (&x)[8], float a, float b) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("v_fma_f32 %0, %1, %2, %0" : "+v"(x[i]) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void probe_exp8(float (&x)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("v_exp_f32 %0, %0" : "+v"(x[i]));
+}
+
+template <int MODE>
+__global__ __launch_bounds__(1024) void issue_probe_kernel(int iters, int64_t* out, float a, float b, int s) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bool first_on_simd = wave < 4;
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = a * (float)(lane + i);
+  const float fa = x[0] * 0.5f + b, fb = x[1] * 0.25f - a;  // fma operands in registers of their own
+  v16i acc[4] = {};
+  v16f facc[4] = {};
+  const v4i qa = {s, s + 1, s + 2, s + 3}, qb = {s, 2 * s, 3, 4};
+  v8bf ba, bb;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ba[i] = (__bf16)(a + (float)i);
+    bb[i] = (__bf16)(b - (float)i);
+  }
+  __syncthreads();
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) probe_fma8(x, fa, fb);
+    } else if constexpr (MODE == 1) {
+      probe_exp8(x);
+    } else if constexpr (MODE == 2) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) probe_fma8(x, fa, fb);
+      probe_exp8(x);
+    } else if constexpr (MODE == 3) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
+    } else if constexpr (MODE == 4) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) facc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ba, bb, facc[j], 0, 0, 0);
+    } else if constexpr (MODE == 5) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) probe_fma8(x, fa, fb);
+    } else {
+      if (first_on_simd) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) probe_fma8(x, fa, fb);
+      }
+    }
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  float sink = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sink += x[i];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sink += (float)acc[j][lane & 15] + facc[j][lane & 15];
+  if (lane == 0) {
+    const int64_t w = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
+    // (the sum joins the stored value only in a case no input produces, so nothing is optimised away)
+    out[2 * w] = (int64_t)(t1 - t0) + (sink == 1234.5f ? 1 : 0);
+    out[2 * w + 1] = (int64_t)(r1 - r0);
+  }
+}
+
+}  // namespace tri

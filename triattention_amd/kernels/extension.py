@@ -40,7 +40,7 @@ EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "t
            "tri_decode_partials", "tri_decode_merge", "tri_decode_short_tail", "tri_decode_merge_short_tail",
            "tri_decode_partials_timed", "tri_decode_noalloc",
            "tri_decode_tasks", "tri_cache_store", "tri_tail_spill", "tri_decode_occupancy", "tri_device_cus",
-           "tri_stream_read")
+           "tri_stream_read", "tri_issue_probe")
 KX_BYTES = 16384
 TASK_WORDS = 512  # int32 words of the decode task table per (sequence, KV head, split)
 
@@ -83,6 +83,7 @@ def load_library() -> ctypes.CDLL:
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_stream_read.argtypes = [P, I64, I, I, I, P, P]
+    lib.tri_issue_probe.argtypes = [I, I, I, P, P]
     for name in EXPORTS:
         if name != "tri_last_error":
             getattr(lib, name).restype = ctypes.c_int
@@ -483,6 +484,16 @@ class Module:
         n = ctypes.c_int(0)
         self._call(self.lib.tri_device_cus, ctypes.byref(n))
         return int(n.value)
+
+    def issue_probe(self, mode: int, waves_per_simd: int, iters: int):
+        """tri_issue_probe: per wave (shader-clock cycles, 100 MHz ticks), int64 [waves, 2] on the CPU."""
+        dev = torch.device("cuda", torch.cuda.current_device())
+        waves = self.device_cus() * 4 * waves_per_simd
+        out = torch.zeros(2 * waves, dtype=torch.int64, device=dev)
+        with torch.cuda.device(dev):
+            self._call(self.lib.tri_issue_probe, mode, waves_per_simd, iters, _ptr(out), self._stream(dev))
+        torch.cuda.synchronize()
+        return out.view(waves, 2).cpu()
 
     def stream_read(self, buf, waves: int, waves_per_group: int, depth: int, sink) -> None:
         """Measurement aid (no reference counterpart): read every 8 KiB record of the device buffer

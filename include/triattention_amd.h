@@ -286,15 +286,18 @@ int tri_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
  * or -1 when no q-head keeps it), the K and V record slots of its first spilled tile (spill n uses
  * slot + n), and the task-table row of its first growth split (-1: none; growth split i holds spilled
  * tiles 64 i .. 64 i + 63 as entries count0 + 64 i ...).  cap: spilled tiles per head that the arrays
- * have room for (when full, nothing moves and the tail clamps as the reference's does).  The metadata
- * arrays, K scales and records are the cache's, as tri_decode reads them; tasks (may be NULL) is its
- * task table. */
+ * have room for (when full, nothing moves and the tail clamps as the reference's does).  count0
+ * [rows][hk]: each head's entry count at the store.  A spill happens for all (sequence, KV head) pairs
+ * or for none: when any pair lacks room for the tile (tile index >= tiles_max, count0 + spills >= maxn,
+ * a record slot past n_k8 / n_k4 / n_v8 / n_kx, or INT4 K without k4c / ka4), nothing is written and
+ * the tail clamps as at cap.  The metadata arrays, K scales and records are the cache's, as tri_decode
+ * reads them; tasks (may be NULL) is its task table. */
 int tri_tail_spill(const int64_t* step, int64_t* tail_base, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh,
                    int64_t t_st, int max_tail, int rows, int hk, int maxn, int tiles_max, const int32_t* grow, int cap,
                    const int32_t* prompt, const int32_t* xslot, int32_t* entry, int32_t* kinfo, int32_t* slot,
-                   int32_t* count, int32_t* fmt, float* ka, float* ka4, const float* kstat, const float* vstat,
-                   void* k8c, int64_t n_k8, void* k4c, int64_t n_k4, void* v8c, int64_t n_v8, void* kxc, void* vxc,
-                   int64_t n_kx, int32_t* tasks, int n_tasks, void* stream);
+                   int32_t* count, const int32_t* count0, int32_t* fmt, float* ka, float* ka4, const float* kstat,
+                   const float* vstat, void* k8c, int64_t n_k8, void* k4c, int64_t n_k4, void* v8c, int64_t n_v8,
+                   void* kxc, void* vxc, int64_t n_kx, int32_t* tasks, int n_tasks, void* stream);
 
 /* Replaces decode_occupancy (common_host.cuh:89-94): resident decode
  * workgroups per compute unit, written to *blocks. */

@@ -120,11 +120,35 @@ def pack_kx(k_bits, v_bits):
 class HostSpill:
     """tri_tail_spill on host tensors, as its header documents it: when the tail is full and room is left,
     the oldest 64 rows of every (sequence, KV head) become tile ceil(prompt / 64) + tail_base / 64, the
-    tail moves up by 64 and tail_base grows by 64."""
+    tail moves up by 64 and tail_base grows by 64; when any (sequence, KV head) lacks room for the tile,
+    nothing changes."""
 
     def __init__(self, step, tail_base, ktail, vtail, grow, cap, prompt, dst, tasks):
         self.step, self.tail_base, self.ktail, self.vtail = step, tail_base, ktail, vtail
         self.grow, self.cap, self.prompt, self.dst, self.tasks = grow, int(cap), prompt, dst, tasks
+
+    def has_room(self, k):
+        """Room for spilled tile k in every (sequence, KV head), as the header states the rule."""
+        d = self.dst
+        rows, hk, maxn = d["entry"].shape
+        tiles_max = d["fmt"].shape[1]
+        n = {kind: 0 if d[kind] is None else d[kind].shape[0] for kind in ("k8", "k4", "v8")}
+        n_kx = 0 if d["kx"] is None else d["kx"].numel() // 16384
+        for row in range(rows):
+            j = (int(self.prompt[row]) + 63) // 64 + k
+            for kh in range(hk):
+                if j >= tiles_max or int(d["count0"][row, kh]) + k >= maxn:
+                    return False
+                info, gk, gv, _ = (int(x) for x in self.grow[row, kh])
+                x0 = int(d["xslot"][row, kh]) if d["xslot"] is not None else -1
+                if x0 >= 0:
+                    if x0 + j >= n_kx:
+                        return False
+                elif info >= 0:
+                    is4 = (info >> 8) & 1
+                    if gk + k >= n["k4" if is4 else "k8"] or gv + k >= n["v8"] or (is4 and d["ka4"] is None):
+                        return False
+        return True
 
     def run(self):
         d = self.dst
@@ -135,6 +159,8 @@ class HostSpill:
         if int(self.step[0]) - tb < max_tail or tb // 64 >= self.cap:
             return
         k = tb // 64
+        if not self.has_room(k):
+            return
         kbits = self.ktail.view(torch.int16).numpy().view(np.uint16)
         vbits = self.vtail.view(torch.int16).numpy().view(np.uint16)
         for row in range(rows):

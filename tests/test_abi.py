@@ -113,8 +113,8 @@ def test_tail_spill_validation_needs_no_gpu():
 
     def args(max_tail=256, tst=128, grow=fake):
         return [fake, fake, fake, fake, 8 * max_tail * tst, max_tail * tst, tst, max_tail, 2, 8, 64, 64, grow, 4,
-                fake, None, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, 16, None, 0, fake, 16, None,
-                None, 0, None, 0, None]
+                fake, None, fake, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, 16, None, 0, fake, 16,
+                None, None, 0, None, 0, None]
     assert lib.tri_tail_spill(*args(max_tail=32)) != 0
     assert b"max_tail must be in [64, 1024]" in lib.tri_last_error()
     assert lib.tri_tail_spill(*args(tst=100)) != 0

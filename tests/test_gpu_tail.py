@@ -115,6 +115,53 @@ def test_tail_spill_kernel_equals_host_restatement(module, bf16_kv):
     assert cache.layers[0]["store"].tb == 64 * 5 and cache.layers[0]["store"].grow_tiles == 8
 
 
+def test_a_spill_without_room_for_one_head_changes_nothing(module):
+    """tri_tail_spill spills for every (sequence, KV head) or for none: with the V record array cut at
+    one head's first growth slot, the launch on a full tail leaves the tails, the tail base, the
+    metadata and the records as they were; the same launch over the whole array then spills."""
+    hq, hk, max_tail = 8, 4, 64
+    print("\n[tail] spill without room for one head", flush=True)
+    cache = DecodeCache(module, max_tail=max_tail, grow_tail=64)
+    pre = Prefill(module, from_bands({"0": BANDS}), cache, out_dtype=torch.float32)
+    dev = torch.device("cuda")
+    q, k, v = small(9900, 2, hq, hk, 130)
+    pre(0, q.to(dev), k.to(dev), v.to(dev), 128 ** -0.5)
+    g = S.gen(9901)
+    for _ in range(max_tail):
+        qd, kd, vd = S.outlier_tensor(g, 2, hq, 1), S.outlier_tensor(g, 2, hk, 1), S.outlier_tensor(g, 2, hk, 1)
+        cache(0, qd.to(dev), kd.to(dev), vd.to(dev), 128 ** -0.5)
+        cache.advance()
+    e = cache.layers[0]
+    st, a, rows = e["store"], e["store"].arrays, e["batch"]
+    torch.cuda.synchronize()
+    assert int(cache.step[0]) == max_tail and int(a["tail_base"][0]) == 0  # full: the next launch spills
+    dst = dict(entry=e["entry"], kinfo=e["kinfo"], slot=e["slot"], count=e["count"], count0=a["count0"][:rows],
+               fmt=e["fmt"], xslot=e["xslot"], ka=e["ka"], ka4=e["ka4"], kstat=e["kstat"], vstat=e["vstat"],
+               k8=e["k8"], k4=e["k4"], v8=e["v"][I8], kx=e["kx"], vx=e["vx"])
+    grow = a["grow"][:rows].cpu()
+    kept = grow[:, :, 0] >= 0
+    assert kept.sum() > 1
+    short = int(grow[:, :, 2][kept].max())  # that head's first growth slot is past the cut array
+    tasks = e.get("tasks") if cache.tasks else None
+    launch = lambda d: module.plan_tail_spill(cache.step, a["tail_base"], e["tail_k"], e["tail_v"], a["grow"][:rows],
+                                              st.grow_tiles, e["prompt"], d, tasks)
+    names = ("entry", "kinfo", "slot", "count", "fmt", "ka", "k8", "tail_k", "tail_v")
+    before = {n: e[n].clone() for n in names}
+    before["v8"], before["tail_base"] = dst["v8"].clone(), a["tail_base"].clone()
+    if tasks is not None:
+        before["tasks"] = tasks[0].clone()
+    now = lambda n: dst["v8"] if n == "v8" else a["tail_base"] if n == "tail_base" else \
+        tasks[0] if n == "tasks" else e[n]
+    launch(dict(dst, v8=dst["v8"][:short])).run()
+    torch.cuda.synchronize()
+    for n, x in before.items():
+        assert torch.equal(now(n), x), f"{n} changed by a spill without room"
+    launch(dst).run()
+    torch.cuda.synchronize()
+    assert a["tail_base"].tolist() == [64, 0]  # (a 64-slot tail has no rows left to move up)
+    assert torch.equal(e["count"][kept.to(dev)], before["count"][kept.to(dev)] + 1)
+
+
 def _decode_run(module, prompts, bf16_kv, steps, max_tail, seed, check_every):
     hq, hk = 8, 4
     bands = torch.tensor(BANDS, dtype=torch.int32)

@@ -675,11 +675,12 @@ int tri_cache_store(const int32_t* bands, const int32_t* exact, int batch, int h
 int tri_tail_spill(const int64_t* step, int64_t* tail_base, void* ktail, void* vtail, int64_t t_sb, int64_t t_sh,
                    int64_t t_st, int max_tail, int rows, int hk, int maxn, int tiles_max, const int32_t* grow, int cap,
                    const int32_t* prompt, const int32_t* xslot, int32_t* entry, int32_t* kinfo, int32_t* slot,
-                   int32_t* count, int32_t* fmt, float* ka, float* ka4, const float* kstat, const float* vstat,
+                   int32_t* count, const int32_t* count0, int32_t* fmt, float* ka, float* ka4, const float* kstat, const float* vstat,
                    void* k8c, int64_t n_k8, void* k4c, int64_t n_k4, void* v8c, int64_t n_v8, void* kxc, void* vxc,
                    int64_t n_kx, int32_t* tasks, int n_tasks, void* stream) {
   g_error.clear();
-  if (!step || !tail_base || !ktail || !vtail || !grow || !prompt || !entry || !kinfo || !slot || !count || !fmt ||
+  if (!step || !tail_base || !ktail || !vtail || !grow || !prompt || !entry || !kinfo || !slot || !count || !count0 ||
+      !fmt ||
       !ka || !kstat || !vstat || !k8c || !v8c)
     return fail("tail_spill: null buffer");
   if (rows < 1 || hk < 1 || maxn < 1 || tiles_max < 1 || cap < 0) return fail("tail_spill: empty shape");
@@ -718,6 +719,7 @@ int tri_tail_spill(const int64_t* step, int64_t* tail_base, void* ktail, void* v
   a.kinfo = kinfo;
   a.slot = slot;
   a.count = count;
+  a.count0 = count0;
   a.fmt = fmt;
   a.ka = ka;
   a.ka4 = ka4;

@@ -38,6 +38,7 @@ struct SpillArgs {
   int32_t* kinfo;
   int32_t* slot;
   int32_t* count;  // [rows][hk]
+  const int32_t* count0;  // [rows][hk]: count at the store (count <= count0 + tiles spilled since)
   int32_t* fmt;    // [rows][tiles_max]
   float* ka;       // [rows][hk][tiles_max][4]
   float* ka4;      // (may be null)
@@ -55,6 +56,29 @@ struct SpillArgs {
 
 constexpr int SPILL_THREADS = 256;
 
+// Whether every (sequence, KV head) has room for spilled tile k.  Each workgroup evaluates the whole
+// launch's rule from arrays that no workgroup of the launch writes (prompt, grow, xslot, count0; the
+// entry count of a head is at most count0 + k), so all of them reach the same answer before any row
+// moves: without room anywhere, no tile is written, the tail and tail_base stay as they are and the
+// tail clamps as the reference's does.
+__device__ bool spill_has_room(const SpillArgs& a, int k) {
+  bool ok = true;
+  for (int p = threadIdx.x; p < a.rows * a.hk; p += SPILL_THREADS) {
+    const int j = (a.prompt[p / a.hk] + BN - 1) / BN + k;
+    ok = ok && j < a.tiles_max && a.count0[p] + k < a.maxn;
+    const int x0 = a.xslot != nullptr ? a.xslot[p] : -1;
+    const int4 gr = *reinterpret_cast<const int4*>(a.grow + (int64_t)p * 4);
+    if (x0 >= 0) {
+      ok = ok && (int64_t)x0 + j < a.n_kx;
+    } else if (gr.x >= 0) {
+      const bool is4 = (gr.x >> 8) & 1;
+      ok = ok && (int64_t)gr.y + k < (is4 ? a.n_k4 : a.n_k8) && (int64_t)gr.z + k < a.n_v8 &&
+           (!is4 || (a.k4c != nullptr && a.ka4 != nullptr));
+    }
+  }
+  return __syncthreads_and(ok);
+}
+
 // One workgroup per (KV head, sequence).
 __global__ __launch_bounds__(SPILL_THREADS) void tail_spill_kernel(SpillArgs a) {
   __shared__ __align__(16) union {
@@ -69,6 +93,7 @@ __global__ __launch_bounds__(SPILL_THREADS) void tail_spill_kernel(SpillArgs a) 
   if (*a.step - tb < a.max_tail) return;  // the tail has a free slot for this step's token
   const int k = (int)(tb / BN);           // tiles this cache has taken from the tail since the store
   if (k >= a.cap) return;                 // no room reserved: the tail clamps as the reference's does
+  if (!spill_has_room(a, k)) return;      // (the same answer in every workgroup)
   const int kh = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const int64_t hb = (int64_t)row * a.hk + kh;
   const int4 gr = *reinterpret_cast<const int4*>(a.grow + hb * 4);

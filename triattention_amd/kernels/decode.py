@@ -525,7 +525,8 @@ class DecodeCache:
             st, a, rows = e["store"], e["store"].arrays, e["batch"]
             if "tasks" not in e or not self.tasks:
                 a["grow"][:rows, :, 3].fill_(-1)
-            dst = dict(entry=e["entry"], kinfo=e["kinfo"], slot=e["slot"], count=e["count"], fmt=e["fmt"],
+            dst = dict(entry=e["entry"], kinfo=e["kinfo"], slot=e["slot"], count=e["count"],
+                       count0=a["count0"][:rows], fmt=e["fmt"],
                        xslot=e["xslot"], ka=e["ka"], ka4=e["ka4"], kstat=e["kstat"], vstat=e["vstat"], k8=e["k8"],
                        k4=e["k4"], v8=e["v"][I8], kx=e["kx"], vx=e["vx"])
             e["spill"] = self.module.plan_tail_spill(self.step, a["tail_base"], e["tail_k"], e["tail_v"],

@@ -79,7 +79,7 @@ def load_library() -> ctypes.CDLL:
                                     P, P, P, P, P, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, P, I64, I64,
                                     P]
     lib.tri_tail_spill.argtypes = [P, P, P, P, I64, I64, I64, I, I, I, I, I, P, I, P, P, P, P, P, P, P, P, P, P, P,
-                                   P, I64, P, I64, P, I64, P, P, I64, P, I, P]
+                                   P, P, I64, P, I64, P, I64, P, P, I64, P, I, P]
     lib.tri_decode_occupancy.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_stream_read.argtypes = [P, I64, I, I, I, P, P]
@@ -439,7 +439,9 @@ class Module:
         tail, common_device.cuh:384).  ``dst``: the cache arrays as ``cache_store`` takes them (entry /
         kinfo / slot, count, fmt, xslot, ka, ka4, kstat, vstat, k8 / k4 / v8 records, kx / vx bytes);
         ``grow`` int32 [rows, hk, 4]; ``cap`` spilled tiles per head the arrays hold; ``tasks`` the
-        decode's (table, n) or None.  The plan's ``run()`` launches on the current stream."""
+        decode's (table, n) or None; ``dst["count0"]`` each head's entry count at the store.  A spill
+        happens for every (sequence, KV head) or, when any lacks room, for none.  The plan's ``run()``
+        launches on the current stream."""
         rows, hk, maxn = dst["entry"].shape
         tiles_max = dst["fmt"].shape[1]
         max_tail = ktail.size(2)
@@ -454,6 +456,8 @@ class Module:
         _check(prompt.dtype == torch.int32 and prompt.numel() == rows and int(cap) >= 0, "tail_spill: prompt / cap")
         for name in ("kinfo", "slot"):
             _check(tuple(dst[name].shape) == (rows, hk, maxn), f"tail_spill: {name}")
+        _check(dst["count0"].dtype == torch.int32 and dst["count0"].is_contiguous() and
+               tuple(dst["count0"].shape) == (rows, hk), "tail_spill: count0 int32 [rows,Hk]")
         _check(tuple(dst["ka"].shape) == (rows, hk, tiles_max, 4) and tuple(dst["count"].shape) == (rows, hk) and
                (dst["ka4"] is None or tuple(dst["ka4"].shape) == (rows, hk, tiles_max, 4)) and
                tuple(dst["kstat"].shape) == (rows, hk, 3, D) and tuple(dst["vstat"].shape) == (rows, hk, 3, D) and
@@ -466,7 +470,8 @@ class Module:
         p = _ptr
         args = [p(step), p(tail_base), p(ktail), p(vtail), ktail.stride(0), ktail.stride(1), ktail.stride(2),
                 max_tail, rows, hk, maxn, tiles_max, p(grow), int(cap), p(prompt), p(dst["xslot"]), p(dst["entry"]),
-                p(dst["kinfo"]), p(dst["slot"]), p(dst["count"]), p(dst["fmt"]), p(dst["ka"]), p(dst["ka4"]),
+                p(dst["kinfo"]), p(dst["slot"]), p(dst["count"]), p(dst["count0"]), p(dst["fmt"]), p(dst["ka"]),
+                p(dst["ka4"]),
                 p(dst["kstat"]), p(dst["vstat"]), p(dst["k8"]), dst["k8"].shape[0], p(dst["k4"]),
                 0 if dst["k4"] is None else dst["k4"].shape[0], p(dst["v8"]), dst["v8"].shape[0],
                 p(dst["kx"] if dst["xslot"] is not None else None), p(dst["vx"] if dst["xslot"] is not None else None),
@@ -551,14 +556,12 @@ class DecodePlan:
 class SpillPlan:
     """A validated, marshalled ``tail_spill`` launch for one layer's decode cache."""
 
-    STREAM = 36
-
     def __init__(self, module, args, device, keep):
         self.module, self.args, self.device, self.keep = module, args, device, keep
 
     def run(self):
         index = self.device.index if self.device.index is not None else torch.cuda.current_device()
-        self.args[self.STREAM] = torch.cuda.current_stream(index).cuda_stream
+        self.args[-1] = torch.cuda.current_stream(index).cuda_stream  # (the stream is the last argument)
         if torch.cuda.current_device() != index:
             with torch.cuda.device(index):
                 self.module._call(self.module.lib.tri_tail_spill, *self.args)

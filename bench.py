@@ -223,7 +223,12 @@ def read_ceiling(args):
 ISSUE_MODES = {0: ("32 v_fma_f32", 32), 1: ("8 v_exp_f32", 8), 2: ("24 v_fma_f32 + 8 v_exp_f32", 32),
                3: ("4 v_mfma_i32_32x32x32_i8", 4), 4: ("4 v_mfma_f32_32x32x16_bf16", 4),
                5: ("4 i8 MFMA + 64 v_fma_f32, one wave", 68),
-               6: ("first wave of a SIMD 4 i8 MFMA, the others 32 v_fma_f32", None)}
+               6: ("first wave of a SIMD 4 i8 MFMA, the others 32 v_fma_f32", None),
+               7: ("4 i8 MFMA + 96 v_fma_f32, spread", 100), 8: ("4 i8 MFMA + 96 v_fma_f32, MFMAs first", 100),
+               9: ("as 8, then a barrier", 100), 10: ("as 9, fma after the MFMA results", 100),
+               11: ("as 10, odd waves half an iteration behind", 100), 12: ("as 7, then a barrier", 100),
+               13: ("tile-shaped: 16 MFMA + 128 fma, then 200 fma + 32 exp, every wave in step", 376),
+               14: ("as 13, odd waves of a SIMD in the other half", 376)}
 
 
 def issue_probe(args):
@@ -236,7 +241,10 @@ def issue_probe(args):
     torch.cuda.set_device(0)
     iters = 4096
     rows = []
+    wanted = {int(m) for m in args.issue_modes.split(",")} if args.issue_modes else set(ISSUE_MODES)
     for mode, (what, per_iter) in ISSUE_MODES.items():
+        if mode not in wanted:
+            continue
         for w in range(1, 5):
             if mode == 6 and w < 2:
                 continue
@@ -642,6 +650,7 @@ def main():
                     help="time the streaming-read probe over every launch shape at the C1 launch's bytes instead")
     ap.add_argument("--issue-probe", action="store_true",
                     help="SIMD cycles per instruction of the attention tiles' instruction kinds (tri_issue_probe)")
+    ap.add_argument("--issue-modes", default="", help="with --issue-probe: comma-separated modes (default all)")
     ap.add_argument("--ceiling-bytes", default="",
                     help="with --read-ceiling: comma-separated byte counts per launch (default: the C1 launch's)")
     ap.add_argument("--merge-form", choices=("auto", "four"), default="auto",

@@ -318,7 +318,12 @@ int tri_stream_read(const void* base, int64_t records, int waves, int waves_per_
  * tiles are made of.  One workgroup per CU of 256 * waves_per_simd threads (1..4 waves per SIMD) runs
  * `iters` iterations of `mode` (0: 32 v_fma_f32; 1: 8 v_exp_f32; 2: 24 v_fma_f32 + 8 v_exp_f32;
  * 3: 4 v_mfma_i32_32x32x32_i8; 4: 4 v_mfma_f32_32x32x16_bf16; 5: 4 i8 MFMA + 64 v_fma_f32 in one wave;
- * 6: the first wave of each SIMD 4 i8 MFMA, the others 32 v_fma_f32) and writes, per wave
+ * 6: the first wave of each SIMD 4 i8 MFMA, the others 32 v_fma_f32; 7-12: 4 i8 MFMA and 96 v_fma_f32
+ * per wave, 7 spread, 8 MFMAs first, 9 as 8 then a barrier, 10 as 9 with the fma after the MFMA results,
+ * 11 as 10 with the odd waves of a SIMD half an iteration behind, 12 as 7 then a barrier; 13: a
+ * tile-shaped iteration, 16 i8 MFMA interleaved with 128 v_fma_f32 then 200 v_fma_f32 and 32 v_exp_f32
+ * after the MFMA results, then a barrier; 14: as 13 with the odd waves of a SIMD in the other order) and
+ * writes, per wave
  * w = workgroup * 4 * waves_per_simd + wave, its elapsed shader-clock cycles (s_memtime) to out[2w]
  * and 100 MHz ticks (s_memrealtime) to out[2w + 1].  out: int64 [2 * CUs * 4 * waves_per_simd]. */
 int tri_issue_probe(int mode, int waves_per_simd, int iters, int64_t* out, void* stream);

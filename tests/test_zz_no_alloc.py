@@ -48,9 +48,12 @@ def _compare(module, cache, seed):
     dev = torch.device("cuda")
     qd, kd, vd = (S.outlier_tensor(g, batch, 8, 1).to(dev), S.outlier_tensor(g, batch, 2, 1).to(dev),
                   S.outlier_tensor(g, batch, 2, 1).to(dev))
-    ref = cache(0, qd, kd, vd, SCALE)  # tri_decode with the cache's own partial buffers
+    # tri_decode (split kernel and the four-wave merge, as tri_decode_noalloc launches them) with the
+    # cache's own partial buffers
+    ref = torch.full((batch, 8, 1, 128), float("nan"), device=dev)
+    plan = cache.plan(0, qd, kd, ref, SCALE)
+    plan.run(qd, kd, vd, ref)
     got = torch.full_like(ref, float("nan"))
-    plan = cache.plan(0, qd, kd, got, SCALE)
     rc = module.lib.tri_decode_noalloc(*_args(plan, qd, kd, vd, got))
     assert rc == 0, module.lib.tri_last_error().decode()
     torch.cuda.synchronize()
@@ -79,10 +82,11 @@ def test_noalloc_refuses_a_second_stream_while_the_first_is_pending(module):
     dev = torch.device("cuda")
     qd, kd, vd = (S.outlier_tensor(g, 2, 8, 1).to(dev), S.outlier_tensor(g, 2, 2, 1).to(dev),
                   S.outlier_tensor(g, 2, 2, 1).to(dev))
-    ref = cache(0, qd, kd, vd, SCALE)
+    ref = torch.full((2, 8, 1, 128), float("nan"), device=dev)
+    plan = cache.plan(0, qd, kd, ref, SCALE)
+    plan.run(qd, kd, vd, ref)  # tri_decode: the four-wave merge, as tri_decode_noalloc
     torch.cuda.synchronize()
     got_a, got_b = torch.full_like(ref, float("nan")), torch.full_like(ref, float("nan"))
-    plan = cache.plan(0, qd, kd, got_a, SCALE)
     sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
     x = torch.randn(8192, 8192, dtype=torch.bfloat16, device=dev)
     torch.cuda.synchronize()

@@ -789,7 +789,11 @@ int tri_issue_probe(int mode, int waves_per_simd, int iters, int64_t* out, void*
   static const K kernels[tri::ISSUE_MODES] = {tri::issue_probe_kernel<0>, tri::issue_probe_kernel<1>,
                                              tri::issue_probe_kernel<2>, tri::issue_probe_kernel<3>,
                                              tri::issue_probe_kernel<4>, tri::issue_probe_kernel<5>,
-                                             tri::issue_probe_kernel<6>};
+                                             tri::issue_probe_kernel<6>, tri::issue_probe_kernel<7>,
+                                             tri::issue_probe_kernel<8>, tri::issue_probe_kernel<9>,
+                                             tri::issue_probe_kernel<10>, tri::issue_probe_kernel<11>,
+                                             tri::issue_probe_kernel<12>, tri::issue_probe_kernel<13>,
+                                             tri::issue_probe_kernel<14>};
   // 100 KiB of LDS per workgroup: at most one workgroup per CU
   constexpr int LDS = 100 * 1024;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernels[mode]), hipFuncAttributeMaxDynamicSharedMemorySize,

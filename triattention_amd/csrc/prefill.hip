@@ -515,6 +515,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   __shared__ __align__(16) uint8_t v_lds0[V8_BYTES], v_lds1[V8_BYTES];
   __shared__ __align__(16) float ks_lds0[4], ks_lds1[4];  // the tile's 4 K group scales
   __shared__ __align__(16) int32_t vs_lds0[SUMS ? D : 4], vs_lds1[SUMS ? D : 4];  // its -127 * V8 sums
+  __shared__ __align__(16) float vms_lds[2 * D];  // the KV head's V mean and scale, for the epilogue
   const int rows = (a.t + BN - 1) / BN;
   // Launch sequence: BandTable's order is KV-head-major (prefill.py:24-25), so the workgroups running at
   // any one time would all belong to one KV head.  Workgroup j takes entry (kv * rows + qd) * g + r of it
@@ -565,6 +566,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int i = 0; i < nf16; ++i) {
     const int col = i == 0 ? 0 : qb;
     __syncthreads();
+    // (with the first copy: the epilogue's V mean and scale, 1 KiB, so that it reads them from LDS)
+    if (i == 0 && tid < 64)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.vstat + ((int64_t)b * a.hk + kh) * 3 * D + tid * 4),
+                                       (__attribute__((address_space(3))) void*)(vms_lds + tid * 4), 16, 0, 0);
     lds_copy_async<K8_BYTES>(a.k8 + (rec0 + col) * K8_BYTES, k_lds0);
     lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES, v_lds0);
     lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES + V16_BYTES / 2, v_lds1);
@@ -679,17 +684,18 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   // ---- epilogue: out = fma(acc / den, scale, mean) (prefill_sm80.cu:466-487)
   if (!row_ok) return;
   const float inv = st.den > 0.f ? 1.f / st.den : 0.f;
-  const float* mean = a.vstat + ((int64_t)b * a.hk + kh) * 3 * D;
-  const float* scale = mean + D;
   const int64_t obase = b * a.osb + qh * a.osh + (int64_t)qrow * a.ost;
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
       const int ch = cb * 32 + 8 * r4 + 4 * half;
+      const float4 mean = *reinterpret_cast<const float4*>(vms_lds + ch);
+      const float4 scale = *reinterpret_cast<const float4*>(vms_lds + D + ch);
+      const float mv[4] = {mean.x, mean.y, mean.z, mean.w}, sv[4] = {scale.x, scale.y, scale.z, scale.w};
       float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(st.acc[cb][r4 * 4 + i] * inv, scale[ch + i], mean[ch + i]);
+      for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(st.acc[cb][r4 * 4 + i] * inv, sv[i], mv[i]);
       if (a.out_dtype == 0) {
         *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + ch) = make_float4(v[0], v[1], v[2], v[3]);
       } else if (a.out_dtype == 1) {

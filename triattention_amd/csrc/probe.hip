@@ -55,8 +55,19 @@ namespace tri {
 //   4: 4 independent v_mfma_f32_32x32x16_bf16
 //   5: 4 v_mfma_i32_32x32x32_i8 and 64 v_fma_f32 in the same wave
 //   6: the first wave of each SIMD 4 v_mfma_i32_32x32x32_i8, the others 32 v_fma_f32
+// and, per wave, 4 v_mfma_i32_32x32x32_i8 and 96 v_fma_f32 (the quantized tile's 1 : 24 ratio) as
+//   7: spread, each MFMA followed by 24 fma           8: the 4 MFMAs back to back, then the 96 fma
+//   9: as 8, then a workgroup barrier                 10: as 9, the first fma reading the last MFMA's
+//      result (the tile's score -> softmax dependency, every wave in the same phase)
+//  11: as 10 in two halves split by barriers, the odd waves of a SIMD half an iteration behind the even
+//      ones (MFMAs of one wave beside the other's fma)
+//  12: as 7, then a workgroup barrier
+// and, per wave, a tile-shaped iteration: P = 16 v_mfma_i32_32x32x32_i8 interleaved with 128 v_fma_f32,
+// S = 200 v_fma_f32 and 32 v_exp_f32 whose first fma reads the last MFMA's result, then a barrier:
+//  13: every wave P then S (the waves of a SIMD in the same phase)
+//  14: even waves of a SIMD P then S, odd waves S then P (one wave's MFMAs beside the other's S)
 // No reference counterpart: a measurement aid for the kernels' cost model.
-constexpr int ISSUE_MODES = 7;
+constexpr int ISSUE_MODES = 15;
 
 __device__ __forceinline__ void probe_fma8(float (&x)[8], float a, float b) {
 #pragma unroll
@@ -107,7 +118,7 @@ __global__ __launch_bounds__(1024) void issue_probe_kernel(int iters, int64_t* o
       for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
 #pragma unroll
       for (int k = 0; k < 8; ++k) probe_fma8(x, fa, fb);
-    } else {
+    } else if constexpr (MODE == 6) {
       if (first_on_simd) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
@@ -115,6 +126,72 @@ __global__ __launch_bounds__(1024) void issue_probe_kernel(int iters, int64_t* o
 #pragma unroll
         for (int k = 0; k < 4; ++k) probe_fma8(x, fa, fb);
       }
+    } else if constexpr (MODE == 7 || MODE == 12) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) probe_fma8(x, fa, fb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (MODE == 12) __syncthreads();
+    } else if constexpr (MODE == 8 || MODE == 9 || MODE == 10) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (MODE == 10) x[0] = __builtin_fmaf(x[0], fa, (float)acc[3][0]);
+#pragma unroll
+      for (int k = 0; k < 12; ++k) probe_fma8(x, fa, fb);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (MODE != 8) __syncthreads();
+    } else if constexpr (MODE == 13 || MODE == 14) {
+      const bool odd = MODE == 14 && ((wave >> 2) & 1);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        if ((half == 0) != odd) {
+          // P: 4 groups of 4 MFMAs, each group followed by 32 fma
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) probe_fma8(x, fa, fb);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+          // S: reads the last MFMA's result, then 25 x 8 fma and 4 x 8 exp
+          x[0] = __builtin_fmaf(x[0], fa, (float)acc[3][0]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int f = 0; f < 6; ++f) probe_fma8(x, fa, fb);
+            probe_exp8(x);
+          }
+          probe_fma8(x, fa, fb);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      __syncthreads();
+    } else {
+      const bool odd = (wave >> 2) & 1;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        if (odd == (half == 1)) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa, qb, acc[j], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          x[0] = __builtin_fmaf(x[0], fa, (float)acc[3][0]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) probe_fma8(x, fa, fb);
+        __builtin_amdgcn_sched_barrier(0);
+        if (half == 0) __syncthreads();
+      }
+      __syncthreads();
     }
   }
   const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();

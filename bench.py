@@ -88,13 +88,54 @@ C1_RECORD_BYTES = 170_655_744
 TRAFFIC_SOURCES = (ROOT / "triattention_amd" / "csrc" / "decode.hip", ROOT / "triattention_amd" / "csrc" / "common.h")
 
 
-def decode_source_hash():
-    """First 16 hex digits of the SHA-256 of the decode kernel's sources (decode.hip, then common.h)."""
+def source_hash(files):
+    """First 16 hex digits of the SHA-256 of ``files``' bytes, in order."""
     import hashlib
     h = hashlib.sha256()
-    for f in TRAFFIC_SOURCES:
+    for f in files:
         h.update(f.read_bytes())
     return h.hexdigest()[:16]
+
+
+def decode_source_hash():
+    """The decode kernel's sources (decode.hip, then common.h), hashed as ``source_hash``."""
+    return source_hash(TRAFFIC_SOURCES)
+
+
+# the prefill kernel's sources, and the counter summary whose per-tile figures the C2 line carries
+PREFILL_SOURCES = (ROOT / "triattention_amd" / "csrc" / "prefill.hip", ROOT / "triattention_amd" / "csrc" / "common.h")
+PREFILL_PROFILE = ROOT / "profiles" / "prefill_counters_C2.md"
+PREFILL_FIELDS = ("simd_cycles_per_tile_wave", "valu_per_tile_wave", "mfma_per_tile_wave",
+                  "transcendental_per_tile_wave", "mfma_busy_fraction", "mfma_coexec_fraction")
+
+
+def prefill_source_hash():
+    """The prefill kernel's sources (prefill.hip, then common.h), hashed as ``source_hash``."""
+    return source_hash(PREFILL_SOURCES)
+
+
+def profile_fields(path, keys):
+    """``key: value`` lines of a committed summary, for the listed keys."""
+    fields = {}
+    if path.exists():
+        for line in path.read_text().splitlines():
+            if ":" in line and line.split(":", 1)[0] in keys:
+                key, val = line.split(":", 1)
+                fields[key] = val.strip()
+    return fields
+
+
+def prefill_counters():
+    """(per-tile counter figures of the C2 mix, note) from the committed counter summary, or None when it
+    was taken on other prefill sources than the ones built here."""
+    fields = profile_fields(PREFILL_PROFILE, PREFILL_FIELDS + ("kernel_source_sha16",))
+    here = prefill_source_hash()
+    if fields.get("kernel_source_sha16") != here:
+        return None, (f"counter summary taken on prefill kernel sources {fields.get('kernel_source_sha16')}, "
+                      f"these are {here}: not reported")
+    return ({k: float(fields[k]) for k in PREFILL_FIELDS if k in fields},
+            f"rocprofv3 counters of the C2 mix per 64-key tile of one wave, {PREFILL_PROFILE.name} "
+            f"(kernel sources {here})")
 
 
 def measured_traffic():
@@ -928,6 +969,7 @@ def main():
         r2 = prefill_case(module, dev, stream, "C2", c2, 5, Prefill, from_bands)
         r2["workload"] = (f"C2 prefill: batch 4, Hq 28 / Hk 4, T 8192, log-uniform channel scales, KV heads "
                           f"{c2['kinds']}")
+        r2["counters"], r2["counters_note"] = prefill_counters()
         result["prefill"] = {"C0": r0, "C2": r2}
 
     # ------------------------------------------------------- C3 ragged decode

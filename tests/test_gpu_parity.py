@@ -448,6 +448,38 @@ def test_attention_with_and_without_v8_sums(module):
     assert_close(out.numpy(), ref, what="prefill with V8 sums", tol=tol)
 
 
+NO_INT8 = [[0, INF], [0, 3], [0, 1], [0, 0], [1, INF], [INF, INF]]
+
+
+@pytest.mark.parametrize("t", [200, 333])
+def test_bands_without_int8_tiles(module, t):
+    """w8 = 0: the INT4 list reaches the query tile itself, which the reference masks as the last entry
+    of its pass (prefill_sm80.cu:328-329) after the fp16 pass has already visited it; t = 333 also masks
+    keys past t in that tile.  All four kernel forms (V8 sums or not, expanded K4 records or not) give
+    the same outputs, within the parity bar of the oracle."""
+    print(f"\n[parity] prefill t={t} with w8 = 0 bands", flush=True)
+    q, k, v = small(3600 + t, 1, 6, 2, t)
+    bands = torch.tensor(NO_INT8, dtype=torch.int32)
+    out, ops, pre = run_prefill(module, q, k, v, bands, 128 ** -0.5)
+    table = next(iter(pre.tables.values()))
+    pk = ops["packed"]
+    for sums, wide in ((None, None), (ops["v8sum"], None), (None, ops["k4x"])):
+        plain = torch.empty_like(out).cuda()
+        module.attention(table.order, table.bands, None, None, pk[1], pk[2], pk[3], ops["vstat"], ops["q8"],
+                         ops["kp"], ops["qa"], ops["ka"], ops["q4"], ops["k4"], ops["qa4"], ops["ka4"], plain,
+                         128 ** -0.5, v8sum=sums, k4x=wide)
+        torch.cuda.synchronize()
+        assert torch.equal(out, plain.cpu()), (sums is not None, wide is not None)
+    ref, codes, tol = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    compare_codes(ops, codes[0], 0, 1, 6, 2, t)
+    assert_close(out.numpy(), ref, what=f"prefill w8 = 0 t={t}", tol=tol)
+
+
+def test_decode_bands_without_int8_tiles(module):
+    """The decode side of w8 = 0 bands: the newest prompt tile is INT4 (or skipped for [0, 0])."""
+    _decode_case(module, 333, torch.tensor(NO_INT8, dtype=torch.int32), steps=2, seed=5260)
+
+
 def test_config2_shape_slice(module):
     """Config 2 recipe (Hq 28 / Hk 4, log-uniform channel scales, one bf16 KV head) at T = 1024, batch 1."""
     print("\n[parity] config 2 slice (B1 T1024)", flush=True)

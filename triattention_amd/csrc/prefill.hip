@@ -71,8 +71,10 @@ __device__ __forceinline__ v4i k_frag(const uint8_t* __restrict__ k_lds, int F, 
 }
 
 // SUMS: the quantized P V accumulators start from the tile's -127 * sum(V8) in LDS (vs_lds, channel
-// order) instead of two MFMAs against a constant -127 operand
-template <int KIND, bool SUMS = false>
+// order) instead of two MFMAs against a constant -127 operand.  QMASK: a quantized tile that is the
+// query tile itself (an INT4 list that reaches the diagonal, w8 = 0): keys past the query row or
+// past t get level 0 and stay out of the tile max, as fp16 tiles mask them.
+template <int KIND, bool SUMS = false, bool QMASK = false>
 __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState& st, const v4i (&qf)[4], float qs,
                                              const float (&ks)[4], int col, bool masked, int qrow,
                                              const uint8_t* __restrict__ k_lds, const uint8_t* __restrict__ v_lds,
@@ -92,10 +94,21 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) s[kb] = mfma_i8(k_frag<KIND>(k_lds, kb * 4 + kstep, L), qf[kstep], s[kb]);
 
+  // Under QMASK the accumulators of masked keys become INT_MIN, which no
+  // accumulator reaches otherwise (8-bit: a positive float's bits; 4-bit:
+  // |16 * dot| < 2^26); the max and the P levels test for it.
+  if constexpr (QMASK) {
+    const int lim = min(qrow, a.t - 1) - col * BN - 4 * half;  // largest valid key offset in this lane
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (kb * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = INT_MIN;
+  }
+
   // score of accumulator r of block kb as a float: the magic float for 8-bit
   // codes (1.5*2^23 + dot), 16*dot for 4-bit codes (the MFMA saw 16*code keys;
-  // the 1/16 is folded into the slope, which is exact).  Only fp16 tiles can
-  // be the diagonal tile or reach past t: INT8/INT4 tiles are never masked.
+  // the 1/16 is folded into the slope, which is exact).  fp16 tiles mask here.
   auto score = [&](int kb, int r) -> float {
     float v = IS4 ? (float)s[kb][r] : __int_as_float(s[kb][r]);
     if constexpr (KIND == KF16) {
@@ -122,8 +135,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
         for (int r = 1; r < 8; ++r) mx = fmaxf(mx, score(kb, hg * 8 + r));
         if (mx > -__builtin_inff()) tile = fmaxf(tile, slope[kb * 2 + hg] * (mx - MAGIC));
       } else {
-        // never masked: the group's largest integer accumulator (the magic-offset dot product, or
-        // 16 * dot), whose order is the scores' order, converted once
+        // the group's largest integer accumulator (the magic-offset dot product, or 16 * dot), whose
+        // order is the scores' order, converted once (under QMASK a group with no valid key, all
+        // INT_MIN, leaves the tile max alone)
         const int g0 = hg * 8;
         int mx = max(max(s[kb][g0], s[kb][g0 + 1]), s[kb][g0 + 2]);
         mx = max(max(mx, s[kb][g0 + 3]), s[kb][g0 + 4]);
@@ -131,7 +145,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
         mx = max(mx, s[kb][g0 + 7]);
         // (|dot| < 2^22: the magic float minus 1.5 * 2^23 is the dot product exactly)
         const float d = IS4 ? (float)mx : __int_as_float(mx) - MAGIC;
-        tile = fmaxf(tile, slope[kb * 2 + hg] * d);
+        if (!QMASK || mx != INT_MIN) tile = fmaxf(tile, slope[kb * 2 + hg] * d);
       }
     }
   tile = xor32_max(tile);
@@ -206,7 +220,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, PrefillState&
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = qd * 4 + i, gi = kb * 2 + (r >> 3);
-          const float e = pexp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
+          float e = pexp2(__builtin_fmaf(slope[gi], score(kb, r), c[gi]));
+          if constexpr (QMASK) e = s[kb][r] == INT_MIN ? 0.f : e;
           y[i] = __float_as_uint(__builtin_fmaf(e, 255.f, PMAGIC_HALF));
         }
         pw[kb][qd] = pack_byte1(y[0], y[1], y[2], y[3]) ^ 0x7f7f7f7fu;  // 127 - P as s8
@@ -640,16 +655,18 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     };
     // tile i of kind KIND: wait for its records (and for every wave to finish
     // tile i-1, whose buffers receive tile i+1), start tile i+1's loads, compute
-    auto step = [&](auto kind, int i, const uint8_t* kc, const uint8_t* vc, const float* sc, const int32_t* vsc,
-                    uint8_t* kn, uint8_t* vn, float* sn, int32_t* vsn) __attribute__((always_inline)) {
+    auto step = [&](auto kind, auto mask, int i, const uint8_t* kc, const uint8_t* vc, const float* sc,
+                    const int32_t* vsc, uint8_t* kn, uint8_t* vn, float* sn,
+                    int32_t* vsn) __attribute__((always_inline)) {
       lds_wait();
       if (i + 1 < total) issue(i + 1, kn, vn, sn, vsn);
       const int col = tile_col(i);
       const float4 k4v = *reinterpret_cast<const float4*>(sc);
       const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
       constexpr int KIND = decltype(kind)::value;
+      constexpr bool QMASK = decltype(mask)::value != 0;
       if constexpr (KIND == KI8) prefill_tile<KI8, SUMS>(a, st, qf, qs8, ks, col, false, qrow, kc, vc, nullptr, vsc);
-      else prefill_tile<KIND, SUMS>(a, st, q4f, qs4, ks, col, false, qrow, kc, vc, nullptr, vsc);
+      else prefill_tile<KIND, SUMS, QMASK>(a, st, q4f, qs4, ks, col, QMASK, qrow, kc, vc, nullptr, vsc);
     };
     // Tiles [i, end) of one kind, the first in buffer set PARITY.  Each kind has a
     // loop of its own: with both kinds in one loop body the compiler copies the
@@ -665,19 +682,33 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
       int32_t* w0 = p ? vs_lds1 : vs_lds0;
       int32_t* w1 = p ? vs_lds0 : vs_lds1;
       for (; i < end; i += 2) {
-        step(kind, i, k0, v0, s0, w0, k1, v1, s1, w1);
-        if (i + 1 < end) step(kind, i + 1, k1, v1, s1, w1, k0, v0, s0, w0);
+        step(kind, Tag<0>{}, i, k0, v0, s0, w0, k1, v1, s1, w1);
+        if (i + 1 < end) step(kind, Tag<0>{}, i + 1, k1, v1, s1, w1, k0, v0, s0, w0);
       }
+    };
+    // The INT4 list ends at the query tile itself when w8 = 0 (then n8 = 0): that last tile is
+    // masked like the reference masks the last entry of a pass when it is the query tile
+    // (prefill_sm80.cu:328-329), in a step of its own outside the loop.
+    const bool diag4 = w8 <= 0 && n4 > 0;
+    const int end4 = total - (diag4 ? 1 : 0);
+    auto last = [&](auto kind) __attribute__((always_inline)) {
+      if (!diag4) return;
+      if ((total - 1) & 1)
+        step(kind, Tag<1>{}, total - 1, k_lds1, v_lds1, ks_lds1, vs_lds1, k_lds0, v_lds0, ks_lds0, vs_lds0);
+      else
+        step(kind, Tag<1>{}, total - 1, k_lds0, v_lds0, ks_lds0, vs_lds0, k_lds1, v_lds1, ks_lds1, vs_lds1);
     };
     __syncthreads();  // every wave is done with the F16 pass's LDS
     issue(0, k_lds0, v_lds0, ks_lds0, vs_lds0);
     run(Tag<KI8>{}, Tag<0>{}, 0, n8);
     if (k4x) {
-      if (n8 & 1) run(Tag<KQ4X>{}, Tag<1>{}, n8, total);
-      else run(Tag<KQ4X>{}, Tag<0>{}, n8, total);
+      if (n8 & 1) run(Tag<KQ4X>{}, Tag<1>{}, n8, end4);
+      else run(Tag<KQ4X>{}, Tag<0>{}, n8, end4);
+      last(Tag<KQ4X>{});
     } else {
-      if (n8 & 1) run(Tag<KQ4>{}, Tag<1>{}, n8, total);
-      else run(Tag<KQ4>{}, Tag<0>{}, n8, total);
+      if (n8 & 1) run(Tag<KQ4>{}, Tag<1>{}, n8, end4);
+      else run(Tag<KQ4>{}, Tag<0>{}, n8, end4);
+      last(Tag<KQ4>{});
     }
   }
 

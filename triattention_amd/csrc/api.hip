@@ -54,14 +54,14 @@ static void launch_one(K kernel, dim3 grid, const tri::DecodeArgs& d, hipStream_
   if (e0 || e1) hipExtLaunchKernelGGL(kernel, grid, dim3(64 * NW), 0, s, e0, e1, 0, d);
   else kernel<<<grid, 64 * NW, 0, s>>>(d);
 }
-template <int NW>
+template <int NW, bool T>
 static void launch_decode(int g, dim3 grid, const tri::DecodeArgs& d, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
   switch (g) {
-    case 1: launch_one<NW>(tri::decode_kernel<1, false, true, NW>, grid, d, s, e0, e1); break;
-    case 2: launch_one<NW>(tri::decode_kernel<2, false, true, NW>, grid, d, s, e0, e1); break;
-    case 3: launch_one<NW>(tri::decode_kernel<3, false, true, NW>, grid, d, s, e0, e1); break;
-    case 4: launch_one<NW>(tri::decode_kernel<4, false, true, NW>, grid, d, s, e0, e1); break;
-    default: launch_one<NW>(tri::decode_kernel<4, false, false, NW>, grid, d, s, e0, e1); break;
+    case 1: launch_one<NW>(tri::decode_kernel<1, false, true, NW, 2, T>, grid, d, s, e0, e1); break;
+    case 2: launch_one<NW>(tri::decode_kernel<2, false, true, NW, 2, T>, grid, d, s, e0, e1); break;
+    case 3: launch_one<NW>(tri::decode_kernel<3, false, true, NW, 2, T>, grid, d, s, e0, e1); break;
+    case 4: launch_one<NW>(tri::decode_kernel<4, false, true, NW, 2, T>, grid, d, s, e0, e1); break;
+    default: launch_one<NW>(tri::decode_kernel<4, false, false, NW, 2, T>, grid, d, s, e0, e1); break;
   }
 }
 
@@ -401,8 +401,14 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
       // a split), which interleave their dependency chains while the dispatcher queues the rest.
       int cus = 0;
       if (device_cus(&cus) != 0) return 1;
-      if ((int64_t)d.items > 8 * (int64_t)cus) launch_decode<2>(g, grid, d, s, ev_start, ev_stop);
-      else launch_decode<1>(g, grid, d, s, ev_start, ev_stop);
+      const bool two = (int64_t)d.items > 8 * (int64_t)cus;
+      if (d.tasks) {
+        if (two) launch_decode<2, true>(g, grid, d, s, ev_start, ev_stop);
+        else launch_decode<1, true>(g, grid, d, s, ev_start, ev_stop);
+      } else {
+        if (two) launch_decode<2, false>(g, grid, d, s, ev_start, ev_stop);
+        else launch_decode<1, false>(g, grid, d, s, ev_start, ev_stop);
+      }
     } else {
       // groups of up to 4 q-heads use the DUP lane layout (both wave halves on rows 0..3)
       switch (g) {

@@ -283,9 +283,14 @@ __device__ __forceinline__ void decode_exact(const DecodeArgs& a, int b, int kh,
 // quantization and metadata, take its tiles alternately (wave w: entries first
 // + w, first + w + 2, ...), and combine their running (m, l, o) in LDS at the
 // end, so that each SIMD holds two waves whose dependency chains interleave.
-template <int R, bool EXACT = false, bool DUP = false, int NW = 1, int W = 2>
+// TASKS: the launch has a task table (a.tasks, quantized heads only), whose rows give each split's
+// entries; a separate instantiation, so that the common path has no branch between the first
+// tile's record loads and the use of Q (at a join of two paths the compiler waits for every
+// outstanding load, which would hold the Q quantization until the records arrive).
+template <int R, bool EXACT = false, bool DUP = false, int NW = 1, int W = 2, bool TASKS = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) void decode_kernel(DecodeArgs a) {
   static_assert(NW == 1 || (NW == 2 && !EXACT), "two waves per workgroup only for quantized heads");
+  static_assert(!(TASKS && EXACT), "task tables list quantized heads only");
   __shared__ __align__(16) int8_t q8s[MAX_GROUP][D];
   __shared__ __align__(16) int8_t q4s[MAX_GROUP][D];
   __shared__ float qsc[MAX_GROUP], qsc4[MAX_GROUP];
@@ -306,7 +311,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
     const int w = (int)(((int64_t)blockIdx.x * a.scatter) % a.launched);
     if (w >= a.items) return;  // the padding item (whole workgroup, before any barrier)
     int item = w;
-    if (a.tasks != nullptr && !EXACT) {
+    if constexpr (TASKS) {
       // w-th listed split: its work item, entry count and every entry the prologue needs
       const int32_t* t = a.tasks + (int64_t)w * TASK_WORDS;
       task_w = *reinterpret_cast<const int4*>(t + 4 * (threadIdx.x & 63));
@@ -326,7 +331,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
   // A split past its head's kept tiles (ragged batches: most splits of the short sequences)
   // writes the empty partial (m = -FLT_MAX, l = 0, o = 0) and leaves.
   const int wv = NW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
-  if (a.tasks == nullptr || EXACT) split_range(a, (int64_t)b * a.hk + kh, split, first, last);
+  if constexpr (!TASKS) split_range(a, (int64_t)b * a.hk + kh, split, first, last);
   if (first >= last) {
     if (wv) return;
     const int L = threadIdx.x & 63, g = a.hq / a.hk;
@@ -445,82 +450,66 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
 
   // Entry first + L of the split (clamped into the entry table, so every lane
   // loads; the tile index is clamped too, as entries past the count are not
-  // tiles); lanes past the split's end get the out-of-range offsets.
-  Meta mc;  // the split's first tile
+  // tiles); lanes past the split's end get the out-of-range offsets.  Both
+  // paths only find the entries: the first tile's record loads, and the wait
+  // for Q after them, follow in straight-line code, where the compiler counts
+  // the loads issued after Q (those 16), so that the quantization overlaps
+  // the records' latency (after a join of two paths it waits for every
+  // outstanding load).
   int4 w = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);  // kslot, vslot, info | v8 << 9 | j << 10
   float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
-  if (a.tasks != nullptr && !EXACT) {
+  if constexpr (TASKS) {
     // the task table holds this lane's entry ready: the records stream right away
     w = make_int4(task_w.x, task_w.y, task_w.z, 0);
     ka = task_k;
-    Meta m0;
-    m0.kslot = __builtin_amdgcn_readlane(w.x, wv);
-    m0.info = __builtin_amdgcn_readlane(w.z & 0x1ff, wv);
-    load_k(m0);
-    mc = unpack(int4{__builtin_amdgcn_readlane(w.x, wv), __builtin_amdgcn_readlane(w.y, wv),
-                     __builtin_amdgcn_readlane(w.z, wv), 0});
-    load_v(mc);
-    meta[L] = w;
-    metk[L] = ka;
-    if (L == 0) {
-      meta[MAX_PER] = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);
-      metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
-    }
   } else {
     const bool valid = L < last - first;
     // (independent of the split's entry count, so these loads need not wait for it)
     const int64_t li = mbase + min(first + min(L, last - first - 1), a.maxn - 1);
     const int info = a.kinfo[li], er = a.entry[li], vs = a.slot[li];
-    // (keep the entry and slot loads ahead of the K loads: the tile-index loads below wait for
+    // (keep the entry and slot loads ahead of the K scales: the tile-index load below waits for
     // the entry, and waits count loads in issue order)
     __builtin_amdgcn_sched_barrier(0);
     const int is4 = valid ? (info >> 8) & 1 : 0;
     const int j = min(max(er & ENTRY_TILE, 0), a.tiles_max - 1);
-    // the K scales first: waits count loads in issue order, so the wait for them (before the
-    // LDS writes below) then holds no record load
     const float4 kl = *reinterpret_cast<const float4*>((is4 ? a.ka4 : a.ka) + (hb * a.tiles_max + j) * 4);
     __builtin_amdgcn_sched_barrier(0);
-    if (valid) w.x = (int)((unsigned)info >> 9);
-    {
-      // the wave's first tile's K streams (lane wv holds entry first + wv)
-      Meta m0;
-      m0.kslot = __builtin_amdgcn_readlane(w.x, wv);
-      m0.info = __builtin_amdgcn_readlane(info & 0x1ff, wv);
-      load_k(m0);
-    }
     // The V format: from the entry when the cache marked it there, else from fmt, one memory
     // round trip after the entry (a uniform branch: the marked path never waits for a fmt load).
-    // Then the first tile's V streams, while Q is quantized.
     int vf = (er & ENTRY_V8) ? 1 : 2;
     if (!__builtin_amdgcn_readfirstlane((int)__all(!valid || (er & ENTRY_VFMT)))) {
       vf = a.fmt[(int64_t)b * a.tiles_max + j];
       asm volatile("" ::"v"(vf));  // wait for it here, so that no wait follows the join
     }
     if (valid) {
-      w.y = vs;
-      w.z = (info & 0x1ff) | ((vf == 1) << 9) | (j << 10);
+      w = make_int4((int)((unsigned)info >> 9), vs, (info & 0x1ff) | ((vf == 1) << 9) | (j << 10), 0);
+      ka = kl;
     }
-    mc = unpack(int4{__builtin_amdgcn_readlane(w.x, wv), __builtin_amdgcn_readlane(w.y, wv),
-                     __builtin_amdgcn_readlane(w.z, wv), 0});
-    load_v(mc);
-    if (valid) ka = kl;
-    meta[L] = w;
-    metk[L] = ka;
-    if (L == 0) {
-      meta[MAX_PER] = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);
-      metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
-    }
+  }
+  // the wave's first tile (lane wv holds entry first + wv): K and V stream while Q is quantized
+  const Meta m0 = unpack(int4{__builtin_amdgcn_readlane(w.x, wv), __builtin_amdgcn_readlane(w.y, wv),
+                              __builtin_amdgcn_readlane(w.z, wv), 0});
+  load_k(m0);
+  load_v(m0);
+  Meta mc = m0;  // the current tile
+  float xv[16];  // this lane's 16 Q features
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint2 raw = qraw[i];
+    xv[4 * i] = bf16f(raw.x & 0xffffu);
+    xv[4 * i + 1] = bf16f(raw.x >> 16);
+    xv[4 * i + 2] = bf16f(raw.y & 0xffffu);
+    xv[4 * i + 3] = bf16f(raw.y >> 16);
+  }
+  meta[L] = w;
+  metk[L] = ka;
+  if (L == 0) {
+    meta[MAX_PER] = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);
+    metk[MAX_PER] = make_float4(1.f, 1.f, 1.f, 1.f);
   }
 
   // ---- in-kernel Q quantization of the g rows (common_device.cuh:291-315)
   {
-    float xv[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint2 raw = qraw[i];
-      xv[4 * i] = bf16f(raw.x & 0xffffu); xv[4 * i + 1] = bf16f(raw.x >> 16);
-      xv[4 * i + 2] = bf16f(raw.y & 0xffffu); xv[4 * i + 3] = bf16f(raw.y >> 16);
-    }
     rotate128_x16(xv, qt);
     float mx = 0.f;
 #pragma unroll

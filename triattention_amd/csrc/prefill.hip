@@ -533,12 +533,23 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   __shared__ __align__(16) float vms_lds[2 * D];  // the KV head's V mean and scale, for the epilogue
   const int rows = (a.t + BN - 1) / BN;
   // Launch sequence: BandTable's order is KV-head-major (prefill.py:24-25), so the workgroups running at
-  // any one time would all belong to one KV head.  Workgroup j takes entry (kv * rows + qd) * g + r of it
-  // for j = (qd * hk + kv) * g + r: the same entries, longest query tiles still first, but the KV heads
-  // interleaved, so exact heads (MFMA-heavy) run beside quantized ones (VALU-heavy) on the same CUs.
+  // any one time would all belong to one KV head.  Group t of the sequence is query tile qd = t / hk of
+  // KV head kv = t % hk, and its q-head r takes entry (kv * rows + qd) * g + r: the same entries,
+  // longest query tiles still first, but the KV heads interleaved, so exact heads (MFMA-heavy) run
+  // beside quantized ones (VALU-heavy) on the same CUs.  The group's q-heads read the same K/V tiles:
+  // when the groups fill whole rounds of the 8 XCDs (which receive the workgroups round-robin, XCD =
+  // blockIdx.x % 8 as gridDim.x is then a multiple of 8), XCD x's k-th workgroup, blockIdx.x = 8k + x,
+  // is q-head k % g of group 8 (k / g) + (x + k / g) % 8, so that a group's q-heads share one XCD's L2
+  // and each XCD still moves through the KV heads.
   int j = blockIdx.x;
   if ((int)gridDim.x == a.hq * rows) {
-    const int g0 = a.hq / a.hk, r = j % g0, t = j / g0;
+    const int g0 = a.hq / a.hk;
+    int r = j % g0, t = j / g0;
+    if ((a.hk * rows) % 8 == 0) {
+      const int x = j & 7, k = j >> 3, gk = k / g0;
+      r = k % g0;
+      t = gk * 8 + ((x + gk) & 7);
+    }
     j = ((t % a.hk) * rows + t / a.hk) * g0 + r;
   }
   const int task = __builtin_amdgcn_readfirstlane(a.order[j]), b = blockIdx.y;
@@ -636,14 +647,37 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     // (a local copy: reading the kernel argument inside the lambda would put the argument block in
     // private memory)
     const int32_t* v8s = SUMS ? a.v8s + rec0 * D : nullptr;
+    // Tile i's copies when it is of kind K (its K records: INT8, expanded INT4 or packed INT4), so
+    // that an INT4 loop issues its next tile's copies with no branch on the format (~19 SALU fewer
+    // per tile).
+    auto issue_as = [&](auto kind, int i, uint8_t* kd, uint8_t* vd, float* sd,
+                        int32_t* vsd) __attribute__((always_inline)) {
+      constexpr int K = decltype(kind)::value;
+      const int col = K == KI8 ? lo8 + i : lo4 + (i - n8);
+      if constexpr (K == KI8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd);
+      else if constexpr (K == KQ4X) lds_copy_buf<K8_BYTES>(rk4x, col * K8_BYTES, kd);
+      else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd);
+      lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd);
+      // the scales (and the V8 sums: 512 bytes, 16 per lane of the first 32) ride along in the same
+      // kind of copy, so reading them later waits on nothing but the records' own wait
+      if (tid == 0)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>((K == KI8 ? ka8 : ka4p) + col * 4),
+                                         (__attribute__((address_space(3))) void*)sd, 16, 0, 0);
+      if constexpr (SUMS) {
+        if (tid < 32)
+          __builtin_amdgcn_global_load_lds(static_cast<const void*>(v8s + col * D + tid * 4),
+                                           (__attribute__((address_space(3))) void*)vsd, 16, 0, 0);
+      }
+    };
+    // tile i of either list, i < total (one copy of the V, scale and sum copies for all three forms,
+    // which keeps the INT8 loop, whose next tile may start the INT4 list, shorter than three
+    // inlined issue_as forms)
     auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd, int32_t* vsd) __attribute__((always_inline)) {
       const int col = tile_col(i);
       if (i < n8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd);
       else if (k4x) lds_copy_buf<K8_BYTES>(rk4x, col * K8_BYTES, kd);
       else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd);
       lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd);
-      // the scales (and the V8 sums: 512 bytes, 16 per lane of the first 32) ride along in the same
-      // kind of copy, so reading them later waits on nothing but the records' own wait
       if (tid == 0)
         __builtin_amdgcn_global_load_lds(static_cast<const void*>((i < n8 ? ka8 : ka4p) + col * 4),
                                          (__attribute__((address_space(3))) void*)sd, 16, 0, 0);
@@ -659,11 +693,15 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
                     const int32_t* vsc, uint8_t* kn, uint8_t* vn, float* sn,
                     int32_t* vsn) __attribute__((always_inline)) {
       lds_wait();
-      if (i + 1 < total) issue(i + 1, kn, vn, sn, vsn);
+      constexpr int KIND = decltype(kind)::value;
+      if (i + 1 < total) {
+        // an INT4 tile is followed by one of its own kind, an INT8 tile by INT8 up to the list's end
+        if constexpr (KIND == KI8) issue(i + 1, kn, vn, sn, vsn);
+        else issue_as(kind, i + 1, kn, vn, sn, vsn);
+      }
       const int col = tile_col(i);
       const float4 k4v = *reinterpret_cast<const float4*>(sc);
       const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
-      constexpr int KIND = decltype(kind)::value;
       constexpr bool QMASK = decltype(mask)::value != 0;
       if constexpr (KIND == KI8) prefill_tile<KI8, SUMS>(a, st, qf, qs8, ks, col, false, qrow, kc, vc, nullptr, vsc);
       else prefill_tile<KIND, SUMS, QMASK>(a, st, q4f, qs4, ks, col, QMASK, qrow, kc, vc, nullptr, vsc);

@@ -160,12 +160,13 @@ def measured_traffic():
                                                      f"{TRAFFIC_PROFILE.name} (kernel sources {here})")
 
 
-MERGE_FORM = "auto"  # --merge-form: "four" keeps the four-wave merge for every tail
+MERGE_FORM = "auto"  # --merge-form: "device" launches tri_decode's merge, which picks its form itself
 
 
 def short_merge(cache, layer):
-    """Whether the decode op of ``layer`` merges with the one-wave form (the cache's choice by tail length,
-    unless --merge-form four)."""
+    """Whether the decode op of ``layer`` launches the one-wave merge kernel (the cache's choice by tail
+    length), rather than tri_decode's merge, which picks the same form on the device (--merge-form
+    device: the launch a graph captured by the model path replays)."""
     return MERGE_FORM == "auto" and cache.short_tail(layer)
 
 
@@ -694,9 +695,9 @@ def main():
     ap.add_argument("--issue-modes", default="", help="with --issue-probe: comma-separated modes (default all)")
     ap.add_argument("--ceiling-bytes", default="",
                     help="with --read-ceiling: comma-separated byte counts per launch (default: the C1 launch's)")
-    ap.add_argument("--merge-form", choices=("auto", "four"), default="auto",
-                    help="decode merge: the one-wave form while the tail holds at most 64 tokens (auto), or "
-                         "the four-wave form always")
+    ap.add_argument("--merge-form", choices=("auto", "device"), default="auto",
+                    help="decode merge launch: the one-wave kernel while the tail holds at most 64 tokens "
+                         "(auto), or always tri_decode's merge, which makes the same choice on the device")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--layers", type=int, default=28, help="C1 layers (own caches, one decode op each per token)")
     ap.add_argument("--c2-kinds", default="", help="with --only c2: also time the C2 inputs with every KV head of "
@@ -881,7 +882,7 @@ def main():
                        "runs decode; ms_per_step is per decode op; eager_ms_per_step launches each kernel from "
                        "Python",
         "merge": ("one wave per (sequence, q-head): the tail holds at most 64 tokens" if MERGE_FORM == "auto"
-                  else "four waves per (sequence, q-head) (--merge-form four)"),
+                  else "tri_decode's merge, its form chosen on the device (--merge-form device)"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

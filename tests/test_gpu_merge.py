@@ -4,9 +4,12 @@ The one-wave merge (tri_decode_short_tail, taken while the tail holds at most 64
 reference's merge order exactly (32-lane butterfly tail scores, split sums in four interleaved
 groups, tail tokens one after another), as the oracle does: given the oracle's own split partials
 (written into the cache's partial buffers, then the merge launched alone), its fp32 output must equal
-the oracle's bit for bit.  Whole decode steps (split kernel and merge) of both forms keep the
-2e-3 / 1e-3 bar (the split kernel's partials agree with the oracle's to fp32 rounding).  Tails past 64
-tokens and split counts past 16 (and 64) run the one-wave form's loops."""
+the oracle's bit for bit.  tri_decode's merge chooses its form on the device from the tail's length
+(the one-wave form up to 64 tokens, four waves beyond), so that a captured graph, replayed at steps
+with longer and longer tails, gives the bits of the eager steps: up to 64 tokens its output equals
+the one-wave form's bit for bit.  Whole decode steps (split kernel and merge) of both launches keep
+the 2e-3 / 1e-3 bar (the split kernel's partials agree with the oracle's to fp32 rounding).  Tails
+past 64 tokens and split counts past 16 (and 64) run the one-wave form's loops."""
 from __future__ import annotations
 
 import numpy as np
@@ -52,15 +55,18 @@ def test_merge_forms_against_the_oracle(module, tail, per, prompt):
                               ktail[b], vtail[b], bits(kd[b, :, 0]), bits(vd[b, :, 0]), step, h)
                for h in range(hq)] for b in range(batch)]
     refs = [np.stack([traces[b][h]["out"] for h in range(hq)]) for b in range(batch)]
+    forms = {}
     for short in (True, False):
         out = torch.full((batch, hq, 1, 128), float("nan"), device=dev)
         plan = cache.plan(0, qd.to(dev), kd.to(dev), out, scale)
         plan.run(qd.to(dev), kd.to(dev), vd.to(dev), out, short_tail=short)
         torch.cuda.synchronize()
-        got = out.cpu().numpy()
+        got = forms[short] = out.cpu().numpy()
         for b in range(batch):
-            assert_close(got[b, :, 0], refs[b], what=f"decode step, {'one' if short else 'four'}-wave merge, "
-                                                      f"seq {b}, splits {splits}")
+            assert_close(got[b, :, 0], refs[b], what=f"decode step, {'one-wave' if short else 'device-chosen'} "
+                                                      f"merge, seq {b}, splits {splits}")
+    if tail <= 64:  # the device chose the one-wave form: the same bits
+        assert np.array_equal(forms[True].view(np.uint32), forms[False].view(np.uint32))
     # the merge alone on the oracle's split partials: the one-wave form is the reference's order
     pm, pl, po = e[("partials", hq)]
     pm_h, pl_h, po_h = pm.cpu().numpy(), pl.cpu().numpy(), po.cpu().numpy().reshape(-1, 128)
@@ -75,14 +81,16 @@ def test_merge_forms_against_the_oracle(module, tail, per, prompt):
     pm.copy_(torch.from_numpy(pm_h))
     pl.copy_(torch.from_numpy(pl_h))
     po.copy_(torch.from_numpy(po_h.reshape(-1)))
-    out = torch.full((batch, hq, 1, 128), float("nan"), device=dev)
-    plan = cache.plan(0, qd.to(dev), kd.to(dev), out, scale)
-    plan.run(qd.to(dev), kd.to(dev), vd.to(dev), out, 2, short_tail=True)
-    torch.cuda.synchronize()
-    got = out.cpu().numpy()
-    for b in range(batch):
-        assert np.array_equal(got[b, :, 0].view(np.uint32), refs[b].view(np.uint32)), \
-            f"one-wave merge on the oracle's partials, seq {b}: max abs {np.abs(got[b, :, 0] - refs[b]).max():.3e}"
+    for short in (True, False) if tail <= 64 else (True,):
+        out = torch.full((batch, hq, 1, 128), float("nan"), device=dev)
+        plan = cache.plan(0, qd.to(dev), kd.to(dev), out, scale)
+        plan.run(qd.to(dev), kd.to(dev), vd.to(dev), out, 2, short_tail=short)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        for b in range(batch):
+            assert np.array_equal(got[b, :, 0].view(np.uint32), refs[b].view(np.uint32)), \
+                (f"{'one-wave' if short else 'device-chosen'} merge on the oracle's partials, seq {b}: "
+                 f"max abs {np.abs(got[b, :, 0] - refs[b]).max():.3e}")
     # both forms appended this step's token to the tail at the same slot
     ktail[:, :, step] = bits(kd[:, :, 0])
     vtail[:, :, step] = bits(vd[:, :, 0])

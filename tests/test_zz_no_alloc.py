@@ -48,7 +48,7 @@ def _compare(module, cache, seed):
     dev = torch.device("cuda")
     qd, kd, vd = (S.outlier_tensor(g, batch, 8, 1).to(dev), S.outlier_tensor(g, batch, 2, 1).to(dev),
                   S.outlier_tensor(g, batch, 2, 1).to(dev))
-    # tri_decode (split kernel and the four-wave merge, as tri_decode_noalloc launches them) with the
+    # tri_decode (split kernel and its merge, as tri_decode_noalloc launches them) with the
     # cache's own partial buffers
     ref = torch.full((batch, 8, 1, 128), float("nan"), device=dev)
     plan = cache.plan(0, qd, kd, ref, SCALE)
@@ -84,7 +84,7 @@ def test_noalloc_refuses_a_second_stream_while_the_first_is_pending(module):
                   S.outlier_tensor(g, 2, 2, 1).to(dev))
     ref = torch.full((2, 8, 1, 128), float("nan"), device=dev)
     plan = cache.plan(0, qd, kd, ref, SCALE)
-    plan.run(qd, kd, vd, ref)  # tri_decode: the four-wave merge, as tri_decode_noalloc
+    plan.run(qd, kd, vd, ref)  # tri_decode: its merge, as tri_decode_noalloc
     torch.cuda.synchronize()
     got_a, got_b = torch.full_like(ref, float("nan")), torch.full_like(ref, float("nan"))
     sa, sb = torch.cuda.Stream(), torch.cuda.Stream()

@@ -862,7 +862,7 @@ struct MergeArgs {
 // tail tokens' V rows), so a short tail costs one memory round trip; longer
 // tails and more splits continue in loops.  Tail scores: 8 lanes per token (16
 // channels each); tail values: 16 lanes per token (8 channels each).
-__global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
+__device__ __forceinline__ void merge_four(const MergeArgs& a) {
   __shared__ float ts[MAX_TAIL];  // tail scores
   __shared__ float vo[16][D];     // tail value sums of the 16 token groups
   __shared__ float wo[4][D];      // split sums of the four waves
@@ -1041,7 +1041,7 @@ namespace tri {
 // and 1 stages add in registers); the split sums run in four interleaved groups (splits w, w + 4, ...)
 // added in group order; the tail tokens are then added one after another.  XCD-aware (sequence,
 // q-head) mapping as decode_merge_kernel.
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_merge1_kernel(MergeArgs a) {
+__device__ __forceinline__ void merge_one(const MergeArgs& a) {
   __shared__ float ts[MAX_TAIL];  // tail scores
   int hq, b;
   {
@@ -1137,7 +1137,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
     krow(8 * u + tg, raw);
     score(raw, 8 * u + tg);
   }
-  __syncthreads();
+  // (one wave: its LDS accesses run in issue order, so the scores written above are seen below once
+  // the compiler keeps the order; no workgroup barrier, as merge_one also runs in a four-wave
+  // workgroup whose other waves have left)
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
   // ---- reference max over the splits and the tail
   float m = pms;
   for (int sp = 64 + L; sp < splits; sp += 64) m = fmaxf(m, a.pm[pbase + sp]);
@@ -1208,6 +1212,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
     static_cast<uint16_t*>(a.out)[o] = f32_to_bf16(r0);
     static_cast<uint16_t*>(a.out)[o + 1] = f32_to_bf16(r1);
   }
+}
+
+// Tokens the merge reads from the tail: the step's own token and those before it (the reference:
+// step, clamped to max_tail - 1); with tail growth the tail holds step - tail_base tokens.
+__device__ __forceinline__ int merge_tail(const MergeArgs& a) {
+  const int64_t held = *a.step - (a.tail_base != nullptr ? *a.tail_base : 0);
+  return (int)max((int64_t)0, min((int64_t)a.max_tail - 1, held)) + 1;
+}
+
+// The merge with the form chosen on the device from the tail's length: one wave (merge_one, the
+// reference's order) while the tail holds at most SHORT_TAIL tokens, four waves (merge_four) beyond.
+// A captured graph replays one launch at steps whose tails grow, so the choice cannot be the host's:
+// made here, every step of an eager run and of a replay takes the same form and gives the same bits.
+// With the one-wave form the other three waves leave at once (a barrier waits only for the waves
+// still running).
+constexpr int SHORT_TAIL = 64;
+__global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
+  if (merge_tail(a) <= SHORT_TAIL) {
+    if (threadIdx.x >= 64) return;
+    merge_one(a);
+  } else {
+    merge_four(a);
+  }
+}
+
+// The one-wave form alone, whatever the tail (tri_decode_short_tail).
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_merge1_kernel(MergeArgs a) {
+  merge_one(a);
 }
 
 }  // namespace tri

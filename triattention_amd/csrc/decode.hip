@@ -450,12 +450,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(W))) vo
 
   // Entry first + L of the split (clamped into the entry table, so every lane
   // loads; the tile index is clamped too, as entries past the count are not
-  // tiles); lanes past the split's end get the out-of-range offsets.  Both
-  // paths only find the entries: the first tile's record loads, and the wait
-  // for Q after them, follow in straight-line code, where the compiler counts
-  // the loads issued after Q (those 16), so that the quantization overlaps
-  // the records' latency (after a join of two paths it waits for every
-  // outstanding load).
+  // tiles); lanes past the split's end get the out-of-range offsets.  Either
+  // source only finds the entries; the first tile's record loads and the use
+  // of Q follow them.  With a task table (TASKS) that is straight-line code,
+  // so the compiler waits for Q with the 16 record loads still in flight and
+  // the quantization overlaps their latency (after a join of two paths it
+  // waits for every outstanding load).
   int4 w = make_int4(NO_RECORD, NO_RECORD, (1 << 9), 0);  // kslot, vslot, info | v8 << 9 | j << 10
   float4 ka = make_float4(1.f, 1.f, 1.f, 1.f);
   if constexpr (TASKS) {
@@ -1225,8 +1225,7 @@ __device__ __forceinline__ int merge_tail(const MergeArgs& a) {
 // reference's order) while the tail holds at most SHORT_TAIL tokens, four waves (merge_four) beyond.
 // A captured graph replays one launch at steps whose tails grow, so the choice cannot be the host's:
 // made here, every step of an eager run and of a replay takes the same form and gives the same bits.
-// With the one-wave form the other three waves leave at once (a barrier waits only for the waves
-// still running).
+// With the one-wave form the other three waves leave at once (merge_one has no workgroup barrier).
 constexpr int SHORT_TAIL = 64;
 __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
   if (merge_tail(a) <= SHORT_TAIL) {

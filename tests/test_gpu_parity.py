@@ -475,6 +475,24 @@ def test_bands_without_int8_tiles(module, t):
     assert_close(out.numpy(), ref, what=f"prefill w8 = 0 t={t}", tol=tol)
 
 
+ODD_BANDS = [[4, 2], [0, 2], [5, 5], [0, 0]]
+
+
+def test_unusual_bands(module):
+    """Bands whose lists degenerate: w4 < w8 (no INT4 tiles), [0, 2] (one or two INT4 tiles ending at the
+    query tile), [5, 5] (INT8 only) and [0, 0] (the two fp16 tiles only), batch 2, t = 257 (the last
+    query tile holds one row); prefill and three decode steps against the oracle."""
+    print("\n[parity] prefill t=257 batch 2 with unusual bands", flush=True)
+    q, k, v = small(3700, 2, 4, 2, 257)
+    bands = torch.tensor(ODD_BANDS, dtype=torch.int32)
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5)
+    ref, codes, tol = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    for b in range(2):
+        compare_codes(ops, codes[b], b, 2, 4, 2, 257)
+    assert_close(out.numpy(), ref, what="prefill unusual bands", tol=tol)
+    _decode_case(module, 257, bands, batch=2, steps=3, seed=5270, hq=4, hk=2)
+
+
 def test_decode_bands_without_int8_tiles(module):
     """The decode side of w8 = 0 bands: the newest prompt tile is INT4 (or skipped for [0, 0])."""
     _decode_case(module, 333, torch.tensor(NO_INT8, dtype=torch.int32), steps=2, seed=5260)

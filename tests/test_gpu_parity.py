@@ -493,6 +493,20 @@ def test_unusual_bands(module):
     _decode_case(module, 257, bands, batch=2, steps=3, seed=5270, hq=4, hk=2)
 
 
+@pytest.mark.parametrize("hq,hk,t", [(4, 4, 256), (8, 8, 130), (16, 2, 512)])
+def test_prefill_group_sizes(module, hq, hk, t):
+    """One q-head per KV head (the launch sequence's XCD rounds with groups of one: 4 x 4 query tiles
+    fill two rounds of 8; 8 x 3 do not) and groups of 8, every band kind."""
+    print(f"\n[parity] prefill hq {hq} hk {hk} t {t}", flush=True)
+    q, k, v = small(3800 + hq + t, 1, hq, hk, t)
+    kinds = [[INF, INF], [1, INF], [2, 4], [0, 3]]
+    bands = torch.tensor([kinds[h % 4] for h in range(hq)], dtype=torch.int32)
+    out, ops, _ = run_prefill(module, q, k, v, bands, 128 ** -0.5)
+    ref, codes, tol = oracle_prefill(q, k, v, bands, 128 ** -0.5)
+    compare_codes(ops, codes[0], 0, 1, hq, hk, t)
+    assert_close(out.numpy(), ref, what=f"prefill hq {hq} hk {hk}", tol=tol)
+
+
 def test_decode_bands_without_int8_tiles(module):
     """The decode side of w8 = 0 bands: the newest prompt tile is INT4 (or skipped for [0, 0])."""
     _decode_case(module, 333, torch.tensor(NO_INT8, dtype=torch.int32), steps=2, seed=5260)

@@ -103,13 +103,14 @@ def test_bf16_output_within_one_ulp(module):
     assert bool((torch.abs(out16 - r) <= ulp + 1e-30).all())
 
 
-def _decode_case(module, prompt, bands, batch=1, steps=3, max_tail=8, seed=5000, hq=6, hk=2, per=None):
-    print(f"\n[parity] decode prompt={prompt} batch={batch} steps={steps} per={per}", flush=True)
+def _decode_case(module, prompt, bands, batch=1, steps=3, max_tail=8, seed=5000, hq=6, hk=2, per=None, tasks=True):
+    print(f"\n[parity] decode prompt={prompt} batch={batch} steps={steps} per={per} tasks={tasks}", flush=True)
     q, k, v = small(seed, batch, hq, hk, prompt)
     scale = 128 ** -0.5
     cache = DecodeCache(module, max_tail=max_tail)
     cache.out_dtype = torch.float32
     cache.per = per
+    cache.tasks = tasks
     _, ops, pre = run_prefill(module, q, k, v, bands, scale, decode_cache=cache)
     ref_codes = [O.prefill_codes(bits(q[b]), bits(k[b]), bits(v[b]), bands.numpy(), decode_cache=True)
                  for b in range(batch)]
@@ -165,6 +166,19 @@ def test_decode_two_waves_per_workgroup(module, hq, hk, per):
     batch = (9 * module.device_cus()) // (splits * hk) + 1
     _decode_case(module, prompt, bands, batch=batch, steps=2, max_tail=4, seed=5300 + 10 * g + per, hq=hq, hk=hk,
                  per=per)
+
+
+@pytest.mark.parametrize("per", [1, 3])
+def test_decode_two_waves_per_workgroup_without_task_table(module, per):
+    """The gather path (no task table: each split finds its entries in the cache's metadata) with a grid
+    larger than the resident one-wave workgroups, so two waves per workgroup."""
+    hq, hk = 24, 8
+    kinds = [[INF, INF], [1, INF], [2, 5], [0, INF]]
+    bands = torch.tensor([kinds[h % 4] for h in range(hk) for _ in range(hq // hk)], dtype=torch.int32)
+    splits = -(-10 // per)
+    batch = (9 * module.device_cus()) // (splits * hk) + 1
+    _decode_case(module, 600, bands, batch=batch, steps=2, max_tail=4, seed=5500 + per, hq=hq, hk=hk, per=per,
+                 tasks=False)
 
 
 def test_decode_short_prompt(module):

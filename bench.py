@@ -165,11 +165,11 @@ def measured_traffic():
 MERGE_FORM = "auto"  # --merge-form: "device" launches tri_decode's merge, which picks its form itself
 
 
-def short_merge(cache, layer):
+def short_merge(cache, layer, hq):
     """Whether the decode op of ``layer`` launches the one-wave merge kernel (the cache's choice by tail
-    length), rather than tri_decode's merge, which picks the same form on the device (--merge-form
-    device: the launch a graph captured by the model path replays)."""
-    return MERGE_FORM == "auto" and cache.short_tail(layer)
+    length and grid size), rather than tri_decode's merge, which picks the same form on the device
+    (--merge-form device: the launch a graph captured by the model path replays)."""
+    return MERGE_FORM == "auto" and cache.short_tail(layer, hq)
 
 
 def kernel_events(n, stream):
@@ -399,7 +399,7 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
         qd, kd, vd = toks[warmup + i]
         layer = i % C3_GRAPH_LAYERS
         plans[layer].run(qd, kd, vd, out, 1, events=evs[i])
-        plans[layer].run(qd, kd, vd, out, 2, short_tail=short_merge(cache, layer))
+        plans[layer].run(qd, kd, vd, out, 2, short_tail=short_merge(cache, layer, hq))
         if layer == C3_GRAPH_LAYERS - 1:
             cache.advance()
     end.record(stream)
@@ -410,7 +410,7 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
     def token():
         qd, kd, vd = toks[warmup]
         for layer in range(C3_GRAPH_LAYERS):
-            plans[layer].run(qd, kd, vd, out, short_tail=short_merge(cache, layer))
+            plans[layer].run(qd, kd, vd, out, short_tail=short_merge(cache, layer, hq))
         cache.advance()
     graph_ms = graph_steps(token, steps, stream) / C3_GRAPH_LAYERS
     ms = eager_ms
@@ -815,7 +815,7 @@ def main():
         # counter advances once per token, after the last layer
         qd, kd, vd = toks[i % total_steps]
         plan = plans[i % layers]
-        short = short_merge(cache, i % layers)
+        short = short_merge(cache, i % layers, hq)
         if ev is None:
             plan.run(qd, kd, vd, out, short_tail=short)
         else:
@@ -860,11 +860,12 @@ def main():
     dec_ms = statistics.fmean(ev[0].elapsed_time(ev[1]) for ev in evs)
 
     # The step as the model path runs it: one token (every layer's decode op, then the step
-    # advance) captured as a HIP graph and replayed; ms_per_step is per decode op (per layer).
+    # advance) captured as a HIP graph and replayed, the merge launched as tri_decode's, which picks
+    # its form on the device at every replay (as a graph the model path captures does); ms_per_step
+    # is per decode op (per layer).
     def token():
         for layer in range(layers):
-            plans[layer].run(*toks[(1 + args.warmup + layer) % total_steps], out,
-                             short_tail=short_merge(cache, layer))
+            plans[layer].run(*toks[(1 + args.warmup + layer) % total_steps], out)
         cache.advance()
     tokens = max(4, -(-args.steps // layers))
     ms_per_step = graph_steps(token, tokens, stream) / layers
@@ -896,7 +897,9 @@ def main():
                        "each -- then the step advance) captured as a HIP graph and replayed, as the model path "
                        "runs decode; ms_per_step is per decode op; eager_ms_per_step launches each kernel from "
                        "Python",
-        "merge": ("one wave per (sequence, q-head): the tail holds at most 64 tokens" if MERGE_FORM == "auto"
+        "merge": ("eager steps: the one-wave kernel (tails of at most 16 tokens on a grid of at least 2 "
+                  "workgroups per CU: C1's 768 on 256 CUs); graph replays: tri_decode's merge, which makes the "
+                  "same choice on the device" if MERGE_FORM == "auto"
                   else "tri_decode's merge, its form chosen on the device (--merge-form device)"),
         "higher_is_better": True,
         "scaling": "weak",

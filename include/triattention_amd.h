@@ -90,9 +90,10 @@ int tri_pack_exact(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, cons
                    void* kx, void* vx, void* stream);
 
 /* Replaces decode (common_host.cuh:47-87), batched and ragged.  The merge takes its form on the
- * device from *step and *tail_base: one wave per (sequence, q-head), in the reference's order
- * (common_device.cuh:373-469), while the tail holds at most 64 tokens, four waves beyond (within fp32
- * rounding of it); a captured graph replayed at later steps therefore takes the eager form every time.
+ * device: one wave per (sequence, q-head), in the reference's order (common_device.cuh:373-469), while
+ * the tail (from *step and *tail_base) holds at most 16 tokens and batch * hq is at least twice the
+ * device's CU count, four waves otherwise (within fp32 rounding of it); a captured graph replayed at
+ * later steps therefore takes the form an eager call would take at every step.
  * q bf16 [batch][hq][1][128] (strides q_sb, q_sh); k8c/k4c/v8c/v4c compacted
  * records; ka/ka4 f32 [batch][hk][tiles_max][4]; entry/kinfo/slot int32
  * [batch][hk][maxn] (kinfo = rowmask | is4 << 8 | kslot << 9); count int32
@@ -168,14 +169,14 @@ int tri_decode_merge(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c,
                      void* stream);
 
 /* tri_decode and tri_decode_merge with the merge run as one wave per (sequence, q-head) whatever the
- * tail: no reference counterpart.  Every load of the first 64 tail tokens and 16 splits is issued at
- * once and no workgroup barrier is needed, so it is the faster merge while the tail (the step minus
- * the tokens moved into the cache) holds at most 64 tokens; any tail length gives a correct result,
- * longer ones more slowly.  Its arithmetic follows the reference's merge order
- * (common_device.cuh:373-469) exactly: tail scores as 32-lane butterfly sums, split sums in four
- * interleaved groups, tail tokens one after another.  tri_decode's merge takes this form by itself
- * (chosen on the device) while the tail holds at most 64 tokens, with the same bits, and four waves per
- * (sequence, q-head) beyond.  Same arguments as tri_decode. */
+ * tail and grid: no reference counterpart.  Every load of the first 64 tail tokens and 16 splits is
+ * issued at once and no workgroup barrier is needed, so on a grid of at least two (sequence, q-head)
+ * workgroups per CU it is the faster merge while the tail (the step minus the tokens moved into the
+ * cache) holds at most 16 tokens; any tail length gives a correct result, longer ones more slowly.
+ * Its arithmetic follows the reference's merge order (common_device.cuh:373-469) exactly: tail scores
+ * as 32-lane butterfly sums, split sums in four interleaved groups, tail tokens one after another.
+ * tri_decode's merge takes this form by itself (chosen on the device) under those two conditions, with
+ * the same bits.  Same arguments as tri_decode. */
 int tri_decode_short_tail(const void* q, int64_t q_sb, int64_t q_sh, const void* k8c, const void* k4c,
                           const float* ka, const float* ka4, const int32_t* entry, const int32_t* kinfo,
                           const int32_t* count, const int32_t* fmt, const int32_t* slot, const void* v8c,

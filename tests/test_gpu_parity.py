@@ -290,7 +290,7 @@ def test_timed_split_launch_matches_untimed(module):
     for e in events:
         e.record(stream)
     plan.run(qd, kd, vd, out, 1, events=events)
-    plan.run(qd, kd, vd, out, 2, short_tail=cache.short_tail(0))  # the merge form the untimed call took
+    plan.run(qd, kd, vd, out, 2, short_tail=cache.short_tail(0, hq))  # the merge form the untimed call took
     torch.cuda.synchronize()
     assert torch.equal(untimed.view(torch.int32), out.cpu().view(torch.int32))
     assert events[0].elapsed_time(events[1]) > 0.0

@@ -389,6 +389,13 @@ static int decode_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k8
   mg.splits = splits;
   mg.max_tail = max_tail;
   mg.sm_log2 = d.sm_log2;
+  {
+    // the one-wave merge form pays on grids of at least SHORT_WIDE (sequence, q-head) workgroups per CU
+    // (the rule DecodeCache.short_tail mirrors for its eager launches)
+    int cus = 0;
+    if (device_cus(&cus) != 0) return 1;
+    mg.wide = (int64_t)batch * hq >= (int64_t)tri::SHORT_WIDE * cus ? 1 : 0;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (phase & 1) {
     const dim3 grid(d.launched);

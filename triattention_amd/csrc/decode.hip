@@ -64,6 +64,8 @@ struct DecodeArgs {
 };
 
 constexpr int MAX_TAIL = 1024;
+// the merge's one-wave form: grids of at least SHORT_WIDE (sequence, q-head) workgroups per CU
+constexpr int SHORT_WIDE = 2;
 // entry words: bits 0-28 the tile index; bit 30 set (extension) marks that bit 29 holds the
 // tile's V format (1 = INT8 V), so the kernel need not read fmt for it
 constexpr int ENTRY_TILE = (1 << 29) - 1, ENTRY_V8 = 1 << 29, ENTRY_VFMT = 1 << 30;
@@ -852,6 +854,7 @@ struct MergeArgs {
   int64_t qsb, qsh, tsb, tsh, tst, csb, csh, osb, osh;
   int hq, hk, splits, max_tail;
   float sm_log2;
+  int wide;  // the grid has at least SHORT_WIDE workgroups per CU (the one-wave form may pay)
 };
 
 // LSE merge of the split partials with the exact bf16 tail
@@ -1221,14 +1224,18 @@ __device__ __forceinline__ int merge_tail(const MergeArgs& a) {
   return (int)max((int64_t)0, min((int64_t)a.max_tail - 1, held)) + 1;
 }
 
-// The merge with the form chosen on the device from the tail's length: one wave (merge_one, the
-// reference's order) while the tail holds at most SHORT_TAIL tokens, four waves (merge_four) beyond.
-// A captured graph replays one launch at steps whose tails grow, so the choice cannot be the host's:
-// made here, every step of an eager run and of a replay takes the same form and gives the same bits.
-// With the one-wave form the other three waves leave at once (merge_one has no workgroup barrier).
-constexpr int SHORT_TAIL = 64;
+// The merge with the form chosen on the device: one wave (merge_one, the reference's order) while
+// the tail holds at most SHORT_TAIL tokens on a grid of at least SHORT_WIDE workgroups per CU (a.wide),
+// four waves (merge_four) otherwise.  Measured (kernel durations, Hq 28): on 896 workgroups the one-wave
+// form takes 5.5 / 6.1 / 7.6 / 10.7 us at tails of 4 / 16 / 32 / 64 tokens against 6.8 / 6.8 / 6.8 / 7.6
+// for four waves; on 448 or fewer four waves are as fast or faster at every tail (4.3-5.5 us).  A
+// captured graph replays one launch at steps whose tails grow, so the choice cannot be the host's:
+// made here (and by the host's eager choice with the same rule), every step of an eager run and of a
+// replay takes the same form and gives the same bits.  With the one-wave form the other three waves
+// leave at once (merge_one has no workgroup barrier).
+constexpr int SHORT_TAIL = 16;
 __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
-  if (merge_tail(a) <= SHORT_TAIL) {
+  if (a.wide && merge_tail(a) <= SHORT_TAIL) {
     if (threadIdx.x >= 64) return;
     merge_one(a);
   } else {

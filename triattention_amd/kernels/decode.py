@@ -458,11 +458,13 @@ class DecodeCache:
         plan = self.plan(layer, q, k, out, scale)
         if st.grow_tiles:
             self._spill_plan(e).run()
-        plan.run(q, k, v, out, short_tail=self.short_tail(layer))
+        plan.run(q, k, v, out, short_tail=self.short_tail(layer, q.shape[1]))
         return out
 
-    # the merge runs as one wave per (sequence, q-head) while the tail holds at most this many tokens
-    SHORT_TAIL = 64
+    # the merge runs as one wave per (sequence, q-head) while the tail holds at most SHORT_TAIL tokens on a
+    # grid of at least SHORT_WIDE (sequence, q-head) workgroups per CU (the rule of tri_decode's merge)
+    SHORT_TAIL = 16
+    SHORT_WIDE = 2
 
     def tail_tokens(self, layer):
         """Tokens the merge of ``layer``'s next decode step reads from its tail (host mirror): the
@@ -474,13 +476,16 @@ class DecodeCache:
             tb += BN
         return min(self.max_tail - 1, max(0, self.host_step - tb)) + 1
 
-    def short_tail(self, layer):
-        """Whether ``layer``'s next merge takes the one-wave form: tail_tokens at most SHORT_TAIL.  A step
-        being captured is replayed at later steps, with longer tails, so it takes the one-wave form only
-        if no tail can outgrow SHORT_TAIL (max_tail at most SHORT_TAIL); either form is correct for any
-        tail, the other one only slower."""
+    def short_tail(self, layer, hq):
+        """Whether ``layer``'s next merge (hq q-heads) launches the one-wave kernel: tail_tokens at most
+        SHORT_TAIL on a grid of at least SHORT_WIDE (sequence, q-head) workgroups per CU, the rule by
+        which tri_decode's merge picks its form on the device, so that an eager step gives the bits a
+        replayed graph gives.  A step being captured launches tri_decode's merge, which makes the choice
+        itself at every replay (a captured one-wave launch would keep that form at later, longer tails)."""
         if self.capturing:
-            return self.max_tail <= self.SHORT_TAIL
+            return False
+        if self.layers[layer]["batch"] * hq < self.SHORT_WIDE * self.module.device_cus():
+            return False
         return self.tail_tokens(layer) <= self.SHORT_TAIL
 
     def plan(self, layer, q, k, out, scale):

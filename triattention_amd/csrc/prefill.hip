@@ -277,18 +277,21 @@ __device__ __forceinline__ void lds_copy_async(const uint8_t* src, uint8_t* dst)
   }
 }
 
-// The same copy from a buffer resource at byte offset soff (uniform): the lane
-// offsets are constants, so no per-copy address arithmetic.
+// The same copy from a buffer resource at byte offset soff (uniform), wave w
+// moving the w-th half of the record (whalf = w * BYTES / 2, computed once per
+// kernel): one LDS base (M0) and one scalar offset per record and wave, the
+// 1 KiB steps in the instruction's offset field, which moves the global and
+// the LDS address alike.
 template <int BYTES>
-__device__ __forceinline__ void lds_copy_buf(__amdgpu_buffer_rsrc_t src, int soff, uint8_t* dst) {
-  static_assert(BYTES % 2048 == 0, "copies move 2 KiB per step");
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+__device__ __forceinline__ void lds_copy_buf(__amdgpu_buffer_rsrc_t src, int soff, uint8_t* dst, int whalf) {
+  static_assert(BYTES == 4096 || BYTES == 8192, "records of 4 or 8 KiB");
   const int lane = (threadIdx.x & 63) * 16;
-#pragma unroll
-  for (int i = 0; i < BYTES / 2048; ++i) {
-    const int off = i * 2048 + wave * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (__attribute__((address_space(3))) void*)(dst + off), 16, lane,
-                                             soff + off, 0, 0);
+  auto* d = (__attribute__((address_space(3))) void*)(dst + whalf);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, d, 16, lane, soff + whalf, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, d, 16, lane, soff + whalf, 1024, 0);
+  if constexpr (BYTES == 8192) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, d, 16, lane, soff + whalf, 2048, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, d, 16, lane, soff + whalf, 3072, 0);
   }
 }
 
@@ -403,10 +406,11 @@ __device__ __forceinline__ void prefill_exact(const PrefillArgs& a, int b, int q
       __builtin_amdgcn_make_buffer_rsrc((void*)kx, (short)0, tiles * KX_BYTES, 0x00020000);
   const __amdgpu_buffer_rsrc_t rvx =
       __builtin_amdgcn_make_buffer_rsrc((void*)vx, (short)0, tiles * KX_BYTES, 0x00020000);
+  const int whalf = __builtin_amdgcn_readfirstlane(wave) * (KX_BYTES / 4);
   auto issue = [&](int st, uint8_t* kd, uint8_t* vd) {
     const int off = (st >> 1) * KX_BYTES + (st & 1) * (KX_BYTES / 2);
-    lds_copy_buf<KX_BYTES / 2>(rkx, off, kd);
-    lds_copy_buf<KX_BYTES / 2>(rvx, off, vd);
+    lds_copy_buf<KX_BYTES / 2>(rkx, off, kd, whalf);
+    lds_copy_buf<KX_BYTES / 2>(rvx, off, vd, whalf);
   };
   issue(0, k0, v0);
   // tiles before the diagonal: no mask
@@ -528,8 +532,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   // an fp16 V record uses both V buffers
   __shared__ __align__(16) uint8_t k_lds0[K8_BYTES], k_lds1[K8_BYTES];
   __shared__ __align__(16) uint8_t v_lds0[V8_BYTES], v_lds1[V8_BYTES];
-  __shared__ __align__(16) float ks_lds0[4], ks_lds1[4];  // the tile's 4 K group scales
-  __shared__ __align__(16) int32_t vs_lds0[SUMS ? D : 4], vs_lds1[SUMS ? D : 4];  // its -127 * V8 sums
+  // the tile's -127 * V8 sums (D words, with SUMS) followed by its 4 K group scales as an INT8 tile
+  // and as an INT4 tile, which one copy instruction brings together
+  constexpr int VK = SUMS ? D : 0;
+  __shared__ __align__(16) int32_t vk_lds0[VK + 8], vk_lds1[VK + 8];
   __shared__ __align__(16) float vms_lds[2 * D];  // the KV head's V mean and scale, for the epilogue
   const int rows = (a.t + BN - 1) / BN;
   // Launch sequence: BandTable's order is KV-head-major (prefill.py:24-25), so the workgroups running at
@@ -647,64 +653,68 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     // (a local copy: reading the kernel argument inside the lambda would put the argument block in
     // private memory)
     const int32_t* v8s = SUMS ? a.v8s + rec0 * D : nullptr;
+    // each wave's half of a record (the copies' per-wave offsets, uniform)
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int kh8 = wv * (K8_BYTES / 2), kh4 = wv * (K4_BYTES / 2), vh8 = wv * (V8_BYTES / 2);
+    // The tile's V8 sums and both lists' K scales in one instruction of wave 0: lanes 0..31 copy 16
+    // bytes of sums each (with SUMS), the next lane the INT8 list's scales and the one after it the
+    // INT4 list's (at words VK and VK + 4), each lane from its own base and stride, so that reading
+    // them later waits on nothing but the records' own wait.
+    const int nsmall = VK / 4 + 2;
+    const uint8_t* sbase = nullptr;
+    int sshift = 4;
+    if (tid < nsmall) {
+      if (SUMS && tid < 32) {
+        sbase = reinterpret_cast<const uint8_t*>(v8s) + tid * 16;
+        sshift = 9;  // D int32 words per tile
+      } else {
+        sbase = reinterpret_cast<const uint8_t*>(tid == VK / 4 || ka4p == nullptr ? ka8 : ka4p);
+      }
+    }
+    auto issue_small = [&](int col, int32_t* vkd) __attribute__((always_inline)) {
+      if (tid < nsmall)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(sbase + ((int64_t)col << sshift)),
+                                         (__attribute__((address_space(3))) void*)vkd, 16, 0, 0);
+    };
     // Tile i's copies when it is of kind K (its K records: INT8, expanded INT4 or packed INT4), so
-    // that an INT4 loop issues its next tile's copies with no branch on the format (~19 SALU fewer
-    // per tile).
-    auto issue_as = [&](auto kind, int i, uint8_t* kd, uint8_t* vd, float* sd,
-                        int32_t* vsd) __attribute__((always_inline)) {
+    // that an INT4 loop issues its next tile's copies with no branch on the format.
+    auto issue_as = [&](auto kind, int i, uint8_t* kd, uint8_t* vd, int32_t* vkd) __attribute__((always_inline)) {
       constexpr int K = decltype(kind)::value;
       const int col = K == KI8 ? lo8 + i : lo4 + (i - n8);
-      if constexpr (K == KI8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd);
-      else if constexpr (K == KQ4X) lds_copy_buf<K8_BYTES>(rk4x, col * K8_BYTES, kd);
-      else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd);
-      lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd);
-      // the scales (and the V8 sums: 512 bytes, 16 per lane of the first 32) ride along in the same
-      // kind of copy, so reading them later waits on nothing but the records' own wait
-      if (tid == 0)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>((K == KI8 ? ka8 : ka4p) + col * 4),
-                                         (__attribute__((address_space(3))) void*)sd, 16, 0, 0);
-      if constexpr (SUMS) {
-        if (tid < 32)
-          __builtin_amdgcn_global_load_lds(static_cast<const void*>(v8s + col * D + tid * 4),
-                                           (__attribute__((address_space(3))) void*)vsd, 16, 0, 0);
-      }
+      if constexpr (K == KI8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd, kh8);
+      else if constexpr (K == KQ4X) lds_copy_buf<K8_BYTES>(rk4x, col * K8_BYTES, kd, kh8);
+      else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd, kh4);
+      lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd, vh8);
+      issue_small(col, vkd);
     };
-    // tile i of either list, i < total (one copy of the V, scale and sum copies for all three forms,
-    // which keeps the INT8 loop, whose next tile may start the INT4 list, shorter than three
-    // inlined issue_as forms)
-    auto issue = [&](int i, uint8_t* kd, uint8_t* vd, float* sd, int32_t* vsd) __attribute__((always_inline)) {
-      const int col = tile_col(i);
-      if (i < n8) lds_copy_buf<K8_BYTES>(rk8, col * K8_BYTES, kd);
-      else if (k4x) lds_copy_buf<K8_BYTES>(rk4x, col * K8_BYTES, kd);
-      else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd);
-      lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd);
-      if (tid == 0)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>((i < n8 ? ka8 : ka4p) + col * 4),
-                                         (__attribute__((address_space(3))) void*)sd, 16, 0, 0);
-      if constexpr (SUMS) {
-        if (tid < 32)
-          __builtin_amdgcn_global_load_lds(static_cast<const void*>(v8s + col * D + tid * 4),
-                                           (__attribute__((address_space(3))) void*)vsd, 16, 0, 0);
-      }
+    // tile i of either list, i < total (the INT8 loop's next tile may start the INT4 list): the
+    // expanded or INT8 K record of the same size from a selected resource, branching only for the
+    // packed INT4 form of a reference-shaped call
+    auto issue = [&](int i, uint8_t* kd, uint8_t* vd, int32_t* vkd) __attribute__((always_inline)) {
+      const bool is8 = i < n8;
+      const int col = is8 ? lo8 + i : lo4 + (i - n8);
+      if (is8 || k4x) lds_copy_buf<K8_BYTES>(is8 ? rk8 : rk4x, col * K8_BYTES, kd, kh8);
+      else lds_copy_buf<K4_BYTES>(rk4, col * K4_BYTES, kd, kh4);
+      lds_copy_buf<V8_BYTES>(rv8, col * V8_BYTES, vd, vh8);
+      issue_small(col, vkd);
     };
     // tile i of kind KIND: wait for its records (and for every wave to finish
     // tile i-1, whose buffers receive tile i+1), start tile i+1's loads, compute
-    auto step = [&](auto kind, auto mask, int i, const uint8_t* kc, const uint8_t* vc, const float* sc,
-                    const int32_t* vsc, uint8_t* kn, uint8_t* vn, float* sn,
-                    int32_t* vsn) __attribute__((always_inline)) {
+    auto step = [&](auto kind, auto mask, int i, const uint8_t* kc, const uint8_t* vc, const int32_t* vkc,
+                    uint8_t* kn, uint8_t* vn, int32_t* vkn) __attribute__((always_inline)) {
       lds_wait();
       constexpr int KIND = decltype(kind)::value;
       if (i + 1 < total) {
         // an INT4 tile is followed by one of its own kind, an INT8 tile by INT8 up to the list's end
-        if constexpr (KIND == KI8) issue(i + 1, kn, vn, sn, vsn);
-        else issue_as(kind, i + 1, kn, vn, sn, vsn);
+        if constexpr (KIND == KI8) issue(i + 1, kn, vn, vkn);
+        else issue_as(kind, i + 1, kn, vn, vkn);
       }
       const int col = tile_col(i);
-      const float4 k4v = *reinterpret_cast<const float4*>(sc);
+      const float4 k4v = *reinterpret_cast<const float4*>(vkc + VK + (KIND == KI8 ? 0 : 4));
       const float ks[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
       constexpr bool QMASK = decltype(mask)::value != 0;
-      if constexpr (KIND == KI8) prefill_tile<KI8, SUMS>(a, st, qf, qs8, ks, col, false, qrow, kc, vc, nullptr, vsc);
-      else prefill_tile<KIND, SUMS, QMASK>(a, st, q4f, qs4, ks, col, QMASK, qrow, kc, vc, nullptr, vsc);
+      if constexpr (KIND == KI8) prefill_tile<KI8, SUMS>(a, st, qf, qs8, ks, col, false, qrow, kc, vc, nullptr, vkc);
+      else prefill_tile<KIND, SUMS, QMASK>(a, st, q4f, qs4, ks, col, QMASK, qrow, kc, vc, nullptr, vkc);
     };
     // Tiles [i, end) of one kind, the first in buffer set PARITY.  Each kind has a
     // loop of its own: with both kinds in one loop body the compiler copies the
@@ -715,13 +725,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
       uint8_t* k1 = p ? k_lds0 : k_lds1;
       uint8_t* v0 = p ? v_lds1 : v_lds0;
       uint8_t* v1 = p ? v_lds0 : v_lds1;
-      float* s0 = p ? ks_lds1 : ks_lds0;
-      float* s1 = p ? ks_lds0 : ks_lds1;
-      int32_t* w0 = p ? vs_lds1 : vs_lds0;
-      int32_t* w1 = p ? vs_lds0 : vs_lds1;
+      int32_t* w0 = p ? vk_lds1 : vk_lds0;
+      int32_t* w1 = p ? vk_lds0 : vk_lds1;
       for (; i < end; i += 2) {
-        step(kind, Tag<0>{}, i, k0, v0, s0, w0, k1, v1, s1, w1);
-        if (i + 1 < end) step(kind, Tag<0>{}, i + 1, k1, v1, s1, w1, k0, v0, s0, w0);
+        step(kind, Tag<0>{}, i, k0, v0, w0, k1, v1, w1);
+        if (i + 1 < end) step(kind, Tag<0>{}, i + 1, k1, v1, w1, k0, v0, w0);
       }
     };
     // The INT4 list ends at the query tile itself when w8 = 0 (then n8 = 0): that last tile is
@@ -732,12 +740,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     auto last = [&](auto kind) __attribute__((always_inline)) {
       if (!diag4) return;
       if ((total - 1) & 1)
-        step(kind, Tag<1>{}, total - 1, k_lds1, v_lds1, ks_lds1, vs_lds1, k_lds0, v_lds0, ks_lds0, vs_lds0);
+        step(kind, Tag<1>{}, total - 1, k_lds1, v_lds1, vk_lds1, k_lds0, v_lds0, vk_lds0);
       else
-        step(kind, Tag<1>{}, total - 1, k_lds0, v_lds0, ks_lds0, vs_lds0, k_lds1, v_lds1, ks_lds1, vs_lds1);
+        step(kind, Tag<1>{}, total - 1, k_lds0, v_lds0, vk_lds0, k_lds1, v_lds1, vk_lds1);
     };
     __syncthreads();  // every wave is done with the F16 pass's LDS
-    issue(0, k_lds0, v_lds0, ks_lds0, vs_lds0);
+    issue(0, k_lds0, v_lds0, vk_lds0);
     run(Tag<KI8>{}, Tag<0>{}, 0, n8);
     if (k4x) {
       if (n8 & 1) run(Tag<KQ4X>{}, Tag<1>{}, n8, end4);

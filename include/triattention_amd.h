@@ -312,6 +312,15 @@ int tri_decode_occupancy(int* blocks);
 /* Compute units of the current device (used to size decode splits). */
 int tri_device_cus(int* cus);
 
+/* Extension, no counterpart in the reference: the launch form of tri_attention for this process.
+ * mode 0 (default): launches with at most two workgroups per compute unit take four-wave workgroups
+ * whose two wave pairs split each query tile's key tiles (the F16 tiles and the start of the
+ * quantized list, and the rest), merged before the output; larger launches take two-wave
+ * workgroups.  mode 1: always two-wave workgroups; mode 2: always four.  Both forms follow the
+ * reference's per-tile arithmetic; they differ only in the fp32 summation order across the two
+ * parts (tests hold both to the same bar).  Returns 1 for another mode. */
+int tri_prefill_pairs(int mode);
+
 /* Measurement aid, no counterpart in the reference: reads `records` records of 8192 bytes from
  * `base` with no compute (wave i takes a contiguous run of ceil(records / waves) records, `depth`
  * of them in flight, 16-byte loads per lane), the device's streaming-read ceiling against which

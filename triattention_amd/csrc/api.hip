@@ -23,6 +23,8 @@
 namespace {
 
 thread_local std::string g_error;
+// tri_attention's launch form: 0 by launch size, 1 two-wave workgroups, 2 four-wave (split key tiles)
+static std::atomic<int> g_prefill_pairs{0};
 
 int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail(const char* fmt, ...) {
@@ -205,8 +207,23 @@ int tri_attention(const int32_t* order, int n_order, const int32_t* bands, int b
   a.v8s = v8sum;
   a.k4x = static_cast<const uint8_t*>(k4x);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (v8sum) tri::prefill_kernel<true><<<dim3(n_order, batch), 128, 0, s>>>(a);
-  else tri::prefill_kernel<false><<<dim3(n_order, batch), 128, 0, s>>>(a);
+  // Launches of at most two workgroups per CU (short prompts) leave SIMDs without a wave: each
+  // workgroup then takes four waves, two pairs that split its key tiles (prefill_kernel<., 2>).
+  const int pmode = g_prefill_pairs.load();
+  bool pairs = pmode == 2;
+  if (pmode == 0) {
+    int cus = 0;
+    if (device_cus(&cus) != 0) return 1;
+    pairs = (int64_t)n_order * batch <= 2 * (int64_t)cus;
+  }
+  const dim3 grid(n_order, batch);
+  if (pairs) {
+    if (v8sum) tri::prefill_kernel<true, 2><<<grid, 256, 0, s>>>(a);
+    else tri::prefill_kernel<false, 2><<<grid, 256, 0, s>>>(a);
+  } else {
+    if (v8sum) tri::prefill_kernel<true, 1><<<grid, 128, 0, s>>>(a);
+    else tri::prefill_kernel<false, 1><<<grid, 128, 0, s>>>(a);
+  }
   return check_launch("attention");
 }
 
@@ -767,6 +784,13 @@ int tri_device_cus(int* cus) {
   g_error.clear();
   if (!cus) return fail("device_cus: null output");
   return device_cus(cus);
+}
+
+int tri_prefill_pairs(int mode) {
+  g_error.clear();
+  if (mode < 0 || mode > 2) return fail("prefill_pairs: mode must be 0, 1 or 2 (got %d)", mode);
+  g_prefill_pairs.store(mode);
+  return 0;
 }
 
 int tri_stream_read(const void* base, int64_t records, int waves, int waves_per_group, int depth, int32_t* sink,

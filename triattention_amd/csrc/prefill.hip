@@ -6,7 +6,9 @@
 // (scaled_row_max, tile_base_margin, run_task, unified_kernel).
 //
 // Work decomposition: one workgroup of 2 waves per (batch, q-head, 64-row query
-// tile); wave w owns query rows 32w..32w+31.  Scores are computed transposed,
+// tile); wave w owns query rows 32w..32w+31 (launches too small to give every
+// SIMD a wave take 4 waves, two such pairs splitting the key tiles: PAIRS = 2
+// below).  Scores are computed transposed,
 // S^T = K Q^T, with v_mfma_i32_32x32x32_i8, so lane L holds the 32 scores of
 // query L%32 for keys {kb*32 + 8*(r/4) + 4*(L/32) + r%4}; the same lane then
 // feeds its probabilities as the B operand of O^T = V^T P^T.  Row statistics
@@ -524,18 +526,25 @@ struct Tag {
   static constexpr int value = V;
 };
 
-// SUMS: a.v8s is given (the P V accumulators of quantized tiles start from it)
-template <bool SUMS>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillArgs a) {
-  // LDS: two K buffers (8 KiB) and two V buffers (8 KiB), distinct objects so
-  // that the compiler can tell a read of one buffer from a load into the other;
-  // an fp16 V record uses both V buffers
-  __shared__ __align__(16) uint8_t k_lds0[K8_BYTES], k_lds1[K8_BYTES];
-  __shared__ __align__(16) uint8_t v_lds0[V8_BYTES], v_lds1[V8_BYTES];
+// SUMS: a.v8s is given (the P V accumulators of quantized tiles start from it).
+// PAIRS = 2 (launches with too few workgroups to give every SIMD a wave): four
+// waves per workgroup, two pairs over the same 64 query rows; pair 0 takes the
+// F16 tiles and the first part of the quantized tile list, pair 1 the rest,
+// each with LDS buffers of its own, and pair 0 merges pair 1's running state
+// (max, denominator, accumulators) through LDS before the epilogue.  Every wave
+// passes the same number of barriers (the pair with fewer tiles waits out the
+// difference), as a workgroup barrier counts the arrivals of all four.
+template <bool SUMS, int PAIRS>
+__global__ __launch_bounds__(128 * PAIRS) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillArgs a) {
+  // LDS: two K buffers (8 KiB) and two V buffers (8 KiB) per pair, distinct
+  // objects so that the compiler can tell a read of one buffer from a load into
+  // the other; an fp16 V record uses both V buffers
+  __shared__ __align__(16) uint8_t k_lds0[PAIRS][K8_BYTES], k_lds1[PAIRS][K8_BYTES];
+  __shared__ __align__(16) uint8_t v_lds0[PAIRS][V8_BYTES], v_lds1[PAIRS][V8_BYTES];
   // the tile's -127 * V8 sums (D words, with SUMS) followed by its 4 K group scales as an INT8 tile
   // and as an INT4 tile, which one copy instruction brings together
   constexpr int VK = SUMS ? D : 0;
-  __shared__ __align__(16) int32_t vk_lds0[VK + 8], vk_lds1[VK + 8];
+  __shared__ __align__(16) int32_t vk_lds0[PAIRS][VK + 8], vk_lds1[PAIRS][VK + 8];
   __shared__ __align__(16) float vms_lds[2 * D];  // the KV head's V mean and scale, for the epilogue
   const int rows = (a.t + BN - 1) / BN;
   // Launch sequence: BandTable's order is KV-head-major (prefill.py:24-25), so the workgroups running at
@@ -560,11 +569,15 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   const int task = __builtin_amdgcn_readfirstlane(a.order[j]), b = blockIdx.y;
   const int qh = task / rows, qb = task % rows, g = a.hq / a.hk, kh = qh / g;
+  const int pair = PAIRS == 2 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 7)) : 0;
   if (a.exact != nullptr && a.exact[qh] > 0) {
-    prefill_exact(a, b, qh, qb, k_lds0, k_lds1, v_lds0, v_lds1);
+    // (pair 0 alone; pair 1 passes the exact path's two barriers per key tile)
+    if (pair == 0) prefill_exact(a, b, qh, qb, k_lds0[0], k_lds1[0], v_lds0[0], v_lds1[0]);
+    else
+      for (int k = 0; k < 2 * (qb + 1); ++k) __syncthreads();
     return;
   }
-  const int tid = threadIdx.x, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
+  const int tid = threadIdx.x & 127, wave = tid >> 6, L = tid & 63, lq = L & 31, half = L >> 5;
   const int qrow = qb * BN + wave * 32 + lq;
   const bool row_ok = qrow < a.t;
   const int tiles = rows;
@@ -593,27 +606,35 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
   const float* ka8 = a.ka + rec0 * 4;
   const float* ka4p = a.ka4 ? a.ka4 + rec0 * 4 : nullptr;
 
-  // ---- F16 pass: tile 0, then the diagonal tile when qb > 0 (synchronous staging)
+  // ---- F16 pass: tile 0, then the diagonal tile when qb > 0 (synchronous staging; pair 0)
   const int nf16 = qb > 0 ? 2 : 1;
-  for (int i = 0; i < nf16; ++i) {
+  // this pair's part [q0, q1) of the quantized tile list (INT8 tiles, then INT4 ones): with two pairs,
+  // pair 0's F16 tiles (each priced as two quantized ones: their copies are synchronous) and quantized
+  // tiles balance pair 1's (C0 attention: 25.3 us with the F16 tiles priced as one, 23.6 as two, 24.9
+  // as three)
+  const int total = n8 + n4;
+  const int c = PAIRS == 2 ? max(0, (total - 2 * nf16 + 1) / 2) : total;
+  const int q0 = pair == 0 ? 0 : c, q1 = pair == 0 ? c : total;
+  // barriers each pair passes: two per F16 tile, one before its quantized part and one per tile of it
+  const int bar0 = 2 * nf16 + (c > 0 ? 1 + c : 0), bar1 = total > c ? 1 + total - c : 0;
+  for (int i = 0; i < (pair == 0 ? nf16 : 0); ++i) {
     const int col = i == 0 ? 0 : qb;
     __syncthreads();
     // (with the first copy: the epilogue's V mean and scale, 1 KiB, so that it reads them from LDS)
     if (i == 0 && tid < 64)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.vstat + ((int64_t)b * a.hk + kh) * 3 * D + tid * 4),
                                        (__attribute__((address_space(3))) void*)(vms_lds + tid * 4), 16, 0, 0);
-    lds_copy_async<K8_BYTES>(a.k8 + (rec0 + col) * K8_BYTES, k_lds0);
-    lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES, v_lds0);
-    lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES + V16_BYTES / 2, v_lds1);
+    lds_copy_async<K8_BYTES>(a.k8 + (rec0 + col) * K8_BYTES, k_lds0[0]);
+    lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES, v_lds0[0]);
+    lds_copy_async<V16_BYTES / 2>(a.v16 + (rec0 + col) * V16_BYTES + V16_BYTES / 2, v_lds1[0]);
     lds_wait();
     const float ks[4] = {ka8[col * 4], ka8[col * 4 + 1], ka8[col * 4 + 2], ka8[col * 4 + 3]};
-    prefill_tile<KF16>(a, st, qf, qs8, ks, col, i == nf16 - 1 && col == qb, qrow, k_lds0, v_lds0, v_lds1);
+    prefill_tile<KF16>(a, st, qf, qs8, ks, col, i == nf16 - 1 && col == qb, qrow, k_lds0[0], v_lds0[0], v_lds1[0]);
   }
 
   // ---- INT8 then INT4 passes as one pipelined tile list: the next tile's
   // records stream into the other LDS buffer while the current one is used
-  const int total = n8 + n4;
-  if (total > 0) {
+  if (q0 < q1) {
     v4i q4f[4];
     float qs4 = 1.17549435e-38f;
     if (n4 > 0) {
@@ -704,7 +725,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
                     uint8_t* kn, uint8_t* vn, int32_t* vkn) __attribute__((always_inline)) {
       lds_wait();
       constexpr int KIND = decltype(kind)::value;
-      if (i + 1 < total) {
+      if (i + 1 < q1) {
         // an INT4 tile is followed by one of its own kind, an INT8 tile by INT8 up to the list's end
         if constexpr (KIND == KI8) issue(i + 1, kn, vn, vkn);
         else issue_as(kind, i + 1, kn, vn, vkn);
@@ -721,12 +742,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     // accumulators between register sets at every tile (~30 VALU per tile).
     auto run = [&](auto kind, auto parity, int i, int end) __attribute__((always_inline)) {
       constexpr bool p = decltype(parity)::value != 0;
-      uint8_t* k0 = p ? k_lds1 : k_lds0;
-      uint8_t* k1 = p ? k_lds0 : k_lds1;
-      uint8_t* v0 = p ? v_lds1 : v_lds0;
-      uint8_t* v1 = p ? v_lds0 : v_lds1;
-      int32_t* w0 = p ? vk_lds1 : vk_lds0;
-      int32_t* w1 = p ? vk_lds0 : vk_lds1;
+      uint8_t* k0 = p ? k_lds1[pair] : k_lds0[pair];
+      uint8_t* k1 = p ? k_lds0[pair] : k_lds1[pair];
+      uint8_t* v0 = p ? v_lds1[pair] : v_lds0[pair];
+      uint8_t* v1 = p ? v_lds0[pair] : v_lds1[pair];
+      int32_t* w0 = p ? vk_lds1[pair] : vk_lds0[pair];
+      int32_t* w1 = p ? vk_lds0[pair] : vk_lds1[pair];
       for (; i < end; i += 2) {
         step(kind, Tag<0>{}, i, k0, v0, w0, k1, v1, w1);
         if (i + 1 < end) step(kind, Tag<0>{}, i + 1, k1, v1, w1, k0, v0, w0);
@@ -735,27 +756,69 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void p
     // The INT4 list ends at the query tile itself when w8 = 0 (then n8 = 0): that last tile is
     // masked like the reference masks the last entry of a pass when it is the query tile
     // (prefill_sm80.cu:328-329), in a step of its own outside the loop.
-    const bool diag4 = w8 <= 0 && n4 > 0;
-    const int end4 = total - (diag4 ? 1 : 0);
+    // (the list's last tile, which the last part holds)
+    const bool diag4 = w8 <= 0 && n4 > 0 && q1 == total;
+    const int s4 = max(n8, q0), end4 = q1 - (diag4 ? 1 : 0);
     auto last = [&](auto kind) __attribute__((always_inline)) {
       if (!diag4) return;
-      if ((total - 1) & 1)
-        step(kind, Tag<1>{}, total - 1, k_lds1, v_lds1, vk_lds1, k_lds0, v_lds0, vk_lds0);
+      if ((total - 1 - q0) & 1)
+        step(kind, Tag<1>{}, total - 1, k_lds1[pair], v_lds1[pair], vk_lds1[pair], k_lds0[pair], v_lds0[pair],
+             vk_lds0[pair]);
       else
-        step(kind, Tag<1>{}, total - 1, k_lds0, v_lds0, vk_lds0, k_lds1, v_lds1, vk_lds1);
+        step(kind, Tag<1>{}, total - 1, k_lds0[pair], v_lds0[pair], vk_lds0[pair], k_lds1[pair], v_lds1[pair],
+             vk_lds1[pair]);
     };
     __syncthreads();  // every wave is done with the F16 pass's LDS
-    issue(0, k_lds0, v_lds0, vk_lds0);
-    run(Tag<KI8>{}, Tag<0>{}, 0, n8);
+    issue(q0, k_lds0[pair], v_lds0[pair], vk_lds0[pair]);
+    run(Tag<KI8>{}, Tag<0>{}, q0, min(n8, q1));
     if (k4x) {
-      if (n8 & 1) run(Tag<KQ4X>{}, Tag<1>{}, n8, end4);
-      else run(Tag<KQ4X>{}, Tag<0>{}, n8, end4);
+      if ((s4 - q0) & 1) run(Tag<KQ4X>{}, Tag<1>{}, s4, end4);
+      else run(Tag<KQ4X>{}, Tag<0>{}, s4, end4);
       last(Tag<KQ4X>{});
     } else {
-      if (n8 & 1) run(Tag<KQ4>{}, Tag<1>{}, n8, end4);
-      else run(Tag<KQ4>{}, Tag<0>{}, n8, end4);
+      if ((s4 - q0) & 1) run(Tag<KQ4>{}, Tag<1>{}, s4, end4);
+      else run(Tag<KQ4>{}, Tag<0>{}, s4, end4);
       last(Tag<KQ4>{});
     }
+  }
+
+  if constexpr (PAIRS == 2) {
+    // the pair with fewer barriers waits out the difference
+    for (int k = pair == 0 ? bar0 : bar1; k < max(bar0, bar1); ++k) __syncthreads();
+    // (each pair's last barrier came before its last tile: wait until every wave is done with its buffers)
+    __syncthreads();
+    // pair 1's running state through LDS (over the K and V buffers, which every wave is done with):
+    // wave w's accumulators in one 16 KiB object, element-major, lane-minor; the maxima and
+    // denominators after them in another
+    float* xs = reinterpret_cast<float*>(wave == 0 ? &k_lds0[0][0] : &k_lds1[0][0]);
+    float* ms = reinterpret_cast<float*>(&v_lds0[0][0]) + wave * 128;
+    if (pair == 1) {
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<float4*>(xs + ((cb * 4 + r4) * 64 + L) * 4) =
+              make_float4(st.acc[cb][r4 * 4], st.acc[cb][r4 * 4 + 1], st.acc[cb][r4 * 4 + 2], st.acc[cb][r4 * 4 + 3]);
+      ms[L] = st.m;
+      ms[64 + L] = st.den;
+    }
+    __syncthreads();
+    if (pair == 1) return;
+    // pair 0: the two running states on the common maximum (acc and den alike)
+    const float m1 = ms[L], den1 = ms[64 + L];
+    const float mn = fmaxf(st.m, m1);
+    const float f0 = texp2(st.m - mn), f1 = texp2(m1 - mn);
+    st.den = __builtin_fmaf(den1, f1, st.den * f0);
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const float4 x = *reinterpret_cast<const float4*>(xs + ((cb * 4 + r4) * 64 + L) * 4);
+        const float xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st.acc[cb][r4 * 4 + i] = __builtin_fmaf(xv[i], f1, st.acc[cb][r4 * 4 + i] * f0);
+      }
+    st.m = mn;
   }
 
   // ---- epilogue: out = fma(acc / den, scale, mean) (prefill_sm80.cu:466-487)

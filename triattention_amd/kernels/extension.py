@@ -40,7 +40,7 @@ EXPORTS = ("tri_last_error", "tri_prepare_qk", "tri_pack_v", "tri_attention", "t
            "tri_decode_partials", "tri_decode_merge", "tri_decode_short_tail", "tri_decode_merge_short_tail",
            "tri_decode_partials_timed", "tri_decode_noalloc",
            "tri_decode_tasks", "tri_cache_store", "tri_tail_spill", "tri_decode_occupancy", "tri_device_cus",
-           "tri_stream_read", "tri_issue_probe")
+           "tri_stream_read", "tri_issue_probe", "tri_prefill_pairs")
 KX_BYTES = 16384
 TASK_WORDS = 512  # int32 words of the decode task table per (sequence, KV head, split)
 
@@ -84,6 +84,7 @@ def load_library() -> ctypes.CDLL:
     lib.tri_device_cus.argtypes = [ctypes.POINTER(ctypes.c_int)]
     lib.tri_stream_read.argtypes = [P, I64, I, I, I, P, P]
     lib.tri_issue_probe.argtypes = [I, I, I, P, P]
+    lib.tri_prefill_pairs.argtypes = [I]
     for name in EXPORTS:
         if name != "tri_last_error":
             getattr(lib, name).restype = ctypes.c_int
@@ -489,6 +490,11 @@ class Module:
         n = ctypes.c_int(0)
         self._call(self.lib.tri_device_cus, ctypes.byref(n))
         return int(n.value)
+
+    def prefill_pairs(self, mode: int) -> None:
+        """tri_prefill_pairs: attention's launch form for this process (0 by launch size, 1 two-wave
+        workgroups, 2 four-wave workgroups whose wave pairs split the key tiles)."""
+        self._call(self.lib.tri_prefill_pairs, int(mode))
 
     def issue_probe(self, mode: int, waves_per_simd: int, iters: int):
         """tri_issue_probe: per wave (shader-clock cycles, 100 MHz ticks), int64 [waves, 2] on the CPU."""

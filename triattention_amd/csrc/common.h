@@ -39,6 +39,11 @@ constexpr int V16_WORDS = V16_BYTES / 4, V8_WORDS = V8_BYTES / 4, V4_WORDS = V4_
 constexpr float MAGIC = 12582912.0f;      // 1.5 * 2^23
 constexpr uint32_t MAGIC_BITS = 0x4B400000u;
 constexpr float PMAGIC_HALF = 49152.5f;    // P quantizer: byte 1 of fma(e, 255, 49152.5)
+// Cache policy of loads that stream data read once (the decode kernels' K/V records): the
+// non-temporal bit (gfx950 buffer loads, "nt"), so the stream does not displace what other loads
+// reuse from the caches.  Prefill's record copies keep the default: the q-heads of a GQA group
+// read the same records through L2.
+constexpr int LOAD_STREAM = 2;
 constexpr int MAX_TILES = 2048;            // 131072 tokens (prefill_sm80.cu:23)
 constexpr int MAX_GROUP = 8;               // GQA group bound of the decode kernel
 constexpr int NEAR_V8 = 16;                // decode V recency window (decode.py:9)

@@ -9,7 +9,7 @@ namespace tri {
 constexpr int PROBE_RECORD = 8192;  // bytes per record (a K8 / V8 record)
 
 // Wave i reads records [i * per, (i + 1) * per) in order, DEPTH records in flight: eight 16-byte
-// loads per lane per record, through a descriptor per record (loads past the array read zeros
+// non-temporal loads per lane per record (the decode kernel's cache policy), through a descriptor per record (loads past the array read zeros
 // without touching memory).  The XOR of everything read goes to sink[0] only if it equals a value
 // no real input produces, so the loads cannot be dropped and nothing is written in practice.
 template <int DEPTH>
@@ -25,7 +25,7 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t* base, i
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(base + (ok ? r : 0) * PROBE_RECORD), (short)0, ok ? PROBE_RECORD : 0, 0x00020000);
 #pragma unroll
-    for (int f = 0; f < 8; ++f) buf[d][f] = __builtin_amdgcn_raw_buffer_load_b128(rs, L * 16 + f * 1024, 0, 0);
+    for (int f = 0; f < 8; ++f) buf[d][f] = __builtin_amdgcn_raw_buffer_load_b128(rs, L * 16 + f * 1024, 0, LOAD_STREAM);
   };
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, r0 + d);

@@ -359,6 +359,8 @@ def c3_decode(module, dev, stream, args, S, DecodeCache, Prefill, from_bands):
     for rep in range(2):
         cache = DecodeCache(module, max_tail=256)
         cache.ragged = True
+        if args.c3_per:
+            cache.per = args.c3_per  # (measurement aid: runs of this many tiles instead of the default)
         pre = Prefill(module, from_bands({str(layer): bands.tolist() for layer in range(C3_GRAPH_LAYERS)}), cache)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -714,6 +716,7 @@ def main():
                     help="decode merge launch: the one-wave kernel while the tail holds at most 64 tokens "
                          "(auto), or always tri_decode's merge, which makes the same choice on the device")
     ap.add_argument("--no-c3", action="store_true")
+    ap.add_argument("--c3-per", type=int, default=0, help="C3 cache split runs of this many tiles (measurement aid)")
     ap.add_argument("--layers", type=int, default=28, help="C1 layers (own caches, one decode op each per token)")
     ap.add_argument("--c2-kinds", default="", help="with --only c2: also time the C2 inputs with every KV head of "
                                                    "each listed kind (i8, i4, bf16; comma-separated)")
